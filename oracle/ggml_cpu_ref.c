@@ -1,0 +1,646 @@
+/*
+ * ORACLE - test infrastructure only (see ggml_cpu_ref.h).
+ *
+ * Restatement of ggml's portable CPU path for MUL_MAT_ID on Q8_0 / Q4_K /
+ * Q6_K / IQ3_S expert weights.  ggml (llama.cpp @ 96ffdc41) is a third-party
+ * dependency that the reference does not vendor; the algorithm followed here
+ * is its published generic C form:
+ *   quantize_row_q8_0_ref, quantize_row_q8_K_ref        (activation quantisers)
+ *   dequantize_row_{q8_0,q4_K,q6_K,iq3_s}                (format readers)
+ *   ggml_vec_dot_{q8_0_q8_0,q4_K_q8_K,q6_K_q8_K,iq3_s_q8_K}_generic
+ *   ggml_compute_forward_mul_mat_id                      (slot i reads row i % ne11)
+ * anchored on the reference's own readers of the same formats
+ * (sabah_rt.cu:2233-2423; gguf-py quants.py:412-435, 509-556, 586-606,
+ * 1091-1159) and its description of the activation step (tools/rc4/opcheck.py:65-83).
+ *
+ * Build with -ffp-contract=off: every float operation below is meant to round
+ * on its own, as in the C source it restates.
+ */
+#include "ggml_cpu_ref.h"
+#include "iq3s_grid_u32.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+int orc_block_elems(int qt) {
+    switch (qt) {
+    case ORC_Q8_0: return 32;
+    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: return 256;
+    }
+    return 0;
+}
+
+int orc_block_bytes(int qt) {
+    switch (qt) {
+    case ORC_Q8_0: return 34;    /* fp16 d + 32 x int8                       */
+    case ORC_Q4_K: return 144;   /* d, dmin, 12 B scales/mins, 128 B nibbles */
+    case ORC_Q6_K: return 210;   /* ql[128], qh[64], int8 sc[16], fp16 d      */
+    case ORC_Q8_K: return 292;   /* float d, int8 qs[256], int16 bsums[16]    */
+    case ORC_IQ3_S: return 110;  /* d, qs[64], qh[8], signs[32], scales[4]    */
+    }
+    return 0;
+}
+
+size_t orc_row_bytes(int qt, int n) {
+    const int be = orc_block_elems(qt);
+    if (be == 0 || n % be) return 0;
+    return (size_t)(n / be) * (size_t)orc_block_bytes(qt);
+}
+
+int orc_vec_dot_type(int qt) {
+    switch (qt) {
+    case ORC_Q8_0: return ORC_Q8_0;
+    case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: return ORC_Q8_K;
+    }
+    return -1;
+}
+
+size_t orc_act_row_bytes(int qt, int k) {
+    const int vt = orc_vec_dot_type(qt);
+    return vt < 0 ? 0 : orc_row_bytes(vt, k);
+}
+
+/* ------------------------------------------------------------------------ */
+/* binary16                                                                  */
+/* ------------------------------------------------------------------------ */
+float orc_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {                       /* subnormal: m * 2^-24 */
+            int sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; ++sh; }
+            bits = sign | ((uint32_t)(113 - sh) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 0x1f) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t orc_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {                         /* inf / nan */
+        return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u | ((ax >> 13) & 0x3ffu) : 0u));
+    }
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   /* >= 65520 rounds to inf */
+    const uint32_t e = ax >> 23;
+    if (e < 113) {                                   /* result is subnormal or zero */
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t s = 126 - e;                  /* value / 2^-24 = m >> s     */
+        if (e == 0 || s > 24) return sign;           /* < half a unit: rounds to 0 */
+        uint32_t q = m >> s;
+        const uint32_t rem = m & ((1u << s) - 1u), half = 1u << (s - 1);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((e - 112) << 10) | ((ax >> 13) & 0x3ffu);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;     /* may carry into exponent */
+    return (uint16_t)(sign | h);
+}
+
+static inline float ld_f16(const uint8_t *p) { return orc_fp16_to_fp32((uint16_t)(p[0] | (p[1] << 8))); }
+static inline void st_f16(uint8_t *p, float f) { const uint16_t h = orc_fp32_to_fp16(f); p[0] = (uint8_t)h; p[1] = (uint8_t)(h >> 8); }
+
+/* ------------------------------------------------------------------------ */
+/* activation quantisers                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_row_q8_0_ref: d = amax/127 (stored fp16), q = roundf(x * (1/d)),
+ * halves away from zero (quants.py:412-427 restates the same steps and calls
+ * them bit-exact with ggml-quants.c). */
+void orc_quantize_q8_0(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 32; ++b, x += 32, y += 34) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = fabsf(x[j]);
+            amax = amax > v ? amax : v;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        st_f16(y, d);
+        for (int j = 0; j < 32; ++j) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+    }
+}
+
+/* quantize_row_q8_K_ref: the signed value of largest magnitude (first one on
+ * ties) sets iscale = -127/max; q = min(127, nearest-even(iscale*x)); d = 1/iscale
+ * kept in fp32; bsums[j] = sum of q over elements 16j..16j+15.  opcheck.py:73-80
+ * restates the same q and d. */
+void orc_quantize_q8_K(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 256; ++b, x += 256, y += 292) {
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < 256; ++j) {
+            const float ax = fabsf(x[j]);
+            if (ax > amax) { amax = ax; max = x[j]; }
+        }
+        int8_t *qs = (int8_t *)(y + 4);
+        int16_t bs[16];
+        if (amax == 0.0f) {
+            memset(y, 0, 292);
+            continue;
+        }
+        const float iscale = -127.0f / max;
+        for (int j = 0; j < 256; ++j) {
+            const int v = (int)rintf(iscale * x[j]);
+            qs[j] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int j = 0; j < 16; ++j) {
+            int s = 0;
+            for (int i = 0; i < 16; ++i) s += qs[16 * j + i];
+            bs[j] = (int16_t)s;
+        }
+        memcpy(y + 260, bs, sizeof(bs));
+        const float d = 1.0f / iscale;
+        memcpy(y, &d, 4);
+    }
+}
+
+int orc_quantize_act(int qt, const float *x, uint8_t *y, int k) {
+    const int vt = orc_vec_dot_type(qt);
+    if (vt < 0 || k % orc_block_elems(vt)) return -1;
+    if (vt == ORC_Q8_0) orc_quantize_q8_0(x, y, k);
+    else orc_quantize_q8_K(x, y, k);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* decoders (dequantize_row_*)                                               */
+/* ------------------------------------------------------------------------ */
+
+/* get_scale_min_k4: sub-block j's 6-bit scale and min from the 12 packed bytes
+ * (sabah_rt.cu:2210-2218 host form, quants.py:513-536 unpacking diagram). */
+static inline void scale_min_k4(int j, const uint8_t *q, int *sc, int *mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+int orc_dequantize_row(int qt, const uint8_t *x, float *y, int k) {
+    if (orc_row_bytes(qt, k) == 0) return -1;
+    switch (qt) {
+    case ORC_Q8_0:
+        for (int b = 0; b < k / 32; ++b, x += 34) {
+            const float d = ld_f16(x);
+            for (int j = 0; j < 32; ++j) *y++ = (float)(int8_t)x[2 + j] * d;
+        }
+        return 0;
+    case ORC_Q4_K:
+        for (int b = 0; b < k / 256; ++b, x += 144) {
+            const float d = ld_f16(x), dmin = ld_f16(x + 2);
+            const uint8_t *sc = x + 4, *q = x + 16;
+            for (int c = 0; c < 4; ++c, q += 32) {
+                int s0, m0, s1, m1;
+                scale_min_k4(2 * c, sc, &s0, &m0);
+                scale_min_k4(2 * c + 1, sc, &s1, &m1);
+                const float d1 = d * (float)s0, n1 = dmin * (float)m0;
+                const float d2 = d * (float)s1, n2 = dmin * (float)m1;
+                for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] & 0xF) - n1;
+                for (int l = 0; l < 32; ++l) *y++ = d2 * (float)(q[l] >> 4) - n2;
+            }
+        }
+        return 0;
+    case ORC_Q6_K:
+        for (int b = 0; b < k / 256; ++b, x += 210) {
+            const uint8_t *ql = x, *qh = x + 128;
+            const int8_t *sc = (const int8_t *)(x + 192);
+            const float d = ld_f16(x + 208);
+            for (int half = 0; half < 2; ++half, y += 128, ql += 64, qh += 32, sc += 8) {
+                for (int l = 0; l < 32; ++l) {
+                    const int is = l / 16;
+                    const int q1 = ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    y[l] = d * (float)sc[is] * (float)q1;
+                    y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                    y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                    y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                }
+            }
+        }
+        return 0;
+    case ORC_IQ3_S:
+        for (int b = 0; b < k / 256; ++b, x += 110) {
+            const float d = ld_f16(x);
+            const uint8_t *qs = x + 2, *qh = x + 66, *signs = x + 74, *scales = x + 106;
+            for (int ib = 0; ib < 8; ++ib) {
+                const float db = d * (float)(1 + 2 * ((scales[ib / 2] >> (4 * (ib & 1))) & 0xF));
+                for (int g = 0; g < 8; ++g) {
+                    const uint32_t gi = (uint32_t)qs[8 * ib + g] | (((uint32_t)(qh[ib] >> g) & 1u) << 8);
+                    const uint32_t grid = orc_iq3s_grid[gi];
+                    const uint8_t sg = signs[4 * ib + g / 2];
+                    for (int j = 0; j < 4; ++j) {
+                        const int bit = (g & 1) * 4 + j;
+                        *y++ = db * (float)((grid >> (8 * j)) & 0xFF) * ((sg >> bit) & 1 ? -1.0f : 1.0f);
+                    }
+                }
+            }
+        }
+        return 0;
+    }
+    return -1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* block dots                                                                */
+/* ------------------------------------------------------------------------ */
+
+/* ggml_vec_dot_q8_0_q8_0: exact int32 per 32-block, sumf += sumi*(dw*dx). */
+static float dot_q8_0(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 32; ++b, w += 34, a += 34) {
+        int sumi = 0;
+        for (int j = 0; j < 32; ++j) sumi += (int)(int8_t)w[2 + j] * (int)(int8_t)a[2 + j];
+        sumf += (float)sumi * (ld_f16(w) * ld_f16(a));
+    }
+    return sumf;
+}
+
+static inline float q8K_d(const uint8_t *a) { float d; memcpy(&d, a, 4); return d; }
+static inline const int8_t *q8K_qs(const uint8_t *a) { return (const int8_t *)(a + 4); }
+static inline int q8K_bsum(const uint8_t *a, int j) { int16_t v; memcpy(&v, a + 260 + 2 * j, 2); return v; }
+
+/* ggml_vec_dot_q4_K_q8_K (generic): eight int32 lanes of scale*sum(q4*q8),
+ * one fp32 lane sum per lane; the min term sum(bsums*mins) is subtracted per
+ * super-block with dmin*d8; lanes are added last. */
+static float dot_q4_K(const uint8_t *w, const uint8_t *a, int k) {
+    float sums[8] = {0};
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 256; ++b, w += 144, a += 292) {
+        int8_t v[256];
+        const uint8_t *q = w + 16;
+        for (int c = 0; c < 4; ++c, q += 32)
+            for (int l = 0; l < 32; ++l) { v[64 * c + l] = (int8_t)(q[l] & 0xF); v[64 * c + 32 + l] = (int8_t)(q[l] >> 4); }
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) scale_min_k4(j, w + 4, &sc[j], &mn[j]);
+        int msum = 0;
+        for (int j = 0; j < 16; ++j) msum += q8K_bsum(a, j) * mn[j / 2];
+        const int8_t *q8 = q8K_qs(a);
+        int aux[8] = {0};
+        for (int j = 0; j < 8; ++j)
+            for (int m = 0; m < 4; ++m)
+                for (int l = 0; l < 8; ++l) {
+                    const int e = 32 * j + 8 * m + l;
+                    aux[l] += sc[j] * ((int)q8[e] * (int)v[e]);
+                }
+        const float d = ld_f16(w) * q8K_d(a);
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux[l];
+        const float dmin = ld_f16(w + 2) * q8K_d(a);
+        sumf -= dmin * (float)msum;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+/* ggml_vec_dot_q6_K_q8_K (generic): signed 6-bit values (q-32), eight int32
+ * lanes of scale16*sum(q6*q8), fp32 lane sums, lanes added last. */
+static float dot_q6_K(const uint8_t *w, const uint8_t *a, int k) {
+    float sums[8] = {0};
+    for (int b = 0; b < k / 256; ++b, w += 210, a += 292) {
+        int8_t v[256];
+        const uint8_t *ql = w, *qh = w + 128;
+        for (int half = 0; half < 2; ++half, ql += 64, qh += 32)
+            for (int l = 0; l < 32; ++l) {
+                v[128 * half + l] = (int8_t)(((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
+                v[128 * half + 32 + l] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+                v[128 * half + 64 + l] = (int8_t)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+                v[128 * half + 96 + l] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+            }
+        const int8_t *sc = (const int8_t *)(w + 192);
+        const int8_t *q8 = q8K_qs(a);
+        int aux[8] = {0};
+        for (int j = 0; j < 16; ++j)
+            for (int m = 0; m < 2; ++m)
+                for (int l = 0; l < 8; ++l) {
+                    const int e = 16 * j + 8 * m + l;
+                    aux[l] += (int)sc[j] * ((int)q8[e] * (int)v[e]);
+                }
+        const float d = ld_f16(w + 208) * q8K_d(a);
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux[l];
+    }
+    float sumf = 0.0f;
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+/* ggml_vec_dot_iq3_s_q8_K (generic): per super-block the exact int32
+ * bsum = sum_ib32 (2*scale+1) * sum(grid*sign*q8); sumf += (dw*d8) * bsum. */
+static float dot_iq3_s(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 256; ++b, w += 110, a += 292) {
+        const uint8_t *qs = w + 2, *qh = w + 66, *signs = w + 74, *scales = w + 106;
+        const int8_t *q8 = q8K_qs(a);
+        int bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int ls = 2 * ((scales[ib / 2] >> (4 * (ib & 1))) & 0xF) + 1;
+            int sumi = 0;
+            for (int g = 0; g < 8; ++g) {
+                const uint32_t gi = (uint32_t)qs[8 * ib + g] | (((uint32_t)(qh[ib] >> g) & 1u) << 8);
+                const uint32_t grid = orc_iq3s_grid[gi];
+                const uint8_t sg = signs[4 * ib + g / 2];
+                for (int j = 0; j < 4; ++j) {
+                    const int mag = (int)((grid >> (8 * j)) & 0xFF);
+                    const int s = (sg >> ((g & 1) * 4 + j)) & 1 ? -1 : 1;
+                    sumi += mag * (int)q8[32 * ib + 4 * g + j] * s;
+                }
+            }
+            bsum += sumi * ls;
+        }
+        const float d = ld_f16(w) * q8K_d(a);
+        sumf += d * (float)bsum;
+    }
+    return sumf;
+}
+
+float orc_vec_dot(int qt, const uint8_t *w, const uint8_t *a, int k) {
+    switch (qt) {
+    case ORC_Q8_0: return dot_q8_0(w, a, k);
+    case ORC_Q4_K: return dot_q4_K(w, a, k);
+    case ORC_Q6_K: return dot_q6_K(w, a, k);
+    case ORC_IQ3_S: return dot_iq3_s(w, a, k);
+    }
+    return NAN;
+}
+
+/* ------------------------------------------------------------------------ */
+/* weight encoders (synthetic data)                                           */
+/* ------------------------------------------------------------------------ */
+static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
+
+/* nearest codebook entry for every 4-tuple of 3-bit levels (squared level distance,
+ * lowest index on ties) */
+static uint16_t g_iq3s_nearest[4096];
+static int g_iq3s_nearest_ready = 0;
+
+static void iq3s_nearest_init(void) {
+    if (g_iq3s_nearest_ready) return;
+    for (int key = 0; key < 4096; ++key) {
+        int best = 0, bestd = 1 << 30;
+        for (int e = 0; e < 512; ++e) {
+            int dist = 0;
+            for (int j = 0; j < 4; ++j) {
+                const int lv = (key >> (3 * j)) & 7;
+                const int ge = (int)((orc_iq3s_grid[e] >> (8 * j)) & 0xFF) / 2;
+                dist += (lv - ge) * (lv - ge);
+            }
+            if (dist < bestd) { bestd = dist; best = e; }
+        }
+        g_iq3s_nearest[key] = (uint16_t)best;
+    }
+    g_iq3s_nearest_ready = 1;
+}
+
+static void enc_iq3_s(const float *x, uint8_t *y, int k) {
+    iq3s_nearest_init();
+    for (int b = 0; b < k / 256; ++b, x += 256, y += 110) {
+        memset(y, 0, 110);
+        float am[8], A = 0.0f;
+        for (int ib = 0; ib < 8; ++ib) {
+            am[ib] = 0.0f;
+            for (int j = 0; j < 32; ++j) am[ib] = fmaxf(am[ib], fabsf(x[32 * ib + j]));
+            A = fmaxf(A, am[ib]);
+        }
+        if (A == 0.0f) continue;
+        st_f16(y, A / 465.0f);
+        const float df = ld_f16(y);
+        if (df == 0.0f) { memset(y, 0, 110); continue; }
+        uint8_t *qs = y + 2, *qh = y + 66, *signs = y + 74, *scales = y + 106;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int s = clampi((int)lrintf((am[ib] / (15.0f * df) - 1.0f) * 0.5f), 0, 15);
+            const float dl = df * (float)(2 * s + 1);
+            scales[ib / 2] |= (uint8_t)(s << (4 * (ib & 1)));
+            for (int g = 0; g < 8; ++g) {
+                int key = 0;
+                for (int j = 0; j < 4; ++j) {
+                    const float v = x[32 * ib + 4 * g + j];
+                    const int lv = clampi((int)lrintf((fabsf(v) / dl - 1.0f) * 0.5f), 0, 7);
+                    key |= lv << (3 * j);
+                    if (v < 0.0f) signs[4 * ib + g / 2] |= (uint8_t)(1u << ((g & 1) * 4 + j));
+                }
+                const int gi = g_iq3s_nearest[key];
+                qs[8 * ib + g] = (uint8_t)(gi & 0xFF);
+                qh[ib] |= (uint8_t)((gi >> 8) << g);
+            }
+        }
+    }
+}
+
+static void enc_q4_K(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 256; ++b, x += 256, y += 144) {
+        memset(y, 0, 144);
+        float scl[8], mns[8], msc = 0.0f, mmn = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            float lo = 0.0f, hi = 0.0f;
+            for (int l = 0; l < 32; ++l) { lo = fminf(lo, x[32 * j + l]); hi = fmaxf(hi, x[32 * j + l]); }
+            scl[j] = (hi - lo) / 15.0f;
+            mns[j] = -lo;
+            msc = fmaxf(msc, scl[j]);
+            mmn = fmaxf(mmn, mns[j]);
+        }
+        st_f16(y, msc / 63.0f);
+        st_f16(y + 2, mmn / 63.0f);
+        const float df = ld_f16(y), dmf = ld_f16(y + 2);
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) {
+            sc[j] = df > 0.0f ? clampi((int)lrintf(scl[j] / df), 0, 63) : 0;
+            mn[j] = dmf > 0.0f ? clampi((int)lrintf(mns[j] / dmf), 0, 63) : 0;
+        }
+        uint8_t *p = y + 4;
+        for (int j = 0; j < 4; ++j) {
+            p[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+            p[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+            p[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+        }
+        uint8_t q[256];
+        for (int j = 0; j < 8; ++j) {
+            const float step = df * (float)sc[j], off = dmf * (float)mn[j];
+            for (int l = 0; l < 32; ++l)
+                q[32 * j + l] = (uint8_t)(step > 0.0f ? clampi((int)lrintf((x[32 * j + l] + off) / step), 0, 15) : 0);
+        }
+        uint8_t *qs = y + 16;
+        for (int c = 0; c < 4; ++c)
+            for (int l = 0; l < 32; ++l) qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
+    }
+}
+
+static void enc_q6_K(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 256; ++b, x += 256, y += 210) {
+        memset(y, 0, 210);
+        float scl[16], ms = 0.0f;
+        for (int j = 0; j < 16; ++j) {
+            float am = 0.0f;
+            for (int l = 0; l < 16; ++l) am = fmaxf(am, fabsf(x[16 * j + l]));
+            scl[j] = am / 31.0f;
+            ms = fmaxf(ms, scl[j]);
+        }
+        st_f16(y + 208, ms / 127.0f);
+        const float df = ld_f16(y + 208);
+        int8_t *sc = (int8_t *)(y + 192);
+        uint8_t u[256];
+        for (int j = 0; j < 16; ++j) {
+            sc[j] = (int8_t)(df > 0.0f ? clampi((int)lrintf(scl[j] / df), -128, 127) : 0);
+            const float step = df * (float)sc[j];
+            for (int l = 0; l < 16; ++l) {
+                const int q = step != 0.0f ? clampi((int)lrintf(x[16 * j + l] / step), -32, 31) : 0;
+                u[16 * j + l] = (uint8_t)(q + 32);
+            }
+        }
+        uint8_t *ql = y, *qh = y + 128;
+        for (int half = 0; half < 2; ++half)
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q1 = u[128 * half + l], q2 = u[128 * half + 32 + l];
+                const uint8_t q3 = u[128 * half + 64 + l], q4 = u[128 * half + 96 + l];
+                ql[64 * half + l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
+                ql[64 * half + 32 + l] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
+                qh[32 * half + l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+    }
+}
+
+int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k) {
+    if (orc_row_bytes(qt, k) == 0) return -1;
+    switch (qt) {
+    case ORC_Q8_0: orc_quantize_q8_0(x, y, k); return 0;
+    case ORC_Q4_K: enc_q4_K(x, y, k); return 0;
+    case ORC_Q6_K: enc_q6_K(x, y, k); return 0;
+    case ORC_IQ3_S: enc_iq3_s(x, y, k); return 0;
+    }
+    return -1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MUL_MAT_ID                                                                */
+/* ------------------------------------------------------------------------ */
+static int threads_or_default(int n) {
+#ifdef _OPENMP
+    return n > 0 ? n : omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}
+
+int orc_mul_mat_id(const void *source, size_t expert_stride, size_t row_stride,
+                   const float *x, size_t x_id_stride, int x_rows, size_t x_token_stride,
+                   const int32_t *ids, size_t ids_id_stride, size_t ids_token_stride,
+                   int n_ids, int n_tokens,
+                   float *dst, size_t dst_id_stride, size_t dst_token_stride,
+                   int rows, int k, int n_experts, int qt, int n_threads) {
+    if (n_tokens == 0) return 0;
+    const size_t rb = orc_row_bytes(qt, k);
+    const size_t ab = orc_act_row_bytes(qt, k);
+    if (!source || !x || !ids || !dst || rb == 0 || ab == 0 || row_stride < rb || rows <= 0 ||
+        n_ids <= 0 || n_tokens < 0 || n_experts <= 0 || (x_rows != 1 && x_rows != n_ids))
+        return -1;
+    for (int t = 0; t < n_tokens; ++t)
+        for (int i = 0; i < n_ids; ++i) {
+            const int32_t e = *(const int32_t *)((const uint8_t *)ids + (size_t)t * ids_token_stride + (size_t)i * ids_id_stride);
+            if (e < 0 || e >= n_experts) return -1;
+        }
+    /* src1 -> vec_dot_type, once per input row (as ggml converts all of src1 first) */
+    uint8_t *act = (uint8_t *)malloc(ab * (size_t)n_tokens * (size_t)x_rows);
+    if (!act) return -1;
+    const int nt = threads_or_default(n_threads);
+    #pragma omp parallel for num_threads(nt) schedule(static)
+    for (int p = 0; p < n_tokens * x_rows; ++p) {
+        const int t = p / x_rows, r = p % x_rows;
+        const float *xr = (const float *)((const uint8_t *)x + (size_t)t * x_token_stride + (size_t)r * x_id_stride);
+        orc_quantize_act(qt, xr, act + (size_t)p * ab, k);
+    }
+    const long total = (long)n_tokens * n_ids * rows;
+    #pragma omp parallel for num_threads(nt) schedule(static)
+    for (long q = 0; q < total; ++q) {
+        const int r = (int)(q % rows);
+        const int i = (int)((q / rows) % n_ids);
+        const int t = (int)(q / ((long)rows * n_ids));
+        const int32_t e = *(const int32_t *)((const uint8_t *)ids + (size_t)t * ids_token_stride + (size_t)i * ids_id_stride);
+        const uint8_t *w = (const uint8_t *)source + (size_t)e * expert_stride + (size_t)r * row_stride;
+        const uint8_t *a = act + ((size_t)t * x_rows + (size_t)(i % x_rows)) * ab;
+        float *o = (float *)((uint8_t *)dst + (size_t)t * dst_token_stride + (size_t)i * dst_id_stride) + r;
+        *o = orc_vec_dot(qt, w, a, k);
+    }
+    free(act);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* one MoE layer (gated FFN of the routed experts + optional shared expert)  */
+/* ------------------------------------------------------------------------ */
+static inline float silu_f32(float v) { return v / (1.0f + expf(-v)); }
+
+/* dense y[r] = W[r] . q(x) for r < rows (ggml MUL_MAT with the same vec_dot) */
+static void dense_matvec(const uint8_t *W, int qt, int rows, int k, const float *x, float *y, int nt) {
+    const size_t rb = orc_row_bytes(qt, k);
+    uint8_t *act = (uint8_t *)malloc(orc_act_row_bytes(qt, k));
+    orc_quantize_act(qt, x, act, k);
+    #pragma omp parallel for num_threads(nt) schedule(static)
+    for (int r = 0; r < rows; ++r) y[r] = orc_vec_dot(qt, W + (size_t)r * rb, act, k);
+    free(act);
+}
+
+int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *ids,
+                  const float *w, int n_used, int n_tokens, float *out, float *h_out, int n_threads) {
+    const int D = L->d_model, F = L->d_ff;
+    const size_t rbg = orc_row_bytes(L->qt_gate, D), rbu = orc_row_bytes(L->qt_up, D);
+    const size_t rbd = orc_row_bytes(L->qt_down, F);
+    if (!rbg || !rbu || !rbd || n_used <= 0) return -1;
+    for (int p = 0; p < n_tokens * n_used; ++p)
+        if (ids[p] < 0 || ids[p] >= L->n_experts) return -1;
+    const int nt = threads_or_default(n_threads);
+    const size_t esg = rbg * (size_t)F, esu = rbu * (size_t)F, esd = rbd * (size_t)D;
+    float *g = (float *)malloc(sizeof(float) * (size_t)F);
+    float *u = (float *)malloc(sizeof(float) * (size_t)F);
+    float *h = (float *)malloc(sizeof(float) * (size_t)F * n_used);
+    float *y = (float *)malloc(sizeof(float) * (size_t)D * n_used);
+    for (int t = 0; t < n_tokens; ++t) {
+        const float *xt = x + (size_t)t * D;
+        for (int s = 0; s < n_used; ++s) {
+            const int e = ids[t * n_used + s];
+            dense_matvec((const uint8_t *)L->gate + (size_t)e * esg, L->qt_gate, F, D, xt, g, nt);
+            dense_matvec((const uint8_t *)L->up + (size_t)e * esu, L->qt_up, F, D, xt, u, nt);
+            float *hs = h + (size_t)s * F;
+            for (int j = 0; j < F; ++j) hs[j] = silu_f32(g[j]) * u[j];
+            dense_matvec((const uint8_t *)L->down + (size_t)e * esd, L->qt_down, D, F, hs, y + (size_t)s * D, nt);
+        }
+        if (h_out) memcpy(h_out + (size_t)t * n_used * F, h, sizeof(float) * (size_t)F * n_used);
+        float *ot = out + (size_t)t * D;
+        for (int i = 0; i < D; ++i) {
+            float acc = y[i] * w[t * n_used + 0];
+            for (int s = 1; s < n_used; ++s) acc = acc + y[(size_t)s * D + i] * w[t * n_used + s];
+            ot[i] = acc;
+        }
+        if (L->shared_gate) {
+            const int Fs = L->d_ff_shared;
+            float *gs = (float *)malloc(sizeof(float) * (size_t)Fs);
+            float *us = (float *)malloc(sizeof(float) * (size_t)Fs);
+            float *ys = (float *)malloc(sizeof(float) * (size_t)D);
+            dense_matvec((const uint8_t *)L->shared_gate, L->qt_shared_gate, Fs, D, xt, gs, nt);
+            dense_matvec((const uint8_t *)L->shared_up, L->qt_shared_up, Fs, D, xt, us, nt);
+            for (int j = 0; j < Fs; ++j) gs[j] = silu_f32(gs[j]) * us[j];
+            dense_matvec((const uint8_t *)L->shared_down, L->qt_shared_down, D, Fs, gs, ys, nt);
+            for (int i = 0; i < D; ++i) ot[i] = ot[i] + ys[i];
+            free(gs); free(us); free(ys);
+        }
+    }
+    free(g); free(u); free(h); free(y);
+    return 0;
+}

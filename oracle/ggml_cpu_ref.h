@@ -1,0 +1,97 @@
+/*
+ * ORACLE - test infrastructure only.
+ *
+ * A plain-C restatement of ggml's CPU MUL_MAT_ID path for the four expert
+ * formats (Q8_0, Q4_K, Q6_K, IQ3_S), used as the checker for the HIP kernels.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * it.  The product library never links or calls it.
+ *
+ * ggml itself (llama.cpp @ 96ffdc41ceb055e1c2d3d96667ae6d9f0ccb710b, pinned in
+ * third_party/llama.cpp.version:1-2) is not vendored in the reference, so the
+ * algorithm is restated from its published form and anchored on the
+ * reference's own call sites and format readers; each function below cites
+ * them.  Function-level pinning is described in oracle/README.md.
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml_type codes (sabah/runtime/rt.py:20-23 uses the same enum values). */
+enum {
+    ORC_F32 = 0,
+    ORC_Q8_0 = 8,
+    ORC_Q4_K = 12,
+    ORC_Q6_K = 14,
+    ORC_Q8_K = 15,
+    ORC_IQ3_S = 21,
+};
+
+/* Block geometry: elements and bytes per block (sabah_rt.cu:2155-2184;
+ * Q6_K from quants.py:586-606 and model_inspector.py:34). */
+int orc_block_elems(int qt);
+int orc_block_bytes(int qt);
+size_t orc_row_bytes(int qt, int n);
+/* the activation format ggml's CPU quantises src1 into for weight type qt */
+int orc_vec_dot_type(int qt);
+
+/* IEEE binary16 conversion; fp32 -> fp16 rounds to nearest even. */
+float orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_fp16(float f);
+
+/* Activation quantisers (ggml quantize_row_q8_0_ref / quantize_row_q8_K_ref). */
+void orc_quantize_q8_0(const float *x, uint8_t *y, int k);
+void orc_quantize_q8_K(const float *x, uint8_t *y, int k);
+/* quantise a row of k floats into the activation format for weight type qt */
+int orc_quantize_act(int qt, const float *x, uint8_t *y, int k);
+size_t orc_act_row_bytes(int qt, int k);
+
+/* Weight encoders.  Q8_0 follows ggml's reference quantiser; Q4_K, Q6_K and
+ * IQ3_S are simple valid encoders of this project's own (parity is judged on
+ * decoding the same bytes, not on encoder quality). */
+int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k);
+
+/* Decode a row of k elements (ggml dequantize_row_*). */
+int orc_dequantize_row(int qt, const uint8_t *x, float *y, int k);
+
+/* One dot product of a weight row with a quantised activation row
+ * (ggml_vec_dot_{q8_0_q8_0, q4_K_q8_K, q6_K_q8_K, iq3_s_q8_K}). */
+float orc_vec_dot(int qt, const uint8_t *w, const uint8_t *a, int k);
+
+/* MUL_MAT_ID on host buffers with the sabah_rt_mul_mat_id_v2 argument
+ * meaning (sabah_rt.cu:3494-3515): dst[t][i][r] = W[ids[t][i]][r] . q8(x[t][i % x_rows]).
+ * Returns 0, or -1 on invalid arguments.  n_threads <= 0 means all cores. */
+int orc_mul_mat_id(const void *source, size_t expert_stride, size_t row_stride,
+                   const float *x, size_t x_id_stride, int x_rows, size_t x_token_stride,
+                   const int32_t *ids, size_t ids_id_stride, size_t ids_token_stride,
+                   int n_ids, int n_tokens,
+                   float *dst, size_t dst_id_stride, size_t dst_token_stride,
+                   int rows, int k, int n_experts, int qt, int n_threads);
+
+/* The gated expert FFN of one MoE layer as ggml's graph runs it
+ * (qwen4exp.cpp:848-862 -> build_moe_ffn; executor.py:1-16):
+ *   g = MUL_MAT_ID(gate), u = MUL_MAT_ID(up), h = silu(g) * u,
+ *   y = MUL_MAT_ID(down, h), out = sum_k (y_k * w_k)   (serial over k)
+ * plus, when shared_gate != NULL, a dense shared expert added last:
+ *   out += down_s(silu(gate_s x) * up_s x).
+ * Expert tensors are [n_experts][rows][row_bytes] (GGUF layout).
+ * x [n_tokens][d_model], ids/w [n_tokens][n_used], out [n_tokens][d_model]. */
+typedef struct {
+    const void *gate, *up, *down;
+    int qt_gate, qt_up, qt_down;
+    int d_model, d_ff, n_experts;
+    const void *shared_gate, *shared_up, *shared_down;   /* optional */
+    int qt_shared_gate, qt_shared_up, qt_shared_down;
+    int d_ff_shared;
+} orc_moe_layer_desc;
+
+int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *ids,
+                  const float *w, int n_used, int n_tokens, float *out,
+                  float *h_out /* optional [n_tokens][n_used][d_ff] */, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif

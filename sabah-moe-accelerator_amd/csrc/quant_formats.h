@@ -1,0 +1,94 @@
+// Quantised block formats of the expert bank, shared by host and device code.
+//
+// Type codes are ggml's enum values so traces stay comparable with llama.cpp
+// (sabah/runtime/rt.py:20-23; Q6_K = 14 and Q8_K = 15 are the same enum).
+// Geometry follows sabah_rt.cu:2155-2191 for Q8_0/Q4_K/IQ3_S and
+// gguf-py quants.py:586-606 for Q6_K (ql[128] qh[64] int8 scales[16] fp16 d).
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "iq3s_grid.h"
+
+namespace sabah {
+
+enum : int {
+    QT_F32 = 0,
+    QT_Q8_0 = 8,
+    QT_Q4_K = 12,
+    QT_Q6_K = 14,
+    QT_Q8_K = 15,
+    QT_IQ3_S = 21,
+};
+
+__host__ __device__ constexpr int block_elems(int qt) {
+    return qt == QT_Q8_0 ? 32
+         : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_Q8_K || qt == QT_IQ3_S) ? 256 : 0;
+}
+
+__host__ __device__ constexpr int block_bytes(int qt) {
+    return qt == QT_Q8_0 ? 34
+         : qt == QT_Q4_K ? 144
+         : qt == QT_Q6_K ? 210
+         : qt == QT_Q8_K ? 292
+         : qt == QT_IQ3_S ? 110 : 0;
+}
+
+__host__ __device__ inline size_t row_bytes(int qt, int n) {
+    const int be = block_elems(qt);
+    if (be == 0 || n % be) return 0;
+    return (size_t)(n / be) * (size_t)block_bytes(qt);
+}
+
+// The activation format ggml's CPU pairs with each weight type
+// (q8_0 for Q8_0; q8_K for the K-quants and IQ3_S).
+__host__ __device__ constexpr int act_type(int qt) {
+    return qt == QT_Q8_0 ? QT_Q8_0
+         : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S) ? QT_Q8_K : -1;
+}
+
+__host__ __device__ constexpr bool supported_weight_type(int qt) {
+    return qt == QT_Q8_0 || qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S;
+}
+
+// Expanded IQ3_S codebook entry: byte j = 2*level_j + 1.
+__host__ __device__ constexpr uint32_t iq3s_entry(uint16_t lv) {
+    return (uint32_t)(2 * ((lv >> 0) & 7) + 1) | ((uint32_t)(2 * ((lv >> 3) & 7) + 1) << 8) |
+           ((uint32_t)(2 * ((lv >> 6) & 7) + 1) << 16) | ((uint32_t)(2 * ((lv >> 9) & 7) + 1) << 24);
+}
+
+struct Iq3sGrid {
+    uint32_t e[512];
+};
+__host__ __device__ constexpr Iq3sGrid make_iq3s_grid() {
+    Iq3sGrid g{};
+    for (int i = 0; i < 512; ++i) g.e[i] = iq3s_entry(kIq3sGridLevels[i]);
+    return g;
+}
+// the expanded codebook as device constant memory; kernels copy it into LDS
+__constant__ Iq3sGrid kIq3sGridDev = make_iq3s_grid();
+
+// ---------------------------------------------------------------------------
+// Device-side activation row layout (scratch, never an ABI):
+//   qs   int8[kp]            kp = k rounded up to a multiple of 256
+//   d    float[kp / QB]      per-block scale (q8_0: the fp16-rounded value)
+//   bsum int16[kp / 16]      q8_K only: sums of 16 consecutive qs
+// padded so every part starts 16-byte aligned; the padding quantises zeros.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+struct ActLayout {
+    int k, at;             // elements, activation type (QT_Q8_0 / QT_Q8_K)
+    size_t off_d, off_bsum, bytes;
+    __host__ __device__ ActLayout(int k_, int at_) : k(k_), at(at_) {
+        const int qb = block_elems(at_);
+        const size_t kp = (size_t)((k_ + 255) / 256) * 256;
+        off_d = kp;
+        off_bsum = align16(off_d + sizeof(float) * (kp / (size_t)qb));
+        bytes = align16(off_bsum + (at_ == QT_Q8_K ? sizeof(int16_t) * (kp / 16) : 0));
+    }
+};
+
+}  // namespace sabah

@@ -1,0 +1,184 @@
+"""
+Sabah / runtime / rt
+
+ctypes binding to libsabah_rt.so, the MI355X build of the runtime.  Same
+shape as the reference binding (sabah/runtime/rt.py:20-142): quant codes and
+block geometry, a `lib()` loader with argument types, `check()` turning a -1
+into an exception that carries the runtime's message, `row_bytes()`.
+
+Device memory and streams come from PyTorch-ROCm; this module only moves
+pointers and sizes.  There is no CPU fallback: if the library is missing,
+every entry point raises RuntimeUnavailable.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(os.path.dirname(HERE))          # sabah-moe-accelerator_amd/
+CSRC = os.path.join(PKG_ROOT, "csrc")
+
+# ggml type codes, so a runtime trace and a llama.cpp trace mean the same thing
+QTYPE = {"Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "IQ3_S": 21}
+QTYPE_NAME = {v: k for k, v in QTYPE.items()}
+
+# (elements per block, bytes per block)
+QBLOCK = {8: (32, 34), 12: (256, 144), 14: (256, 210), 21: (256, 110)}
+
+
+class RuntimeUnavailable(Exception):
+    """The HIP runtime library is missing or could not be loaded."""
+
+
+class SabahRuntimeError(Exception):
+    """A runtime entry point returned -1; the message is the runtime's."""
+
+
+# the reference's name for the same exception (rt.py:37-38)
+SabahCudaError = SabahRuntimeError
+
+
+def library_path() -> str:
+    return os.environ.get("SABAH_RT_LIB") or os.path.join(CSRC, "libsabah_rt.so")
+
+
+_lib = None
+
+c_vp, c_sz, c_i, c_u64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_ulonglong
+
+
+class MoeLayerDesc(ctypes.Structure):
+    """sabah_moe_layer_desc (include/sabah_rt.h)."""
+    _fields_ = [("gate", c_vp), ("up", c_vp), ("down", c_vp),
+                ("qt_gate", c_i), ("qt_up", c_i), ("qt_down", c_i),
+                ("d_model", c_i), ("d_ff", c_i), ("n_experts", c_i),
+                ("shared_gate", c_vp), ("shared_up", c_vp), ("shared_down", c_vp),
+                ("qt_shared_gate", c_i), ("qt_shared_up", c_i), ("qt_shared_down", c_i),
+                ("d_ff_shared", c_i)]
+
+
+# every symbol include/sabah_rt.h declares, with its ctypes signature
+SIGNATURES = {
+    "sabah_rt_init": ([c_i], c_i),
+    "sabah_rt_shutdown": ([], c_i),
+    "sabah_rt_last_error": ([], ctypes.c_char_p),
+    "sabah_rt_build_info": ([], ctypes.c_char_p),
+    "sabah_rt_device_count": ([], c_i),
+    "sabah_rt_mul_mat_id_v2": ([c_vp, c_sz, c_sz, c_vp, c_sz, c_i, c_sz, c_vp, c_sz, c_sz, c_i, c_i,
+                                c_vp, c_sz, c_sz, c_i, c_i, c_i, c_i, c_vp, c_vp], c_i),
+    "sabah_rt_register_bank": ([c_vp, c_vp, c_sz, c_sz, c_i], c_i),
+    "sabah_rt_unregister_bank": ([c_vp], c_i),
+    "sabah_rt_check_errors": ([], c_i),
+    "sabah_rt_get_metrics": ([ctypes.POINTER(c_u64)] * 5, c_i),
+    "sabah_rt_get_diag": ([ctypes.POINTER(c_u64)] * 5, c_i),
+    "sabah_rt_snapshot": ([ctypes.c_char_p, c_sz], c_i),
+    "sabah_row_bytes": ([c_i, c_i], c_sz),
+    "sabah_dequant": ([c_vp, c_vp, c_i, c_i, c_i], c_i),
+    "sabah_quantize_act": ([c_vp, c_vp, c_i, c_i, c_i, c_vp], c_i),
+    "sabah_moe_block": ([c_vp, c_vp, c_vp, c_vp, c_vp, c_i, c_i, c_i, c_i, c_i, c_i, c_i], c_i),
+    "sabah_moe_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
+    "sabah_moe_chain": ([ctypes.POINTER(MoeLayerDesc), c_i, c_vp, c_vp, c_vp, c_i, c_i, c_vp], c_i),
+}
+
+# harness-only exports (not part of the drop-in header)
+EXTRA_SIGNATURES = {
+    "sabah_sync_all": ([], c_i),
+    "sabah_sync_compute": ([], c_i),
+    "sabah_synth_weights": ([c_vp, c_i, ctypes.c_longlong, c_i, ctypes.c_ulonglong, ctypes.c_float, c_vp], c_i),
+}
+
+
+def lib():
+    """Load the runtime library once, with an actionable error if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = library_path()
+    if not os.path.exists(p):
+        raise RuntimeUnavailable(
+            "Sabah HIP runtime not built: %s\nBuild it with:\n"
+            "    python -c 'import __graft_entry__ as g; g.build()'   (or: make -C %s)" % (p, CSRC))
+    try:
+        L = ctypes.CDLL(p)
+    except OSError as e:
+        raise RuntimeUnavailable("could not load %s: %s" % (p, e))
+    for table in (SIGNATURES, EXTRA_SIGNATURES):
+        for name, (argt, rest) in table.items():
+            fn = getattr(L, name)
+            fn.argtypes = argt
+            fn.restype = rest
+    _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    try:
+        return (lib().sabah_rt_last_error() or b"").decode("utf-8", "replace")
+    except Exception:
+        return ""
+
+
+def check(rc, what="runtime call"):
+    if rc is None or (isinstance(rc, int) and rc != 0):
+        raise SabahRuntimeError("%s failed: %s" % (what, last_error()))
+    return rc
+
+
+def row_bytes(qt: int, n: int) -> int:
+    """Bytes occupied by one row of n elements at quant type qt."""
+    be, bb = QBLOCK[qt]
+    if n % be:
+        raise ValueError("row of %d elements is not a whole number of %s blocks"
+                         % (n, QTYPE_NAME.get(qt, qt)))
+    return n // be * bb
+
+
+def available() -> bool:
+    try:
+        lib()
+        return True
+    except RuntimeUnavailable:
+        return False
+
+
+def device_count() -> int:
+    try:
+        return int(lib().sabah_rt_device_count())
+    except RuntimeUnavailable:
+        return 0
+
+
+_initialised = None
+
+
+def init(device: int = 0) -> None:
+    """sabah_rt_init once per process (idempotent for the same device)."""
+    global _initialised
+    if _initialised == device:
+        return
+    check(lib().sabah_rt_init(device), "sabah_rt_init")
+    _initialised = device
+
+
+def metrics() -> dict:
+    v = [c_u64() for _ in range(5)]
+    check(lib().sabah_rt_get_metrics(*[ctypes.byref(z) for z in v]), "get_metrics")
+    return dict(zip(("hits", "misses", "evictions", "bytes_fetched", "resident_bytes"), (z.value for z in v)))
+
+
+def diag() -> dict:
+    v = [c_u64() for _ in range(5)]
+    check(lib().sabah_rt_get_diag(*[ctypes.byref(z) for z in v]), "get_diag")
+    return dict(zip(("calls", "tokens", "overflow", "verify_ok", "verify_fail"), (z.value for z in v)))
+
+
+def snapshot() -> dict:
+    import json
+    buf = ctypes.create_string_buffer(2048)
+    check(lib().sabah_rt_snapshot(buf, 2048), "snapshot")
+    return json.loads(buf.value.decode())
+
+
+def build_info() -> str:
+    return lib().sabah_rt_build_info().decode()

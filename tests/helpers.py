@@ -1,0 +1,95 @@
+"""Shared test helpers: parity metrics, hand-built quant blocks, decoded activations."""
+from __future__ import annotations
+
+import os
+import re
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REF = "/root/reference"
+
+MAX_REL_TOL = 1e-3      # max|y - r| / max|r|
+COS_TOL = 0.99999
+
+
+def max_rel(y, r) -> float:
+    y, r = np.asarray(y, np.float64), np.asarray(r, np.float64)
+    return float(np.abs(y - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def rel_l2(y, r) -> float:
+    y, r = np.asarray(y, np.float64), np.asarray(r, np.float64)
+    return float(np.linalg.norm(y - r) / max(np.linalg.norm(r), 1e-30))
+
+
+def cosine(y, r) -> float:
+    y, r = np.asarray(y, np.float64).ravel(), np.asarray(r, np.float64).ravel()
+    return float(y @ r / max(np.sqrt((y @ y) * (r @ r)), 1e-300))
+
+
+def assert_parity(y, r, what=""):
+    mr, c = max_rel(y, r), cosine(y, r)
+    assert mr <= MAX_REL_TOL and c >= COS_TOL, "%s: max_rel=%.3e (tol %.0e) cos=%.8f (tol %.5f) rel_l2=%.3e" % (
+        what, mr, MAX_REL_TOL, c, COS_TOL, rel_l2(y, r))
+    return mr, c
+
+
+def f16(x: float) -> bytes:
+    return np.array([x], np.float16).tobytes()
+
+
+def dequant_act(O, qt: int, act: np.ndarray, k: int) -> np.ndarray:
+    """float64 values of a quantised activation row (as its vec_dot partner sees them)."""
+    act = np.ascontiguousarray(act, np.uint8).reshape(-1)
+    if qt == O.Q8_0:
+        blk = act.reshape(-1, 34)
+        d = blk[:, :2].copy().view(np.float16).astype(np.float64)
+        return (blk[:, 2:].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
+    blk = act.reshape(-1, 292)
+    d = blk[:, :4].copy().view(np.float32).astype(np.float64)
+    return (blk[:, 4:260].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
+
+
+def reference_iq3s_grid() -> list[int] | None:
+    """The 512-entry IQ3_S grid as the reference's table header spells it (text parse)."""
+    p = os.path.join(REF, "sabah/runtime/cuda/sabah_iq_tables.h")
+    if not os.path.exists(p):
+        return None
+    t = open(p).read()
+    i = t.index("static const uint32_t iq3s_grid[512]")
+    body = t[i:t.index("};", i)]
+    return [int(x, 16) for x in re.findall(r"0x([0-9a-fA-F]{8})", body)]
+
+
+def oracle_iq3s_grid() -> list[int]:
+    t = open(os.path.join(ROOT, "oracle", "iq3s_grid_u32.h")).read()
+    return [int(x, 16) for x in re.findall(r"0x([0-9a-fA-F]{8})", t)]
+
+
+def product_iq3s_grid() -> list[int]:
+    """Expand the product's packed level table (csrc/iq3s_grid.h) to the byte form."""
+    t = open(os.path.join(ROOT, "sabah-moe-accelerator_amd", "csrc", "iq3s_grid.h")).read()
+    body = t[t.index("kIq3sGridLevels"):]
+    lv = [int(x, 16) for x in re.findall(r"0x([0-9a-fA-F]{3})", body)]
+    return [sum((2 * ((v >> (3 * j)) & 7) + 1) << (8 * j) for j in range(4)) for v in lv]
+
+
+def random_blocks(rng, qt: int, n_rows: int, k: int) -> np.ndarray:
+    """Random bytes that form valid blocks: every field random, fp16 scales finite and modest."""
+    from oracle import BLOCK
+    qb, bb = BLOCK[qt]
+    nb = k // qb
+    raw = rng.integers(0, 256, size=(n_rows, nb, bb), dtype=np.uint8)
+
+    def scales(n):
+        return (rng.uniform(0.25, 2.0, size=n) * rng.choice([-1, 1], size=n) * 1e-2).astype(np.float16)
+
+    if qt in (8, 21):                       # Q8_0, IQ3_S: fp16 d at 0
+        raw[:, :, 0:2] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
+    elif qt == 12:                          # Q4_K: d, dmin at 0, 2 (non-negative in real data)
+        raw[:, :, 0:2] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)
+        raw[:, :, 2:4] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)
+    elif qt == 14:                          # Q6_K: d at 208
+        raw[:, :, 208:210] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
+    return raw.reshape(n_rows, nb * bb)

@@ -1,0 +1,94 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol the public
+header declares, and rejects invalid MUL_MAT_ID arguments before touching the
+device (the host-side checks of sabah_rt.cu:3516-3547)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from helpers import ROOT
+
+HEADER = os.path.join(ROOT, "include", "sabah_rt.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sabah_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from sabah.runtime import rt
+    L = rt.lib()
+    names = declared_functions()
+    assert len(names) >= 17
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header():
+    from sabah.runtime import rt
+    assert set(declared_functions()) == set(rt.SIGNATURES)
+
+
+def test_build_info_and_row_bytes():
+    from sabah.runtime import rt
+    L = rt.lib()
+    assert rt.build_info().startswith("sabah_rt abi=v2 sentinel=0")
+    assert L.sabah_row_bytes(21, 2048) == 880 and L.sabah_row_bytes(21, 768) == 330
+    assert L.sabah_row_bytes(12, 768) == 432 and L.sabah_row_bytes(14, 768) == 630
+    assert L.sabah_row_bytes(8, 1024) == 1088
+    assert L.sabah_row_bytes(2, 1024) == 0           # unsupported type
+    assert L.sabah_row_bytes(21, 100) == 0           # not a whole number of blocks
+
+
+def _v2(L, **kw):
+    a = dict(source=1, expert_stride=880 * 768, row_stride=880, d_x=1, x_id_stride=8192, x_rows=1,
+             x_token_stride=8192, d_ids=1, ids_id_stride=4, ids_token_stride=40, n_ids=10, n_tokens=1,
+             d_dst=1, dst_id_stride=3072, dst_token_stride=30720, rows=768, k=2048, n_experts=512, qt=21)
+    a.update(kw)
+    vp = ctypes.c_void_p
+    return L.sabah_rt_mul_mat_id_v2(vp(a["source"]), a["expert_stride"], a["row_stride"], vp(a["d_x"]),
+                                    a["x_id_stride"], a["x_rows"], a["x_token_stride"], vp(a["d_ids"]),
+                                    a["ids_id_stride"], a["ids_token_stride"], a["n_ids"], a["n_tokens"],
+                                    vp(a["d_dst"]), a["dst_id_stride"], a["dst_token_stride"], a["rows"], a["k"],
+                                    a["n_experts"], a["qt"], None, None)
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(k=2047), "geometry"),
+    (dict(k=2016), "whole number"),
+    (dict(x_rows=3), "input rows"),
+    (dict(qt=2), "unsupported quant type"),
+    (dict(row_stride=879), "row stride"),
+    (dict(source=0), "null pointer"),
+    (dict(n_experts=0), "geometry"),
+])
+def test_v2_rejects_invalid_arguments_without_a_device(bad, msg):
+    from sabah.runtime import rt
+    L = rt.lib()
+    assert _v2(L, **bad) == -1
+    assert msg in rt.last_error()
+
+
+def test_v2_zero_tokens_is_a_counted_noop():
+    from sabah.runtime import rt
+    L = rt.lib()
+    before = rt.snapshot()["empty_calls"]
+    assert _v2(L, n_tokens=0) == 0
+    assert rt.snapshot()["empty_calls"] == before + 1
+
+
+def test_v2_requires_init():
+    from sabah.runtime import rt
+    if rt._initialised is not None:
+        pytest.skip("runtime already initialised in this process")
+    assert _v2(rt.lib()) == -1
+    assert "sabah_rt_init" in rt.last_error()
+
+
+def test_metrics_before_any_call():
+    from sabah.runtime import rt
+    m = rt.metrics()
+    assert m["misses"] == 0 and m["evictions"] == 0 and m["bytes_fetched"] == 0

@@ -1,0 +1,304 @@
+"""HIP kernels vs the oracle, through the C ABI (needs an MI355X).
+
+Bar: q8 activation bytes, dequantised weights and routing bit-exact; outputs
+within max|y-r|/max|r| <= 1e-3 and cosine >= 0.99999 of the oracle (the
+ggml-CPU restatement) on the same seeded inputs.
+"""
+from __future__ import annotations
+
+import ctypes
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_parity, random_blocks
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_K, Q6_K, IQ3_S = 8, 12, 14, 21
+DEV = torch.device("cuda:0")
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def make_bank(orc, rng, qts, E, D, F, n_layers=1):
+    from sabah.runtime.bank import ExpertBank
+    bank = ExpertBank(n_layers, E, D, F, {"gate": qts[0], "up": qts[1], "down": qts[2]}, device="cuda:0")
+    raws = {}
+    for l in range(n_layers):
+        for role, (rows, cols), qt in (("gate", (F, D), qts[0]), ("up", (F, D), qts[1]), ("down", (D, F), qts[2])):
+            raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32))
+            bank.load(l, role, raw)
+            raws[(l, role)] = raw
+    return bank, raws
+
+
+# ---------------------------------------------------------------------------
+# bit-exact pieces
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("qt", [Q8_0, IQ3_S])
+def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
+    rng = np.random.default_rng(100 + qt)
+    k = 2048
+    x = rng.standard_normal((9, k)).astype(np.float32)
+    x[1] *= 1e-3
+    x[2] = 0.0                                              # zero rows
+    x[3, :] = np.round(rng.standard_normal(k) * 40) + 0.5   # many exact ties
+    x[3, 0] = -127.0 if qt != Q8_0 else 127.0
+    x[4, 5] = 7.0
+    x[4, 900] = -7.0                                        # equal magnitudes, opposite signs
+    x[5] = 0.75                                             # constant row
+    x[6, ::2] = 0.0
+    x[7] *= 1e4
+    ab = orc.act_row_bytes(qt, k)
+    y = torch.zeros(9, ab, dtype=torch.uint8, device=DEV)
+    hip_rt.check(hip_rt.lib().sabah_quantize_act(vp(T(x)), vp(y), qt, 9, k, stream()), "quantize_act")
+    torch.cuda.synchronize()
+    want = orc.quantize_act(qt, x)
+    assert np.array_equal(y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768)])
+def test_dequant_is_bit_exact(hip_rt, orc, qt, k):
+    rng = np.random.default_rng(qt * 7 + k)
+    raw = random_blocks(rng, qt, 37, k)
+    src = T(raw)
+    dst = torch.empty(37, k, dtype=torch.float32, device=DEV)
+    torch.cuda.synchronize()
+    hip_rt.check(hip_rt.lib().sabah_dequant(vp(src), vp(dst), qt, 37, k), "dequant")
+    got = dst.cpu().numpy()
+    want = orc.dequantize(qt, raw, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# MUL_MAT_ID through sabah_rt_mul_mat_id_v2
+# ---------------------------------------------------------------------------
+def v2(hip_rt, src, expert_stride, row_bytes, x, ids, out, rows, k, E, qt):
+    return hip_rt.lib().sabah_rt_mul_mat_id_v2(
+        ctypes.c_void_p(src), expert_stride, row_bytes,
+        vp(x), x.stride(1) * 4, x.shape[1], x.stride(0) * 4,
+        vp(ids), 4, ids.stride(0) * 4, ids.shape[1], ids.shape[0],
+        vp(out), out.stride(1) * 4, out.stride(0) * 4, rows, k, E, qt, stream(), None)
+
+
+CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q4_K, 2048, 48), (Q4_K, 768, 64),
+         (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104)]
+
+
+@pytest.mark.parametrize("qt,k,rows", CASES)
+@pytest.mark.parametrize("x_rows_is_n_ids", [False, True])
+def test_mul_mat_id_matches_oracle(hip_rt, orc, qt, k, rows, x_rows_is_n_ids):
+    rng = np.random.default_rng(qt * 1000 + k + rows + x_rows_is_n_ids)
+    E, Tn, K = 7, 3, 4
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    ids = np.stack([rng.choice(E, K, replace=False) for _ in range(Tn)]).astype(np.int32)
+    ids[2, 3] = ids[2, 1]                                    # duplicate id
+    x_rows = K if x_rows_is_n_ids else 1
+    x = rng.standard_normal((Tn, x_rows, k)).astype(np.float32)
+    bank = T(raw)
+    out = torch.full((Tn, K, rows), float("nan"), dtype=torch.float32, device=DEV)
+    rb = raw.shape[-1]
+    hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * rb, rb, T(x), T(ids), out, rows, k, E, qt), "v2")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    assert_parity(got, want, "qt=%d k=%d" % (qt, k))
+    if qt in (Q8_0, IQ3_S):
+        # same int sums, same fp32 scale-and-accumulate order as ggml's vec_dot
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if x_rows == 1:
+        assert np.array_equal(got[2, 3], got[2, 1])
+
+
+def test_mul_mat_id_detects_wrong_expert_and_wrong_row(hip_rt, orc):
+    rng = np.random.default_rng(77)
+    qt, E, rows, k, K = IQ3_S, 8, 64, 768, 4
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    ids = np.array([[1, 5, 2, 7]], np.int32)
+    x = rng.standard_normal((1, K, k)).astype(np.float32)
+    out = torch.empty(1, K, rows, dtype=torch.float32, device=DEV)
+    hip_rt.check(v2(hip_rt, T(raw).data_ptr(), rows * 330, 330, T(x), T(ids), out, rows, k, E, qt), "v2")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    exact = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    wrong_expert = orc.mul_mat_id(raw, x, (ids + 1) % E, rows, k, qt)
+    row0 = orc.mul_mat_id(raw, np.repeat(x[:, :1], K, axis=1), ids, rows, k, qt)
+    from helpers import rel_l2
+    err = rel_l2(got, exact)
+    assert rel_l2(wrong_expert, exact) > 1e4 * max(err, 1e-9)
+    assert rel_l2(row0, exact) > 1e-1
+
+
+def test_registered_key_gives_bit_identical_results(hip_rt, orc):
+    """A caller-side (host) address registered for the bank selects the same bytes
+    as the device pointer itself; moving the bank does not change a bit."""
+    rng = np.random.default_rng(78)
+    qt, E, rows, k, K = IQ3_S, 6, 48, 2048, 3
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    host_key = np.zeros(raw.size, np.uint8)                 # stands for llama.cpp's mmap address
+    dev_a, dev_b = T(raw), T(raw)
+    ids = np.array([[4, 0, 4]], np.int32)
+    x = rng.standard_normal((1, 1, k)).astype(np.float32)
+    L = hip_rt.lib()
+    outs = []
+    for src in (dev_a.data_ptr(), dev_b.data_ptr(), host_key.ctypes.data):
+        if src == host_key.ctypes.data:
+            hip_rt.check(L.sabah_rt_register_bank(ctypes.c_void_p(src), vp(dev_b), raw.size, rows * 880, E), "register")
+        out = torch.empty(1, K, rows, dtype=torch.float32, device=DEV)
+        hip_rt.check(v2(hip_rt, src, rows * 880, 880, T(x), T(ids), out, rows, k, E, qt), "v2")
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    hip_rt.check(L.sabah_rt_unregister_bank(ctypes.c_void_p(host_key.ctypes.data)), "unregister")
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    # an unregistered host address is refused with a message, not read
+    out = torch.empty(1, K, rows, dtype=torch.float32, device=DEV)
+    assert v2(hip_rt, host_key.ctypes.data, rows * 880, 880, T(x), T(ids), out, rows, k, E, qt) == -1
+    assert "register" in hip_rt.last_error()
+
+
+def test_out_of_range_id_poisons_its_slot_and_fails_the_next_call(hip_rt, orc):
+    rng = np.random.default_rng(79)
+    qt, E, rows, k = Q8_0, 4, 16, 256
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    bank = T(raw)
+    x = T(rng.standard_normal((1, 1, k)).astype(np.float32))
+    ids = T(np.array([[1, 9]], np.int32))                    # 9 >= n_experts
+    out = torch.zeros(1, 2, rows, dtype=torch.float32, device=DEV)
+    assert v2(hip_rt, bank.data_ptr(), rows * 272, 272, x, ids, out, rows, k, E, qt) == 0
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.all(np.isnan(o[0, 1])) and np.all(np.isfinite(o[0, 0]))
+    assert hip_rt.lib().sabah_rt_check_errors() == -1
+    assert "outside" in hip_rt.last_error()
+    assert hip_rt.lib().sabah_rt_check_errors() == 0       # the word was cleared
+
+
+def test_metrics_count_every_lookup_as_resident(hip_rt, orc):
+    before = hip_rt.metrics()["hits"]
+    rng = np.random.default_rng(80)
+    raw = orc.quantize_weights(Q8_0, (rng.standard_normal((3, 8, 64)) * 0.02).astype(np.float32))
+    out = torch.empty(2, 2, 8, dtype=torch.float32, device=DEV)
+    x = T(rng.standard_normal((2, 1, 64)).astype(np.float32))
+    hip_rt.check(v2(hip_rt, T(raw).data_ptr(), 8 * 68, 68, x, T(np.array([[0, 1], [2, 2]], np.int32)), out, 8, 64,
+                    3, Q8_0), "v2")
+    torch.cuda.synchronize()
+    m = hip_rt.metrics()
+    assert m["hits"] == before + 4 and m["misses"] == 0 and m["evictions"] == 0
+
+
+# ---------------------------------------------------------------------------
+# fused block / layer / chain
+# ---------------------------------------------------------------------------
+def test_moe_block_single_token_q8_0(hip_rt, orc):
+    """sabah_moe_block with the reference's signature, on the Q8_0 / E=8 / top-2 /
+    1024<->2048 workload (weights N(0,0.02) -> Q8_0, x ~ N(0,1), 2 distinct ids,
+    softmax weights)."""
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(2024)
+    E, D, F, K = 8, 1024, 2048, 2
+    bank, raws = make_bank(orc, rng, (Q8_0, Q8_0, Q8_0), E, D, F)
+    ex = MoEExecutor(bank, max_used=K)
+    x = rng.standard_normal(D).astype(np.float32)
+    ids = rng.choice(E, K, replace=False).astype(np.int32)
+    lg = rng.standard_normal(K)
+    w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
+    ex.upload_x(x)
+    ex.run_block(0, ids, w)
+    got = ex.download_out()
+    want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], (Q8_0,) * 3, x[None], ids[None],
+                         w[None])[0]
+    assert_parity(got, want, "moe_block")
+    # accumulate adds onto the previous output
+    ex.run_block(0, ids, w, accumulate=True)
+    assert_parity(ex.download_out(), 2 * want, "moe_block accumulate")
+
+
+@pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small"])
+def test_moe_layer_matches_oracle(hip_rt, orc, name):
+    from sabah.runtime import routing
+    from sabah.runtime.bank import DenseExpert
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(zlib.crc32(name.encode()) % 1000)
+    shared = None
+    if name == "q4k_e128_top8":
+        E, D, F, K, Tn, qts = 128, 2048, 768, 8, 1, (Q4_K, Q4_K, Q4_K)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
+    elif name == "mixed_t32_q4k_q6k_shared":
+        E, D, F, K, Tn, qts = 96, 2048, 768, 10, 32, (Q4_K, Q4_K, Q6_K)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
+    else:
+        E, D, F, K, Tn, qts = 64, 2048, 768, 10, 4, (IQ3_S, IQ3_S, IQ3_S)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    bank, raws = make_bank(orc, rng, qts, E, D, F)
+    sh_raw = None
+    if name.startswith("mixed"):
+        Fs = 512
+        shared = DenseExpert(D, Fs, Q8_0, device="cuda:0")
+        sh_raw = {}
+        for role, (rows, cols) in {"gate": (Fs, D), "up": (Fs, D), "down": (D, Fs)}.items():
+            sh_raw[role] = orc.quantize_weights(Q8_0, (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+            shared.load(role, sh_raw[role])
+    ex = MoEExecutor(bank, max_used=K, shared=shared)
+    x = rng.standard_normal((Tn, D)).astype(np.float32)
+    out = ex.run_layer(0, T(x), T(ids), T(w))
+    torch.cuda.synchronize()
+    sh = None if sh_raw is None else (sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3)
+    want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], qts, x, ids, w, shared=sh)
+    assert_parity(out.cpu().numpy(), want, name)
+
+
+def test_moe_chain_is_the_sequence_of_residual_layers(hip_rt, orc):
+    from sabah.runtime import routing
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(31)
+    E, D, F, K, L = 32, 1024, 512, 6, 3
+    bank, raws = make_bank(orc, rng, (IQ3_S,) * 3, E, D, F, n_layers=L)
+    ids, w = routing.zipf_routing(rng, 1, E, K, n_layers=L)
+    x0 = rng.standard_normal((1, D)).astype(np.float32)
+    ex = MoEExecutor(bank, max_used=K)
+    xd = T(x0)
+    ex.run_chain(xd, T(ids), T(w))
+    torch.cuda.synchronize()
+    xr = x0.copy()
+    for l in range(L):
+        xr = xr + orc.moe_layer(raws[(l, "gate")], raws[(l, "up")], raws[(l, "down")], (IQ3_S,) * 3, xr, ids[l], w[l])
+    assert_parity(xd.cpu().numpy(), xr, "chain")
+
+
+def test_full_size_iq3s_layer_on_synthetic_bank(hip_rt, orc):
+    """One layer of the 512-expert IQ3_S shape with the bank generated on the
+    device; the oracle reads back the ten routed experts' bytes."""
+    from sabah.runtime import routing
+    from sabah.runtime.bank import ExpertBank
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(48)
+    E, D, F, K = 512, 2048, 768, 10
+    bank = ExpertBank(1, E, D, F, {"gate": IQ3_S, "up": IQ3_S, "down": IQ3_S}, device="cuda:0")
+    bank.fill_synthetic(seed=7)
+    ids, w = routing.zipf_routing(rng, 1, E, K)
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    ex = MoEExecutor(bank, max_used=K)
+    out = ex.run_layer(0, T(x), T(ids), T(w))
+    torch.cuda.synchronize()
+    used = np.unique(ids)
+    remap = {int(e): i for i, e in enumerate(used)}
+    sub = {r: np.stack([bank.read_expert(0, r, int(e)) for e in used]) for r in ("gate", "up", "down")}
+    # weights look like quantised N(0, 0.02): the decoded spread is in range
+    dq = orc.dequantize(IQ3_S, sub["gate"][0], D)
+    assert 0.012 < dq.std() < 0.03
+    ids_local = np.vectorize(remap.get)(ids).astype(np.int32)
+    want = orc.moe_layer(sub["gate"], sub["up"], sub["down"], (IQ3_S,) * 3, x, ids_local, w)
+    assert_parity(out.cpu().numpy(), want, "full-size layer")
