@@ -5,7 +5,8 @@
  * (patches/llama.cpp/0001-sabah-native-mul-mat-id.patch:138-175) and that the
  * Python harness binds with ctypes (sabah/runtime/rt.py:53-114).  Plain
  * pointers and sizes only; device pointers are HIP device memory, `stream`
- * is a hipStream_t (NULL selects the library's own stream).
+ * is a hipStream_t used as given (NULL is the HIP null stream); entry points
+ * without a stream argument run on the library's own stream.
  *
  * Every int-returning entry point returns 0 on success and -1 on failure with
  * a message readable through sabah_rt_last_error().  The library is not
@@ -63,7 +64,7 @@ int sabah_rt_device_count(void);
  *                 dst_token_stride = nb[2]
  *   rows, k, n_experts, qt   src0->ne[1], ne[0], ne[2], ggml_type
  *                 (8 Q8_0, 12 Q4_K, 14 Q6_K, 21 IQ3_S; k % block size == 0)
- *   stream        hipStream_t the kernel is enqueued on (NULL: library stream)
+ *   stream        hipStream_t the kernel is enqueued on (NULL: the null stream)
  *   ids_key       accepted and ignored: ids are read on the device, never
  *                 downloaded, so there is nothing to reuse.  Callers passing
  *                 only 20 arguments (tests/test_mul_mat_id_contract.py:153-154)

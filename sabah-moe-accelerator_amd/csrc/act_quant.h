@@ -1,4 +1,4 @@
-// Activation quantisation on the device: one fp32 row -> q8_0 or q8_K, in the
+// Activation quantisation on the device: fp32 rows -> q8_0 or q8_K, in the
 // ActLayout scratch form (quant_formats.h).  The integer values and scales are
 // the ones ggml's CPU path feeds its vec_dot kernels:
 //   q8_0 (quantize_row_q8_0_ref): per 32 elements d = amax/127 rounded to fp16,
@@ -8,21 +8,36 @@
 //        (nearest even), d = 1/iscale in fp32, bsums = sums of 16 consecutive q.
 // The reference's own restatement of both steps is tools/rc4/opcheck.py:65-80.
 //
-// Work split: a wave64 owns one 256-element chunk at a time, four elements per
-// lane, so every reduction is a lane shuffle inside the wave.
+// Work split: sixteen lanes (one DPP row) own one 256-element chunk, sixteen
+// consecutive elements per lane, so a wave quantises four chunks at once,
+// every reduction is four DPP steps inside the row, and each lane's sixteen
+// values are exactly one q8_K bsum.
 #pragma once
 #include "quant_formats.h"
 
 namespace sabah {
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+template <int CTRL>
+__device__ inline uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within each 8-lane half-row
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within each 16-lane row
+
+__device__ inline float row16_max(float v) {
+    v = fmaxf(v, __uint_as_float(dpp<kDppXor1>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp<kDppXor2>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp<kDppMirror>(__float_as_uint(v))));
     return v;
 }
-__device__ inline int wave_min_i(int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+__device__ inline uint32_t row16_min(uint32_t v) {
+    v = min(v, dpp<kDppXor1>(v));
+    v = min(v, dpp<kDppXor2>(v));
+    v = min(v, dpp<kDppHalfMirror>(v));
+    v = min(v, dpp<kDppMirror>(v));
     return v;
 }
 
@@ -31,83 +46,167 @@ __device__ inline uint32_t pack4_i8(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// Quantise one 256-element chunk (chunk index c of the row) held as float4 by
-// the lanes of one wave.  Writes qs / d / bsum of that chunk into `act`.
-__device__ inline void wave_quant_chunk_q8K(float4 v, int c, uint8_t* act, const ActLayout& L) {
-    const int lane = threadIdx.x & 63;
-    const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
-    const float amax = wave_max(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
-    // first element (in row order) whose magnitude equals amax
-    int first = 0x7fffffff;
-    float cand = 0.0f;
-    if (a3 == amax) { first = 4 * lane + 3; cand = v.w; }
-    if (a2 == amax) { first = 4 * lane + 2; cand = v.z; }
-    if (a1 == amax) { first = 4 * lane + 1; cand = v.y; }
-    if (a0 == amax) { first = 4 * lane + 0; cand = v.x; }
-    const int fmin = wave_min_i(first);
-    const float mx = __shfl(cand, (fmin == 0x7fffffff ? 0 : fmin) >> 2, 64);
-    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+// sixteen consecutive floats of one lane
+struct Act16 {
+    float v[16];
+};
+
+// Quantise the chunk held by one 16-lane row (lane l holds elements 16l..16l+15)
+// into act (the row's ActLayout block), chunk index c.
+__device__ inline void row16_quant_q8K(const Act16& a, int c, uint8_t* act, const ActLayout& L) {
+    const uint32_t l = threadIdx.x & 15u;
+    float amax_l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax_l = fmaxf(amax_l, fabsf(a.v[j]));
+    const float amax = row16_max(amax_l);
+    // first element whose magnitude is amax, with its sign: key = index << 1 | sign
+    uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 15; j >= 0; --j)
+        if (fabsf(a.v[j]) == amax) key = ((16u * l + (uint32_t)j) << 1) | (__float_as_uint(a.v[j]) >> 31);
+    key = row16_min(key);
+    int q[16];
     float d = 0.0f;
     if (amax != 0.0f) {
+        const float mx = (key & 1u) ? -amax : amax;          // the first max's signed value
         const float iscale = __fdiv_rn(-127.0f, mx);
-        q0 = min(127, (int)rintf(__fmul_rn(iscale, v.x)));
-        q1 = min(127, (int)rintf(__fmul_rn(iscale, v.y)));
-        q2 = min(127, (int)rintf(__fmul_rn(iscale, v.z)));
-        q3 = min(127, (int)rintf(__fmul_rn(iscale, v.w)));
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = min(127, (int)rintf(__fmul_rn(iscale, a.v[j])));
         d = __fdiv_rn(1.0f, iscale);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = 0;
     }
-    reinterpret_cast<uint32_t*>(act)[c * 64 + lane] = pack4_i8(q0, q1, q2, q3);
-    // 16-element sums: four lanes per sum
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(act + L.off_bsum)[c * 16 + (lane >> 2)] = (int16_t)s;
-    if (lane == 0) reinterpret_cast<float*>(act + L.off_d)[c] = d;
+    uint4 packed;
+    packed.x = pack4_i8(q[0], q[1], q[2], q[3]);
+    packed.y = pack4_i8(q[4], q[5], q[6], q[7]);
+    packed.z = pack4_i8(q[8], q[9], q[10], q[11]);
+    packed.w = pack4_i8(q[12], q[13], q[14], q[15]);
+    reinterpret_cast<uint4*>(act + c * kActChunkStride)[l] = packed;
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += q[j];
+    reinterpret_cast<int16_t*>(act + L.off_bsum)[c * 16 + l] = (int16_t)s;
+    if (l == 0) reinterpret_cast<float*>(act + L.off_d)[c] = d;
 }
 
-// Same chunk shape for q8_0: eight 32-element blocks of eight lanes each.
-__device__ inline void wave_quant_chunk_q8_0(float4 v, int c, uint8_t* act, const ActLayout& L) {
-    const int lane = threadIdx.x & 63;
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+// q8_0: the 32-element block b of the chunk is lanes 2b and 2b+1
+__device__ inline void row16_quant_q8_0(const Act16& a, int c, uint8_t* act, const ActLayout& L) {
+    const uint32_t l = threadIdx.x & 15u;
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(a.v[j]));
+    amax = fmaxf(amax, __uint_as_float(dpp<kDppXor1>(__float_as_uint(amax))));
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    const int q0 = (int)roundf(__fmul_rn(v.x, id));
-    const int q1 = (int)roundf(__fmul_rn(v.y, id));
-    const int q2 = (int)roundf(__fmul_rn(v.z, id));
-    const int q3 = (int)roundf(__fmul_rn(v.w, id));
-    reinterpret_cast<uint32_t*>(act)[c * 64 + lane] = pack4_i8(q0, q1, q2, q3);
-    if ((lane & 7) == 0) {
-        const float dh = __half2float(__float2half_rn(d));
-        reinterpret_cast<float*>(act + L.off_d)[c * 8 + (lane >> 3)] = dh;
+    int q[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) q[j] = (int)roundf(__fmul_rn(a.v[j], id));
+    uint4 packed;
+    packed.x = pack4_i8(q[0], q[1], q[2], q[3]);
+    packed.y = pack4_i8(q[4], q[5], q[6], q[7]);
+    packed.z = pack4_i8(q[8], q[9], q[10], q[11]);
+    packed.w = pack4_i8(q[12], q[13], q[14], q[15]);
+    reinterpret_cast<uint4*>(act + c * kActChunkStride)[l] = packed;
+    if ((l & 1u) == 0) reinterpret_cast<float*>(act + L.off_d)[c * 8 + (l >> 1)] = __half2float(__float2half_rn(d));
+}
+
+// Load sixteen consecutive floats: elements e..e+15 of a row of k (k is a
+// multiple of 16, so a lane's sixteen are all in the row or all past it).
+// Every lane issues the same loads (a lane past the row re-reads the row's
+// first sixteen, which act_quantize replaces by zeros), so the number of
+// loads in flight is static.  `vec` (uniform: row pointers 16-byte aligned)
+// selects four 16-byte loads; rows need only be 4-byte aligned.
+__device__ inline void load16(const float* row, int e, int k, bool vec, Act16& a) {
+    const float* p = row + (e < k ? e : 0);
+    if (vec) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 f = reinterpret_cast<const float4*>(p)[i];
+            a.v[4 * i] = f.x; a.v[4 * i + 1] = f.y; a.v[4 * i + 2] = f.z; a.v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a.v[j] = p[j];
     }
 }
 
-// Load four consecutive floats of a row.  Rows handed over by the caller need
-// not be 16-byte aligned (ggml views are 4-byte aligned), so fall back to
-// scalar loads when they are not.
-__device__ inline float4 load_f4(const float* p, bool aligned16) {
-    if (aligned16) return *reinterpret_cast<const float4*>(p);
-    return make_float4(p[0], p[1], p[2], p[3]);
+// An activation batch: n_rows rows of k floats, row_stride floats apart,
+// quantised into ActLayout blocks act_stride bytes apart.  Chunk-row q (row
+// q / nch, chunk q % nch) belongs to row-slot q % nslots (a row-slot is one
+// 16-lane DPP row of the workgroup) in round q / nslots.
+struct ActBatch {
+    const float* x;
+    size_t row_stride;
+    int n_rows, k, at;
+    uint8_t* act;
+    int act_stride;
+};
+
+// Split form: the loads (act_prefetch) are issued early and the quantisation
+// (act_quantize) runs later, so the caller can issue its own long-latency
+// loads in between.  Rounds past ROUNDS fall back to load-then-quantise.
+template <int ROUNDS>
+struct ActRegs {
+    Act16 a[ROUNDS];
+};
+
+// The batch is handled by threads w0 .. blockDim.x-1 (whole 16-lane rows).
+__device__ inline bool act_vec(const ActBatch& B) {
+    return (reinterpret_cast<uintptr_t>(B.x) & 15) == 0 && (B.row_stride & 3) == 0;
 }
 
-// All threads of the workgroup: quantise the k floats at x into act.
-// Requires k % 256 == 0 for q8_K and k % 32 == 0 for q8_0.
+// every lane loads in every round (slots past the batch re-load its last
+// chunk-row and skip the quantisation)
+template <int ROUNDS>
+__device__ inline void act_prefetch(const ActBatch& B, ActRegs<ROUNDS>& R, int w0 = 0) {
+    const int slot = ((int)threadIdx.x - w0) >> 4, nslots = ((int)blockDim.x - w0) >> 4, l = threadIdx.x & 15;
+    const int nch = (B.k + 255) / 256, nq = B.n_rows * nch;
+    const bool vec = act_vec(B);
+#pragma unroll
+    for (int i = 0; i < ROUNDS; ++i) {
+        const int q = min(slot + nslots * i, nq - 1);
+        const int r = q / nch, c = q - r * nch;
+        load16(B.x + (size_t)r * B.row_stride, c * 256 + 16 * l, B.k, vec, R.a[i]);
+    }
+}
+
+__device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q) {
+    const int nch = (B.k + 255) / 256;
+    const int r = q / nch, c = q - r * nch;
+    const ActLayout L(B.k, B.at);
+    const bool in = c * 256 + 16 * (int)(threadIdx.x & 15u) < B.k;
+    Act16 a;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a.v[j] = in ? a_in.v[j] : 0.0f;
+    if (B.at == QT_Q8_K) row16_quant_q8K(a, c, B.act + r * B.act_stride, L);
+    else row16_quant_q8_0(a, c, B.act + r * B.act_stride, L);
+}
+
+template <int ROUNDS>
+__device__ inline void act_quantize(const ActBatch& B, const ActRegs<ROUNDS>& R, int w0 = 0) {
+    const int slot = ((int)threadIdx.x - w0) >> 4, nslots = ((int)blockDim.x - w0) >> 4, l = threadIdx.x & 15;
+    const int nch = (B.k + 255) / 256, nq = B.n_rows * nch;
+#pragma unroll
+    for (int i = 0; i < ROUNDS; ++i) {
+        const int q = slot + nslots * i;
+        if (q < nq) quant_chunk(B, R.a[i], q);
+    }
+    const bool vec = act_vec(B);
+    for (int q = slot + nslots * ROUNDS; q < nq; q += nslots) {
+        const int r = q / nch, c = q - r * nch;
+        Act16 a;
+        load16(B.x + (size_t)r * B.row_stride, c * 256 + 16 * l, B.k, vec, a);
+        quant_chunk(B, a, q);
+    }
+}
+
+// All threads of the workgroup: quantise one row of k floats at x into act.
 __device__ inline void wg_quantize_row(const float* __restrict__ x, int k, int at, uint8_t* act) {
-    const ActLayout L(k, at);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const bool al = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    const int nchunk = (k + 255) / 256;
-    for (int c = wave; c < nchunk; c += nwave) {
-        const int e = c * 256 + 4 * lane;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e < k) v = load_f4(x + e, al);
-        // lanes past k quantise zeros into the padding, which is never read
-        if (at == QT_Q8_K) wave_quant_chunk_q8K(v, c, act, L);
-        else wave_quant_chunk_q8_0(v, c, act, L);
-    }
+    const ActBatch B{x, 0, 1, k, at, act, 0};
+    ActRegs<1> R;
+    act_prefetch<1>(B, R);
+    act_quantize<1>(B, R);
 }
 
 }  // namespace sabah

@@ -71,21 +71,26 @@ __host__ __device__ constexpr Iq3sGrid make_iq3s_grid() {
 __constant__ Iq3sGrid kIq3sGridDev = make_iq3s_grid();
 
 // ---------------------------------------------------------------------------
-// Device-side activation row layout (scratch, never an ABI):
-//   qs   int8[kp]            kp = k rounded up to a multiple of 256
+// Device-side activation row layout (LDS scratch, never an ABI):
+//   qs   int8 chunks of 256 values, chunk c at c * kActChunkStride
 //   d    float[kp / QB]      per-block scale (q8_0: the fp16-rounded value)
 //   bsum int16[kp / 16]      q8_K only: sums of 16 consecutive qs
-// padded so every part starts 16-byte aligned; the padding quantises zeros.
+// kp = k rounded up to a multiple of 256; the padding quantises zeros.  The
+// 16-byte pad between chunks puts the chunks of one row in different LDS
+// banks, so lanes reading different chunks at the same offset do not conflict.
 // ---------------------------------------------------------------------------
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+constexpr int kActChunkStride = 272;
 
 struct ActLayout {
     int k, at;             // elements, activation type (QT_Q8_0 / QT_Q8_K)
     size_t off_d, off_bsum, bytes;
     __host__ __device__ ActLayout(int k_, int at_) : k(k_), at(at_) {
         const int qb = block_elems(at_);
-        const size_t kp = (size_t)((k_ + 255) / 256) * 256;
-        off_d = kp;
+        const size_t nchunk = (size_t)((k_ + 255) / 256);
+        const size_t kp = nchunk * 256;
+        off_d = nchunk * kActChunkStride;
         off_bsum = align16(off_d + sizeof(float) * (kp / (size_t)qb));
         bytes = align16(off_bsum + (at_ == QT_Q8_K ? sizeof(int16_t) * (kp / 16) : 0));
     }

@@ -7,6 +7,7 @@
 // table upload, copy stream or stream drain.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -50,8 +51,45 @@ struct Scratch {
     void* p = nullptr;
     size_t bytes = 0;
 };
-Scratch g_scratch_y, g_scratch_h, g_scratch_hs, g_scratch_ys;
+Scratch g_scratch_h, g_scratch_hs, g_scratch_ys;
 uint16_t* g_nearest_dev = nullptr;   // IQ3_S encoder table, uploaded on first use
+
+// Optional HIP-event timing of every kernel the library launches, by kernel
+// kind (the reference's SABAH_LLAMA_EVENTS probe, sabah_rt.cu:118-151):
+// an event pair brackets each launch on its own stream; elapsed times are
+// collected when the caller asks for them.
+enum KernelKind { KK_MMID = 0, KK_GATE_UP = 1, KK_DOWN = 2, KK_CHAIN = 3, KK_COUNT = 4 };
+struct EvPair {
+    hipEvent_t a, b;
+    int kind;
+};
+bool g_timing = false;
+std::vector<EvPair> g_ev_free, g_ev_pending;
+double g_kind_ms[KK_COUNT] = {0};
+unsigned long long g_kind_launches[KK_COUNT] = {0};
+
+struct TimedLaunch {
+    EvPair ev{};
+    bool on = false;
+    hipStream_t st;
+    TimedLaunch(int kind, hipStream_t s) : st(s) {
+        if (!g_timing) return;
+        if (g_ev_free.empty()) {
+            EvPair p{};
+            if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return;
+            g_ev_free.push_back(p);
+        }
+        ev = g_ev_free.back();
+        g_ev_free.pop_back();
+        ev.kind = kind;
+        on = hipEventRecord(ev.a, st) == hipSuccess;
+    }
+    ~TimedLaunch() {
+        if (!on) return;
+        if (hipEventRecord(ev.b, st) == hipSuccess) g_ev_pending.push_back(ev);
+        else g_ev_free.push_back(ev);
+    }
+};
 
 int fail(const char* fmt, ...) {
     va_list ap;
@@ -67,7 +105,9 @@ bool ck(hipError_t e, const char* what) {
     return false;
 }
 
-hipStream_t pick_stream(void* s) { return s ? reinterpret_cast<hipStream_t>(s) : g_stream; }
+// a stream argument is used as given: NULL is the HIP null stream, as in any
+// HIP API (the entry points without a stream argument use the library stream)
+hipStream_t pick_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     if (s.bytes >= bytes) return s.p;
@@ -84,14 +124,15 @@ void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     return s.p;
 }
 
-// tile height: ~16 KB of weights per tile, 8..64 rows, a multiple of 8 so every
-// tile of a contiguous expert matrix starts 16-byte aligned
-int pick_rows(int qt, int k) {
-    const int rb = (int)row_bytes(qt, k);
-    int R = 16384 / (rb > 0 ? rb : 1);
-    R = R < 8 ? 8 : (R > 64 ? 64 : R);
-    return R & ~7;
+constexpr int kMaxLds = 65536;
+
+// rows per workgroup (rows_per_wg); rows that are not packed are one tile
+// each, at most kMaxTiles per workgroup
+int rows_mmid(int qt, int k, bool packed) {
+    return packed ? rows_per_wg(qt, k, 1) : std::min(kMaxTiles, rows_per_wg(qt, k, 1));
 }
+int rows_gate_up(int qt, int k) { return rows_per_wg(qt, k, 2); }
+int rows_down(int qt, int k, int n_slots) { return rows_per_wg(qt, k, n_slots); }
 
 bool check_sticky() {
     if (g_err_host && __atomic_load_n(g_err_host, __ATOMIC_ACQUIRE) != 0) {
@@ -143,8 +184,10 @@ bool sync_ids_enabled() {
 
 template <int QT>
 hipError_t launch_mmid(const MmidArgs& a, hipStream_t st) {
-    const LdsPlan P = make_plan(QT, 0, a.k, a.R);
+    const Plan P = make_plan(QT, a.k, 1, a.R * contribs_per_row(QT, a.k));
+    if (P.bytes > kMaxLds) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)a.n_ids, (unsigned)a.n_tokens);
+    TimedLaunch tl(KK_MMID, st);
     hipLaunchKernelGGL(k_mmid<QT>, grid, dim3(kThreads), P.bytes, st, a);
     return hipGetLastError();
 }
@@ -159,22 +202,43 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
     return hipErrorInvalidValue;
 }
 
-template <int QTG, int QTU>
+template <int QT>
 hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
-    const LdsPlan P = make_plan(QTG, QTU, a.d_model, a.R);
+    const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * contribs_per_row(QT, a.d_model));
+    if (P.bytes > kMaxLds) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)((a.d_ff + a.R - 1) / a.R), (unsigned)a.n_slots, (unsigned)n_tokens);
-    hipLaunchKernelGGL((k_gate_up<QTG, QTU>), grid, dim3(kThreads), P.bytes, st, a);
+    TimedLaunch tl(KK_GATE_UP, st);
+    hipLaunchKernelGGL(k_gate_up<QT>, grid, dim3(kThreads), P.bytes, st, a);
     return hipGetLastError();
 }
 
-hipError_t dispatch_gate_up(int qtg, int qtu, const GateUpArgs& a, int n_tokens, hipStream_t st) {
-#define SB_GU(A, B) \
-    if (qtg == A && qtu == B) return launch_gate_up<A, B>(a, n_tokens, st);
-    SB_GU(QT_IQ3_S, QT_IQ3_S)
-    SB_GU(QT_Q4_K, QT_Q4_K)
-    SB_GU(QT_Q8_0, QT_Q8_0)
-    SB_GU(QT_Q6_K, QT_Q6_K)
-#undef SB_GU
+hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream_t st) {
+    switch (qt) {
+    case QT_Q8_0: return launch_gate_up<QT_Q8_0>(a, n_tokens, st);
+    case QT_Q4_K: return launch_gate_up<QT_Q4_K>(a, n_tokens, st);
+    case QT_Q6_K: return launch_gate_up<QT_Q6_K>(a, n_tokens, st);
+    case QT_IQ3_S: return launch_gate_up<QT_IQ3_S>(a, n_tokens, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int QT>
+hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
+    const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * contribs_per_row(QT, a.d_ff));
+    if (P.bytes > kMaxLds) return hipErrorInvalidConfiguration;
+    dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
+    TimedLaunch tl(KK_DOWN, st);
+    hipLaunchKernelGGL(k_down_combine<QT>, grid, dim3(kThreads), P.bytes, st, a);
+    return hipGetLastError();
+}
+
+hipError_t dispatch_down(int qt, const DownArgs& a, int n_tokens, hipStream_t st) {
+    switch (qt) {
+    case QT_Q8_0: return launch_down<QT_Q8_0>(a, n_tokens, st);
+    case QT_Q4_K: return launch_down<QT_Q4_K>(a, n_tokens, st);
+    case QT_Q6_K: return launch_down<QT_Q6_K>(a, n_tokens, st);
+    case QT_IQ3_S: return launch_down<QT_IQ3_S>(a, n_tokens, st);
+    }
     return hipErrorInvalidValue;
 }
 
@@ -227,7 +291,7 @@ SABAH_API int sabah_rt_init(int device) {
 SABAH_API int sabah_rt_shutdown(void) {
     if (g_device < 0) return 0;
     if (g_stream) (void)hipStreamSynchronize(g_stream);
-    for (Scratch* s : {&g_scratch_y, &g_scratch_h, &g_scratch_hs, &g_scratch_ys}) {
+    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->bytes = 0;
@@ -255,6 +319,37 @@ SABAH_API int sabah_sync_compute(void) {
 }
 
 SABAH_API int sabah_rt_check_errors(void) { return check_sticky() ? 0 : -1; }
+
+SABAH_API int sabah_rt_set_kernel_timing(int on) {
+    g_timing = on != 0;
+    return 0;
+}
+
+// Accumulated kernel time (ms) and launch count of one kernel kind
+// (0 MUL_MAT_ID, 1 gate/up, 2 down+combine, 3 decode chain); waits for the
+// launches still in flight.  reset != 0 clears the totals after reading.
+SABAH_API int sabah_rt_get_kernel_timing(int kind, double* total_ms, unsigned long long* launches, int reset) {
+    if (kind < 0 || kind >= KK_COUNT) return fail("unknown kernel kind %d", kind);
+    for (EvPair& p : g_ev_pending) {
+        float ms = 0.0f;
+        if (!ck(hipEventSynchronize(p.b), "timing event sync")) return -1;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            g_kind_ms[p.kind] += ms;
+            g_kind_launches[p.kind] += 1;
+        }
+        g_ev_free.push_back(p);
+    }
+    g_ev_pending.clear();
+    if (total_ms) *total_ms = g_kind_ms[kind];
+    if (launches) *launches = g_kind_launches[kind];
+    if (reset) {
+        for (int i = 0; i < KK_COUNT; ++i) {
+            g_kind_ms[i] = 0;
+            g_kind_launches[i] = 0;
+        }
+    }
+    return 0;
+}
 
 // ===========================================================================
 // bank registry
@@ -347,7 +442,7 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
     a.dst_token_stride = dst_token_stride;
     a.rows = rows;
     a.k = k;
-    a.R = pick_rows(qt, k);
+    a.R = rows_mmid(qt, k, row_stride == sabah_row_bytes(qt, k));
     a.err = g_err_dev;
     if (!ck(dispatch_mmid(qt, a, st), "MUL_MAT_ID launch")) return -1;
     ++g_calls;
@@ -413,15 +508,15 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
         return fail("dequant: unsupported type %d or row of %d elements", qt, row_elems);
     if (g_device < 0) return fail("sabah_rt_init has not been called");
     if (n_rows == 0) return 0;
-    const int R = pick_rows(qt, row_elems);
-    const LdsPlan P = make_plan(qt, 0, row_elems, R);
-    dim3 grid((unsigned)((n_rows + R - 1) / R));
+    const long long nunits = (long long)n_rows * units_per_row(qt, row_elems);
+    dim3 grid((unsigned)((nunits + kThreads - 1) / kThreads));
+    const size_t lds = qt == QT_IQ3_S ? kLdsTables : 0;
     const uint8_t* s = reinterpret_cast<const uint8_t*>(d_src);
     switch (qt) {
-    case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, dim3(kThreads), P.bytes, g_stream, s, d_dst, n_rows, row_elems, R); break;
-    case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, dim3(kThreads), P.bytes, g_stream, s, d_dst, n_rows, row_elems, R); break;
-    case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, dim3(kThreads), P.bytes, g_stream, s, d_dst, n_rows, row_elems, R); break;
-    case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, dim3(kThreads), P.bytes, g_stream, s, d_dst, n_rows, row_elems, R); break;
+    case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     }
     if (!ck(hipGetLastError(), "dequant launch")) return -1;
     return ck(hipStreamSynchronize(g_stream), "dequant sync") ? 0 : -1;
@@ -439,36 +534,26 @@ SABAH_API int sabah_quantize_act(const float* d_x, void* d_y, int qt, int n_rows
     return ck(hipGetLastError(), "quantize launch") ? 0 : -1;
 }
 
-// one layer on `st`: gate/up (+SwiGLU) -> h, down -> y, combine -> out
-static int run_layer(const GateUpArgs& gu, int qtg, int qtu, int qtd, const ExpertSrc& D, const Routing& rt,
-                     int n_slots, int d_model, int d_ff, int n_tokens, const float* w, const float* shared,
-                     const float* resid, float* out, int accumulate, float* y, hipStream_t st) {
-    if (!ck(dispatch_gate_up(qtg, qtu, gu, n_tokens, st), "gate/up launch")) return -1;
-    MmidArgs a{};
-    a.W = D;
+// one layer on `st`: gate/up (+SwiGLU) -> h, then down + routed combine -> out
+static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D, const Routing& rt, int n_slots,
+                     int d_model, int d_ff, int n_tokens, const float* w, const float* shared, const float* resid,
+                     float* out, int accumulate, hipStream_t st) {
+    if (!ck(dispatch_gate_up(qtg, gu, n_tokens, st), "gate/up launch")) return -1;
+    DownArgs a{};
+    a.D = D;
     a.rt = rt;
-    a.row_stride = row_bytes(qtd, d_ff);
-    a.x = reinterpret_cast<const uint8_t*>(gu.h);
-    a.x_id_stride = (size_t)d_ff * 4;
-    a.x_token_stride = (size_t)n_slots * d_ff * 4;
-    a.x_rows = n_slots;
-    a.n_ids = n_slots;
-    a.n_tokens = n_tokens;
-    a.dst = reinterpret_cast<uint8_t*>(y);
-    a.dst_id_stride = (size_t)d_model * 4;
-    a.dst_token_stride = (size_t)n_slots * d_model * 4;
-    a.rows = d_model;
-    a.k = d_ff;
-    a.R = pick_rows(qtd, d_ff);
+    a.h = gu.h;
+    a.w = w;
+    a.shared = shared;
+    a.resid = resid;
+    a.out = out;
+    a.n_slots = n_slots;
+    a.d_model = d_model;
+    a.d_ff = d_ff;
+    a.R = rows_down(qtd, d_ff, n_slots);
+    a.accumulate = accumulate;
     a.err = g_err_dev;
-    if (!ck(dispatch_mmid(qtd, a, st), "down launch")) return -1;
-    if (w) {
-        dim3 grid((unsigned)((d_model + 255) / 256), (unsigned)n_tokens);
-        hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, st, y, w, shared, resid, out, n_slots, d_model, n_tokens,
-                           accumulate);
-        if (!ck(hipGetLastError(), "combine launch")) return -1;
-    }
-    return 0;
+    return ck(dispatch_down(qtd, a, n_tokens, st), "down/combine launch") ? 0 : -1;
 }
 
 static bool layer_types_ok(int qtg, int qtu, int qtd, int d_model, int d_ff) {
@@ -480,12 +565,11 @@ static bool layer_types_ok(int qtg, int qtu, int qtd, int d_model, int d_ff) {
 SABAH_API int sabah_moe_block(const float* d_x, float* d_out, float* d_h, const void* const* d_ptrs, const float* d_w,
                               int d_model, int ff, int n_used, int qt_gate, int qt_up, int qt_down, int accumulate) {
     if (!d_x || !d_out || !d_h || !d_ptrs || !d_w || n_used <= 0) return fail("invalid moe_block arguments");
+    if (n_used > kMaxTiles) return fail("n_used %d exceeds the supported maximum %d", n_used, kMaxTiles);
     if ((d_model % 32) || (ff % 32)) return fail("d_model and ff must be multiples of 32");
     if (!layer_types_ok(qt_gate, qt_up, qt_down, d_model, ff))
         return fail("moe_block: unsupported type mix gate=%d up=%d down=%d", qt_gate, qt_up, qt_down);
     if (g_device < 0) return fail("sabah_rt_init has not been called");
-    float* y = static_cast<float*>(scratch(g_scratch_y, sizeof(float) * (size_t)n_used * d_model, g_stream));
-    if (!y) return -1;
     GateUpArgs gu{};
     gu.G = {nullptr, d_ptrs, 0};
     gu.U = {nullptr, d_ptrs + n_used, 0};
@@ -495,12 +579,12 @@ SABAH_API int sabah_moe_block(const float* d_x, float* d_out, float* d_h, const 
     gu.n_slots = n_used;
     gu.d_model = d_model;
     gu.d_ff = ff;
-    gu.R = pick_rows(qt_gate, d_model);
+    gu.R = rows_gate_up(qt_gate, d_model);
     gu.err = g_err_dev;
     const ExpertSrc D{nullptr, d_ptrs + 2 * n_used, 0};
     ++g_layer_calls;
-    return run_layer(gu, qt_gate, qt_up, qt_down, D, gu.rt, n_used, d_model, ff, 1, d_w, nullptr, nullptr, d_out,
-                     accumulate, y, g_stream);
+    return run_layer(gu, qt_gate, qt_down, D, gu.rt, n_used, d_model, ff, 1, d_w, nullptr, nullptr, d_out, accumulate,
+                     g_stream);
 }
 
 static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const int32_t* d_ids, const float* d_w,
@@ -508,6 +592,7 @@ static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const i
     const int D = L->d_model, F = L->d_ff;
     const float* shared = nullptr;
     if (L->shared_gate) {
+        // dense shared expert: gate/up + SwiGLU -> hs, down -> ys (added by the routed combine)
         const int Fs = L->d_ff_shared;
         float* hs = static_cast<float*>(scratch(g_scratch_hs, sizeof(float) * (size_t)n_tokens * Fs, st));
         float* ys = static_cast<float*>(scratch(g_scratch_ys, sizeof(float) * (size_t)n_tokens * D, st));
@@ -521,17 +606,31 @@ static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const i
         gs.n_slots = 1;
         gs.d_model = D;
         gs.d_ff = Fs;
-        gs.R = pick_rows(L->qt_shared_gate, D);
+        gs.R = rows_gate_up(L->qt_shared_gate, D);
         gs.err = g_err_dev;
-        const ExpertSrc SD{reinterpret_cast<const uint8_t*>(L->shared_down), nullptr, 0};
-        if (run_layer(gs, L->qt_shared_gate, L->qt_shared_up, L->qt_shared_down, SD, gs.rt, 1, D, Fs, n_tokens,
-                      nullptr, nullptr, nullptr, nullptr, 0, ys, st))
-            return -1;
+        if (!ck(dispatch_gate_up(L->qt_shared_gate, gs, n_tokens, st), "shared gate/up launch")) return -1;
+        MmidArgs a{};
+        a.W = {reinterpret_cast<const uint8_t*>(L->shared_down), nullptr, 0};
+        a.rt = {nullptr, 0, 0, 1};
+        a.row_stride = row_bytes(L->qt_shared_down, Fs);
+        a.x = reinterpret_cast<const uint8_t*>(hs);
+        a.x_id_stride = (size_t)Fs * 4;
+        a.x_token_stride = (size_t)Fs * 4;
+        a.x_rows = 1;
+        a.n_ids = 1;
+        a.n_tokens = n_tokens;
+        a.dst = reinterpret_cast<uint8_t*>(ys);
+        a.dst_id_stride = (size_t)D * 4;
+        a.dst_token_stride = (size_t)D * 4;
+        a.rows = D;
+        a.k = Fs;
+        a.R = rows_mmid(L->qt_shared_down, Fs, true);
+        a.err = g_err_dev;
+        if (!ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch")) return -1;
         shared = ys;
     }
     float* h = static_cast<float*>(scratch(g_scratch_h, sizeof(float) * (size_t)n_tokens * n_used * F, st));
-    float* y = static_cast<float*>(scratch(g_scratch_y, sizeof(float) * (size_t)n_tokens * n_used * D, st));
-    if (!h || !y) return -1;
+    if (!h) return -1;
     const Routing rt{reinterpret_cast<const uint8_t*>(d_ids), 4, (size_t)n_used * 4, L->n_experts};
     GateUpArgs gu{};
     gu.G = {reinterpret_cast<const uint8_t*>(L->gate), nullptr, row_bytes(L->qt_gate, D) * (size_t)F};
@@ -542,11 +641,10 @@ static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const i
     gu.n_slots = n_used;
     gu.d_model = D;
     gu.d_ff = F;
-    gu.R = pick_rows(L->qt_gate, D);
+    gu.R = rows_gate_up(L->qt_gate, D);
     gu.err = g_err_dev;
     const ExpertSrc DS{reinterpret_cast<const uint8_t*>(L->down), nullptr, row_bytes(L->qt_down, F) * (size_t)D};
-    return run_layer(gu, L->qt_gate, L->qt_up, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, shared, d_resid,
-                     d_out, 0, y, st);
+    return run_layer(gu, L->qt_gate, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, shared, d_resid, d_out, 0, st);
 }
 
 static int check_layer_desc(const sabah_moe_layer_desc* L) {
@@ -567,6 +665,7 @@ SABAH_API int sabah_moe_layer(const sabah_moe_layer_desc* layer, const float* d_
                               void* stream) {
     if (check_layer_desc(layer)) return -1;
     if (!d_x || !d_ids || !d_w || !d_out || n_used <= 0 || n_tokens < 0) return fail("invalid MoE layer arguments");
+    if (n_used > kMaxTiles) return fail("n_used %d exceeds the supported maximum %d", n_used, kMaxTiles);
     if (g_device < 0) return fail("sabah_rt_init has not been called");
     if (!check_sticky()) return -1;
     if (n_tokens == 0) return 0;
@@ -579,6 +678,7 @@ SABAH_API int sabah_moe_chain(const sabah_moe_layer_desc* layers, int n_layers, 
                               const float* d_w, int n_used, int n_tokens, void* stream) {
     if (!layers || n_layers <= 0 || !d_x || !d_ids || !d_w || n_used <= 0 || n_tokens < 0)
         return fail("invalid MoE chain arguments");
+    if (n_used > kMaxTiles) return fail("n_used %d exceeds the supported maximum %d", n_used, kMaxTiles);
     for (int l = 0; l < n_layers; ++l)
         if (check_layer_desc(layers + l)) return -1;
     if (g_device < 0) return fail("sabah_rt_init has not been called");

@@ -1,0 +1,407 @@
+// Register-resident decoding of quantised weights, one "unit" per lane.
+//
+// A unit is one 256-element super-block (Q4_K 144 B, Q6_K 210 B, IQ3_S 110 B)
+// or four 32-element Q8_0 blocks (136 B).  Each lane loads its unit straight
+// from HBM into VGPRs with 8-byte loads that cover exactly the unit's 8-byte
+// granules (so a load never touches a page the unit does not), then
+// re-aligns the bytes so that every field of the format sits at a static
+// dword index, and decodes with integer dot products against the unit's 256
+// q8 activations held in LDS.
+//
+// Field origin: all fields used in the inner loops start at the same residue
+// mod 4 inside the block (IQ3_S: byte 2; Q8_0 even blocks: byte 2; Q4_K and
+// Q6_K: byte 0).  F[i] is the dword at (unit start + ORG + 4 i); Fm1 is the
+// dword before it (IQ3_S reads its fp16 d there).
+//
+// Block layouts: sabah_rt.cu:2462-2485 (Q4_K), 2537-2545 (Q8_0), 2618-2647
+// (IQ3_S); gguf-py quants.py:586-606 (Q6_K: ql[128] qh[64] int8 sc[16] d).
+#pragma once
+#include "quant_formats.h"
+
+namespace sabah {
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Weight loads are plain cached loads: the eight lanes that share a weight row
+// read overlapping cache lines across several load instructions, and L1/L2
+// must absorb those repeats.  SABAH_STREAM_LOADS=1 selects non-temporal loads.
+#ifndef SABAH_STREAM_LOADS
+#define SABAH_STREAM_LOADS 0
+#endif
+template <typename T>
+__device__ inline T weight_load(const T* p) {
+#if SABAH_STREAM_LOADS
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+template <int QT> struct UnitFmt;
+template <> struct UnitFmt<QT_IQ3_S> { static constexpr int BYTES = 110, ELEMS = 256, ORG = 2, NF = 27, CONTRIB = 1; };
+template <> struct UnitFmt<QT_Q4_K> { static constexpr int BYTES = 144, ELEMS = 256, ORG = 0, NF = 36, CONTRIB = 1; };
+template <> struct UnitFmt<QT_Q6_K> { static constexpr int BYTES = 210, ELEMS = 256, ORG = 0, NF = 53, CONTRIB = 1; };
+template <> struct UnitFmt<QT_Q8_0> { static constexpr int BYTES = 136, ELEMS = 128, ORG = 2, NF = 34, CONTRIB = 4; };
+
+// Window: the unit's granules, loaded from base = (origin - 4) rounded down to
+// 8 bytes; the origin then sits at byte p in [4, 11] of the window.
+template <int QT>
+struct UnitWindow {
+    static constexpr int ORG = UnitFmt<QT>::ORG;
+    static constexpr int NF = UnitFmt<QT>::NF;
+    static constexpr int NG = (11 + UnitFmt<QT>::BYTES - ORG + 7) / 8;   // granules, worst case
+    static constexpr int NW = 2 * NG + 2;                                 // dwords incl. zero tail
+    uint32_t W[NW];
+    int p;
+
+    // Every load is issued unconditionally (so the compiler can count them
+    // when it waits for older loads); a first or last granule that holds no
+    // byte of the unit is replaced by a neighbour that does, whose bytes are
+    // never read.  Only granules holding unit bytes are read, so no load
+    // touches a page the unit does not.
+    // len: bytes of this unit (smaller than BYTES only for the last Q8_0 unit
+    // of a row that is not a whole number of 4-block units)
+    __device__ inline void load(const uint8_t* unit, int len = UnitFmt<QT>::BYTES) {
+        const uint8_t* o = unit + ORG;
+        const int mis = (int)((reinterpret_cast<uintptr_t>(o) - 4) & 7);
+        p = 4 + mis;
+        const uint8_t* base = o - p;                            // 8-byte aligned
+        const int first = (p - ORG < 8) ? 0 : 1;                // first granule holding unit bytes
+        const int lim = len - ORG + p;                          // window offset one past the unit
+        const int last = min(NG - 1, (lim - 1) >> 3);           // last granule holding unit bytes
+        typedef __attribute__((address_space(1))) const u32x2 gu32x2;
+        gu32x2* g = (gu32x2*)base;
+        u32x2 v = weight_load(g + first);
+        W[0] = v.x;
+        W[1] = v.y;
+#pragma unroll
+        for (int i = 1; i < NG - 1; ++i) {
+            v = weight_load(g + i);
+            W[2 * i] = v.x;
+            W[2 * i + 1] = v.y;
+        }
+        v = weight_load(g + last);
+        W[2 * (NG - 1)] = v.x;
+        W[2 * (NG - 1) + 1] = v.y;
+        W[NW - 2] = W[NW - 1] = 0u;
+    }
+
+    // The same window read from a tile staged in LDS (the staging area has a
+    // 16-byte guard on both sides, so no bound checks are needed).
+    __device__ inline void load_lds(const uint8_t* unit_lds) {
+        const uint8_t* o = unit_lds + ORG;
+        const int mis = (int)((reinterpret_cast<uintptr_t>(o) - 4) & 7);
+        p = 4 + mis;
+        const u32x2* g = reinterpret_cast<const u32x2*>(o - p);
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            const u32x2 v = g[i];
+            W[2 * i] = v.x;
+            W[2 * i + 1] = v.y;
+        }
+        W[NW - 2] = W[NW - 1] = 0u;
+    }
+
+    // F[-1 .. NF-1] at static indices: select the dword shift (p >= 8), then the
+    // byte shift (p & 3 in {0, 2})
+    __device__ inline void fields(uint32_t (&F)[NF], uint32_t& Fm1) const {
+        const bool hi = p >= 8;
+        const uint32_t sh = (uint32_t)(p & 3);
+        uint32_t V[NF + 2];
+#pragma unroll
+        for (int i = 0; i < NF + 2; ++i) V[i] = hi ? W[i + 1] : W[i];
+        // origin dword index inside V is 1 (p in [4, 7]) / 2 (p in [8, 11]) -> 1 after the select
+        Fm1 = __builtin_amdgcn_alignbyte(V[1], V[0], sh);
+#pragma unroll
+        for (int i = 0; i < NF; ++i) F[i] = __builtin_amdgcn_alignbyte(V[i + 2], V[i + 1], sh);
+    }
+};
+
+__device__ inline float h2f(uint32_t bits16) { return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xFFFFu))); }
+
+__device__ inline int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+// ---------------------------------------------------------------------------
+// LDS tables for IQ3_S
+//   grid  512 x u32 at LDS byte 0     (expanded codebook)
+//   sgn   256 x u32x4 at LDS byte 2048: for sign byte b, {m(lo), t(lo), m(hi), t(hi)}
+//         with t(n) = nibble bits spread to bytes (0x01), m(n) = t * 0xFF, so
+//         (mag ^ m) + t negates exactly the bytes whose sign bit is set
+// ---------------------------------------------------------------------------
+constexpr int kLdsGrid = 0;
+constexpr int kLdsSign = 2048;
+constexpr int kLdsTables = 2048 + 4096;
+
+__device__ inline uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
+
+// The IQ3_S tables in LDS, built by NT threads (w = 0 .. NT-1 of them):
+// the 512-entry codebook (loaded early into registers, written later) and
+// the 256-entry sign table (computed).
+template <int NT>
+struct GridRegs {
+    uint32_t e[512 / NT];
+};
+template <int NT>
+__device__ inline GridRegs<NT> load_grid_regs(int w) {
+    GridRegs<NT> g;
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) g.e[i] = kIq3sGridDev.e[w + NT * i];
+    return g;
+}
+template <int NT>
+__device__ inline void store_iq3s_tables(uint8_t* smem, const GridRegs<NT>& g, int w) {
+    uint32_t* grid = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
+    uint4* sgn = reinterpret_cast<uint4*>(smem + kLdsSign);
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) grid[w + NT * i] = g.e[i];
+#pragma unroll
+    for (int i = 0; i < 256 / NT; ++i) {
+        const uint32_t b = (uint32_t)(w + NT * i);
+        const uint32_t tl = spread4(b & 15u), th = spread4(b >> 4);
+        sgn[b] = make_uint4(tl * 0xFFu, tl, th * 0xFFu, th);
+    }
+}
+// all 256 threads of the workgroup
+__device__ inline void stage_iq3s_tables(uint8_t* smem) {
+    store_iq3s_tables<256>(smem, load_grid_regs<256>((int)threadIdx.x), (int)threadIdx.x);
+}
+
+__device__ inline uint32_t lds_u32(const uint8_t* smem, uint32_t byte_off) {
+    return *reinterpret_cast<const uint32_t*>(smem + byte_off);
+}
+
+// 32 activation bytes of item j of a 256-element chunk (8 dwords)
+__device__ inline void act8(const uint8_t* chunk, int j, uint32_t (&A)[8]) {
+    const uint4 a0 = reinterpret_cast<const uint4*>(chunk)[2 * j];
+    const uint4 a1 = reinterpret_cast<const uint4*>(chunk)[2 * j + 1];
+    A[0] = a0.x; A[1] = a0.y; A[2] = a0.z; A[3] = a0.w;
+    A[4] = a1.x; A[5] = a1.y; A[6] = a1.z; A[7] = a1.w;
+}
+
+// ---------------------------------------------------------------------------
+// IQ3_S: element 32*ib + 4*g + j = ls(ib) * grid[qs[8ib+g] | bit g of qh[ib] << 8][j]
+//        * (-1 if bit (4*(g&1)+j) of signs[4ib + g/2]); ls = 2*scale_nibble + 1.
+// F[0..15] qs, F[16..17] qh, F[18..25] signs, F[26] scales, Fm1 >> 16 = d.
+// ---------------------------------------------------------------------------
+// packed int8 weights of item ib (8 dwords) and its scale
+__device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* smem, uint32_t (&v)[8]) {
+    const uint32_t qh = (F[16 + (ib >> 2)] >> (8 * (ib & 3))) & 0xFFu;
+    const uint32_t T0 = spread4(qh & 15u), T1 = spread4(qh >> 4);
+    const uint32_t S = F[18 + ib];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t Q = F[2 * ib + (l >> 1)];
+        const uint32_t T = (l >> 1) ? T1 : T0;
+        const uint32_t pp = 2u * (uint32_t)(l & 1);
+        // bytes [qs_g, qhbit_g, qs_g+1, qhbit_g+1] -> two 9-bit codebook indices, x4 -> byte offsets
+        const uint32_t sel = (4u + pp) | (pp << 8) | ((5u + pp) << 16) | ((pp + 1u) << 24);
+        const uint32_t D = __builtin_amdgcn_perm(Q, T, sel) << 2;
+        const uint32_t g0 = lds_u32(smem, kLdsGrid + (D & 0xFFFFu));
+        const uint32_t g1 = lds_u32(smem, kLdsGrid + (D >> 16));
+        const uint4 sm = *reinterpret_cast<const uint4*>(smem + kLdsSign + 16u * ((S >> (8 * l)) & 0xFFu));
+        v[2 * l] = (g0 ^ sm.x) + sm.y;
+        v[2 * l + 1] = (g1 ^ sm.z) + sm.w;
+    }
+    return 2 * (int)((F[26] >> (4 * ib)) & 15u) + 1;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K: element 32j + l = d*sc_j*nib - dmin*m_j, nibble low (j even) / high (j
+// odd) of qs[32*(j/2) + l].  F[0] = d | dmin << 16, F[1..3] packed 6-bit
+// scales/mins (get_scale_min_k4), F[4..35] qs.
+// ---------------------------------------------------------------------------
+__device__ inline uint32_t byte_of(const uint32_t* F, int b) { return (F[b >> 2] >> (8 * (b & 3))) & 0xFFu; }
+
+__device__ inline void q4k_scale_min(const uint32_t (&F)[36], int j, int& sc, int& mn) {
+    const uint32_t* q = F + 1;      // the 12 scale bytes
+    if (j < 4) {
+        sc = (int)(byte_of(q, j) & 63u);
+        mn = (int)(byte_of(q, j + 4) & 63u);
+    } else {
+        sc = (int)((byte_of(q, j + 4) & 0xFu) | ((byte_of(q, j - 4) >> 6) << 4));
+        mn = (int)((byte_of(q, j + 4) >> 4) | ((byte_of(q, j) >> 6) << 4));
+    }
+}
+
+__device__ inline void q4k_item(const uint32_t (&F)[36], int j, uint32_t (&v)[8]) {
+    const int sh = 4 * (j & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (F[4 + 8 * (j >> 1) + i] >> sh) & 0x0F0F0F0Fu;
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K: item j (elements 32j..32j+31) = half h = j/4, quarter q = j%4: low 4 bits
+// from ql[64h + 32(q&1) + l] (nibble q>>1), high 2 bits from qh[32h + l] bits 2q..;
+// value (q6 - 32) * d * sc[16-element half].  F[0..31] ql, F[32..47] qh,
+// F[48..51] int8 scales, F[52] & 0xFFFF = d.
+// ---------------------------------------------------------------------------
+__device__ inline void q6k_item(const uint32_t (&F)[53], int j, uint32_t (&v)[8]) {
+    const int h = j >> 2, q = j & 3;
+    const int nsh = 4 * (q >> 1), hsh = 2 * q;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        v[i] = ((F[16 * h + 8 * (q & 1) + i] >> nsh) & 0x0F0F0F0Fu) | (((F[32 + 8 * h + i] >> hsh) & 0x03030303u) << 4);
+}
+__device__ inline int q6k_scale(const uint32_t (&F)[53], int s16) {
+    return (int)(int8_t)((F[48 + (s16 >> 2)] >> (8 * (s16 & 3))) & 0xFFu);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 unit = 4 blocks of 34 B; block j at unit byte 34j: d at 34j, qs at 34j+2.
+// With the field origin at unit byte 2, block j's d is at F-byte 34j-2 and its
+// qs at F-byte 34j (dword aligned for even j, 2 past a dword for odd j).
+// ---------------------------------------------------------------------------
+template <int J>
+__device__ inline void q8_0_block(const uint32_t (&F)[34], uint32_t Fm1, uint32_t (&v)[8], uint32_t& dbits) {
+    constexpr int qo = 34 * J;               // F-byte of the qs
+    if constexpr ((qo & 3) == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = F[qo / 4 + i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_alignbyte(F[qo / 4 + i + 1], F[qo / 4 + i], 2);
+    }
+    constexpr int dob = qo - 2;              // F-byte of d (even)
+    if constexpr (dob < 0) dbits = Fm1 >> 16;
+    else if constexpr ((dob & 3) == 0) dbits = F[dob / 4] & 0xFFFFu;
+    else dbits = F[dob / 4] >> 16;
+}
+
+// ---------------------------------------------------------------------------
+// unit dot: contribution(s) of one unit to its row, ggml's float order per
+// block: (d_w * d_x) * isum  [Q4_K: minus (dmin_w * d_x) * msum]
+//   chunk: LDS activation bytes of the unit's 256-element chunk
+//   dx   : activation scale(s) of the unit's block(s); bs: its q8_K bsums
+// ---------------------------------------------------------------------------
+template <int QT>
+struct UnitDot {
+    float c[UnitFmt<QT>::CONTRIB];
+};
+
+template <int QT>
+__device__ inline UnitDot<QT> unit_dot(const UnitWindow<QT>& Wn, const uint8_t* smem, const uint8_t* chunk,
+                                       const float* dx, const int16_t* bs) {
+    uint32_t F[UnitFmt<QT>::NF];
+    uint32_t Fm1;
+    Wn.fields(F, Fm1);
+    UnitDot<QT> r;
+    if constexpr (QT == QT_IQ3_S) {
+        int bsum = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t v[8], A[8];
+            const int ls = iq3s_item(F, ib, smem, v);
+            act8(chunk, ib, A);
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
+            bsum += ls * s;
+        }
+        r.c[0] = __fmul_rn(__fmul_rn(h2f(Fm1 >> 16), dx[0]), (float)bsum);
+    } else if constexpr (QT == QT_Q4_K) {
+        int isum = 0, msum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[8], A[8];
+            q4k_item(F, j, v);
+            act8(chunk, j, A);
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
+            int sc, mn;
+            q4k_scale_min(F, j, sc, mn);
+            isum += sc * s;
+            msum += mn * ((int)bs[2 * j] + (int)bs[2 * j + 1]);
+        }
+        const float d = h2f(F[0]), dmin = h2f(F[0] >> 16);
+        r.c[0] = __fsub_rn(__fmul_rn(__fmul_rn(d, dx[0]), (float)isum), __fmul_rn(__fmul_rn(dmin, dx[0]), (float)msum));
+    } else if constexpr (QT == QT_Q6_K) {
+        int isum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[8], A[8];
+            q6k_item(F, j, v);
+            act8(chunk, j, A);
+            int sa = 0, sb = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sa = sdot4(v[i], A[i], sa);
+#pragma unroll
+            for (int i = 4; i < 8; ++i) sb = sdot4(v[i], A[i], sb);
+            // sum (q - 32) * q8 = sum q * q8 - 32 * bsum over each 16-element half
+            sa -= 32 * (int)bs[2 * j];
+            sb -= 32 * (int)bs[2 * j + 1];
+            isum += q6k_scale(F, 2 * j) * sa + q6k_scale(F, 2 * j + 1) * sb;
+        }
+        r.c[0] = __fmul_rn(__fmul_rn(h2f(F[52]), dx[0]), (float)isum);
+    } else {   // Q8_0: four independent blocks
+        uint32_t v[8], A[8], db;
+#define SB_Q8_BLOCK(J)                                                              \
+        {                                                                           \
+            q8_0_block<J>(F, Fm1, v, db);                                           \
+            act8(chunk, J, A);                                                      \
+            int s = 0;                                                              \
+            _Pragma("unroll") for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s); \
+            r.c[J] = __fmul_rn((float)s, __fmul_rn(h2f(db), dx[J]));                \
+        }
+        SB_Q8_BLOCK(0) SB_Q8_BLOCK(1) SB_Q8_BLOCK(2) SB_Q8_BLOCK(3)
+#undef SB_Q8_BLOCK
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// dequantised values of a unit, ggml dequantize_row_* float order, through the
+// same field extraction and item decoders as unit_dot
+// ---------------------------------------------------------------------------
+// n: elements of the unit to write (a row's last Q8_0 unit may be partial)
+template <int QT>
+__device__ inline void unit_dequant(const UnitWindow<QT>& Wn, const uint8_t* smem, float* out, int n) {
+    uint32_t F[UnitFmt<QT>::NF];
+    uint32_t Fm1;
+    Wn.fields(F, Fm1);
+    if constexpr (QT == QT_IQ3_S) {
+        const float d = h2f(Fm1 >> 16);
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t v[8];
+            const int ls = iq3s_item(F, ib, smem, v);
+            const float db = __fmul_rn(d, (float)ls);           // d * (1 + 2*scale)
+            for (int e = 0; e < 32; ++e)
+                out[32 * ib + e] = __fmul_rn(db, (float)(int8_t)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu));
+        }
+    } else if constexpr (QT == QT_Q4_K) {
+        const float d = h2f(F[0]), dmin = h2f(F[0] >> 16);
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[8];
+            q4k_item(F, j, v);
+            int sc, mn;
+            q4k_scale_min(F, j, sc, mn);
+            const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+            for (int e = 0; e < 32; ++e)
+                out[32 * j + e] = __fsub_rn(__fmul_rn(d1, (float)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu)), m1);
+        }
+    } else if constexpr (QT == QT_Q6_K) {
+        const float d = h2f(F[52]);
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[8];
+            q6k_item(F, j, v);
+            for (int e = 0; e < 32; ++e) {
+                const int q = (int)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu) - 32;
+                out[32 * j + e] = __fmul_rn(__fmul_rn(d, (float)q6k_scale(F, 2 * j + (e >> 4))), (float)q);
+            }
+        }
+    } else {
+        uint32_t v[8], db;
+#define SB_Q8_DEQ(J)                                                                                       \
+        {                                                                                                  \
+            q8_0_block<J>(F, Fm1, v, db);                                                                  \
+            const float d = h2f(db);                                                                       \
+            if (32 * J < n)                                                                                \
+                for (int e = 0; e < 32; ++e)                                                               \
+                    out[32 * J + e] = __fmul_rn((float)(int8_t)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu), d); \
+        }
+        SB_Q8_DEQ(0) SB_Q8_DEQ(1) SB_Q8_DEQ(2) SB_Q8_DEQ(3)
+#undef SB_Q8_DEQ
+    }
+}
+
+}  // namespace sabah

@@ -46,7 +46,8 @@ def zipf_bias(rng: np.random.Generator, n_experts: int, s: float = ZIPF_S, tau: 
 def zipf_routing(rng: np.random.Generator, n_tokens: int, n_experts: int, k: int,
                  n_layers: int | None = None) -> tuple[np.ndarray, np.ndarray]:
     """Top-k of N(0,1) + Zipf-bias logits.  With n_layers, each layer has its
-    own popularity ranking; shapes [n_layers, n_tokens, k] (else [n_tokens, k])."""
+    own popularity ranking, shared by all n_tokens tokens; shapes
+    [n_layers, n_tokens, k] (else [n_tokens, k])."""
     layers = 1 if n_layers is None else n_layers
     ids = np.empty((layers, n_tokens, k), np.int32)
     w = np.empty((layers, n_tokens, k), np.float32)

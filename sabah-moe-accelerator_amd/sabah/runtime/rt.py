@@ -86,7 +86,19 @@ EXTRA_SIGNATURES = {
     "sabah_sync_all": ([], c_i),
     "sabah_sync_compute": ([], c_i),
     "sabah_synth_weights": ([c_vp, c_i, ctypes.c_longlong, c_i, ctypes.c_ulonglong, ctypes.c_float, c_vp], c_i),
+    "sabah_rt_set_kernel_timing": ([c_i], c_i),
+    "sabah_rt_get_kernel_timing": ([c_i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_u64), c_i], c_i),
 }
+
+KERNEL_KINDS = {"mmid": 0, "gate_up": 1, "down": 2, "chain": 3}
+
+
+def kernel_timing(kind: str, reset: bool = False) -> tuple[float, int]:
+    """(total ms, launches) of one kernel kind since timing was switched on."""
+    ms, n = ctypes.c_double(), c_u64()
+    check(lib().sabah_rt_get_kernel_timing(KERNEL_KINDS[kind], ctypes.byref(ms), ctypes.byref(n), int(reset)),
+          "kernel timing")
+    return ms.value, n.value
 
 
 def lib():

@@ -70,7 +70,7 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
     assert np.array_equal(y.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768)])
+@pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768)])
 def test_dequant_is_bit_exact(hip_rt, orc, qt, k):
     rng = np.random.default_rng(qt * 7 + k)
     raw = random_blocks(rng, qt, 37, k)
@@ -94,7 +94,7 @@ def v2(hip_rt, src, expert_stride, row_bytes, x, ids, out, rows, k, E, qt):
         vp(out), out.stride(1) * 4, out.stride(0) * 4, rows, k, E, qt, stream(), None)
 
 
-CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q4_K, 2048, 48), (Q4_K, 768, 64),
+CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), (Q4_K, 768, 64),
          (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104)]
 
 
