@@ -6,6 +6,7 @@
 // in HBM, the ids are read by the kernel itself, and there is no pointer
 // table upload, copy stream or stream drain.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <atomic>
@@ -55,9 +56,9 @@ Scratch g_scratch_h, g_scratch_hs, g_scratch_ys;
 uint16_t* g_nearest_dev = nullptr;   // IQ3_S encoder table, uploaded on first use
 
 // Optional HIP-event timing of every kernel the library launches, by kernel
-// kind (the reference's SABAH_LLAMA_EVENTS probe, sabah_rt.cu:118-151):
-// an event pair brackets each launch on its own stream; elapsed times are
-// collected when the caller asks for them.
+// kind (the reference's SABAH_LLAMA_EVENTS probe, sabah_rt.cu:118-151): each
+// dispatch records its own start/stop event pair (launch_kernel); elapsed
+// times are collected when the caller asks for them.
 enum KernelKind { KK_MMID = 0, KK_GATE_UP = 1, KK_DOWN = 2, KK_CHAIN = 3, KK_COUNT = 4 };
 struct EvPair {
     hipEvent_t a, b;
@@ -68,28 +69,27 @@ std::vector<EvPair> g_ev_free, g_ev_pending;
 double g_kind_ms[KK_COUNT] = {0};
 unsigned long long g_kind_launches[KK_COUNT] = {0};
 
-struct TimedLaunch {
-    EvPair ev{};
-    bool on = false;
-    hipStream_t st;
-    TimedLaunch(int kind, hipStream_t s) : st(s) {
-        if (!g_timing) return;
+// Launch a kernel; with kernel timing on, the dispatch itself records a
+// start and a stop event (hipExtLaunchKernelGGL), so the pair brackets that
+// kernel's execution on its stream and nothing else.
+template <typename K, typename A>
+void launch_kernel(int kind, K kernel, dim3 grid, int lds, hipStream_t st, const A& args) {
+    if (g_timing) {
         if (g_ev_free.empty()) {
             EvPair p{};
-            if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return;
-            g_ev_free.push_back(p);
+            if (hipEventCreate(&p.a) == hipSuccess && hipEventCreate(&p.b) == hipSuccess) g_ev_free.push_back(p);
         }
-        ev = g_ev_free.back();
-        g_ev_free.pop_back();
-        ev.kind = kind;
-        on = hipEventRecord(ev.a, st) == hipSuccess;
+        if (!g_ev_free.empty()) {
+            EvPair ev = g_ev_free.back();
+            g_ev_free.pop_back();
+            ev.kind = kind;
+            hipExtLaunchKernelGGL(kernel, grid, dim3(kThreads), (uint32_t)lds, st, ev.a, ev.b, 0u, args);
+            g_ev_pending.push_back(ev);
+            return;
+        }
     }
-    ~TimedLaunch() {
-        if (!on) return;
-        if (hipEventRecord(ev.b, st) == hipSuccess) g_ev_pending.push_back(ev);
-        else g_ev_free.push_back(ev);
-    }
-};
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, st, args);
+}
 
 int fail(const char* fmt, ...) {
     va_list ap;
@@ -124,7 +124,20 @@ void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     return s.p;
 }
 
-constexpr int kMaxLds = 65536;
+// LDS a workgroup may allocate (the device's limit: 160 KB on gfx950)
+int g_max_lds = 65536;
+
+// Plans above 64 KB of dynamic LDS declare their size to the runtime first.
+template <typename K>
+hipError_t fit_lds(K kernel, int bytes) {
+    if (bytes > g_max_lds) return hipErrorInvalidConfiguration;
+    if (bytes > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
 
 // rows per workgroup (rows_per_wg); rows that are not packed are one tile
 // each, at most kMaxTiles per workgroup
@@ -185,10 +198,9 @@ bool sync_ids_enabled() {
 template <int QT>
 hipError_t launch_mmid(const MmidArgs& a, hipStream_t st) {
     const Plan P = make_plan(QT, a.k, 1, a.R * contribs_per_row(QT, a.k));
-    if (P.bytes > kMaxLds) return hipErrorInvalidConfiguration;
+    if (const hipError_t e = fit_lds(k_mmid<QT>, P.bytes)) return e;
     dim3 grid((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)a.n_ids, (unsigned)a.n_tokens);
-    TimedLaunch tl(KK_MMID, st);
-    hipLaunchKernelGGL(k_mmid<QT>, grid, dim3(kThreads), P.bytes, st, a);
+    launch_kernel(KK_MMID, k_mmid<QT>, grid, P.bytes, st, a);
     return hipGetLastError();
 }
 
@@ -205,10 +217,9 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
 template <int QT>
 hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * contribs_per_row(QT, a.d_model));
-    if (P.bytes > kMaxLds) return hipErrorInvalidConfiguration;
+    if (const hipError_t e = fit_lds(k_gate_up<QT>, P.bytes)) return e;
     dim3 grid((unsigned)((a.d_ff + a.R - 1) / a.R), (unsigned)a.n_slots, (unsigned)n_tokens);
-    TimedLaunch tl(KK_GATE_UP, st);
-    hipLaunchKernelGGL(k_gate_up<QT>, grid, dim3(kThreads), P.bytes, st, a);
+    launch_kernel(KK_GATE_UP, k_gate_up<QT>, grid, P.bytes, st, a);
     return hipGetLastError();
 }
 
@@ -225,10 +236,9 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
 template <int QT>
 hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
     const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * contribs_per_row(QT, a.d_ff));
-    if (P.bytes > kMaxLds) return hipErrorInvalidConfiguration;
+    if (const hipError_t e = fit_lds(k_down_combine<QT>, P.bytes)) return e;
     dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
-    TimedLaunch tl(KK_DOWN, st);
-    hipLaunchKernelGGL(k_down_combine<QT>, grid, dim3(kThreads), P.bytes, st, a);
+    launch_kernel(KK_DOWN, k_down_combine<QT>, grid, P.bytes, st, a);
     return hipGetLastError();
 }
 
@@ -278,6 +288,9 @@ SABAH_API int sabah_rt_init(int device) {
     if (g_device == device && g_stream) return 0;
     if (g_device >= 0) return fail("sabah_rt_init(%d): already initialised on device %d", device, g_device);
     if (!ck(hipSetDevice(device), "hipSetDevice")) return -1;
+    int lds = 0;
+    if (!ck(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device), "LDS limit")) return -1;
+    g_max_lds = lds;
     if (!ck(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "create stream")) return -1;
     if (!ck(hipHostMalloc(reinterpret_cast<void**>(&g_err_host), sizeof(unsigned int), hipHostMallocMapped),
             "sticky error word")) return -1;

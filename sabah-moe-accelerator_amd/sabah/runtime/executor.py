@@ -141,3 +141,35 @@ class MoEExecutor:
         rt.check(rt.lib().sabah_moe_chain(descs, L, _vp(x), _vp(ids), _vp(w), k, T, _stream(self.device)),
                  "moe_chain")
         return x
+
+
+class ChainGraph:
+    """The decode chain (every layer's gate/up and down kernels) captured once
+    as a HIP graph over static x / ids / weights buffers.  replay() copies one
+    step's inputs in and replays the graph: the host submits one graph per
+    step instead of two kernels per layer.  The library allocates its scratch
+    in an eager call before the capture, so nothing is allocated inside it."""
+
+    def __init__(self, ex: MoEExecutor, n_tokens: int, k: int, descs=None):
+        L = ex.bank.n_layers
+        dev = ex.device
+        self.ex = ex
+        self.descs = ex.layer_descs() if descs is None else descs
+        self.x = torch.zeros(n_tokens, ex.d_model, dtype=torch.float32, device=dev)
+        self.ids = torch.zeros(L, n_tokens, k, dtype=torch.int32, device=dev)
+        self.w = torch.zeros(L, n_tokens, k, dtype=torch.float32, device=dev)
+        ex.run_chain(self.x, self.ids, self.w, self.descs)       # eager: sizes the library scratch
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            ex.run_chain(self.x, self.ids, self.w, self.descs)
+        torch.cuda.synchronize(dev)
+
+    def replay(self, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """x [n_tokens, d_model], ids / w [n_layers, n_tokens, k]; returns the
+        static output buffer (valid in stream order)."""
+        self.x.copy_(x)
+        self.ids.copy_(ids)
+        self.w.copy_(w)
+        self.graph.replay()
+        return self.x

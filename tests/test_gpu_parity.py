@@ -94,8 +94,10 @@ def v2(hip_rt, src, expert_stride, row_bytes, x, ids, out, rows, k, E, qt):
         vp(out), out.stride(1) * 4, out.stride(0) * 4, rows, k, E, qt, stream(), None)
 
 
+# (Q8_0, 32768): a row (34816 bytes) larger than a workgroup's 32 KB staging
+# area, so each row is staged in two passes, with over 64 KB of LDS
 CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), (Q4_K, 768, 64),
-         (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104)]
+         (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104), (Q8_0, 32768, 6)]
 
 
 @pytest.mark.parametrize("qt,k,rows", CASES)
@@ -121,6 +123,29 @@ def test_mul_mat_id_matches_oracle(hip_rt, orc, qt, k, rows, x_rows_is_n_ids):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     if x_rows == 1:
         assert np.array_equal(got[2, 3], got[2, 1])
+
+
+@pytest.mark.parametrize("qt,k,rows,pad", [(IQ3_S, 2560, 40, 36), (Q8_0, 1024, 24, 6), (Q4_K, 512, 70, 16)])
+def test_mul_mat_id_padded_rows(hip_rt, orc, qt, k, rows, pad):
+    """Rows `pad` bytes apart beyond their length (src0->nb[1] > row bytes):
+    each row is staged as its own tile; IQ3_S k=2560 rows (1100 bytes) take
+    two passes at 25 tiles per workgroup."""
+    rng = np.random.default_rng(qt * 7 + k + pad)
+    E, Tn, K = 5, 2, 3
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    rb = raw.shape[-1]
+    padded = np.full((E, rows, rb + pad), 0xA5, dtype=np.uint8)
+    padded[:, :, :rb] = raw
+    ids = np.stack([rng.choice(E, K, replace=False) for _ in range(Tn)]).astype(np.int32)
+    x = rng.standard_normal((Tn, 1, k)).astype(np.float32)
+    bank = T(padded)
+    out = torch.full((Tn, K, rows), float("nan"), dtype=torch.float32, device=DEV)
+    hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * (rb + pad), rb + pad, T(x), T(ids), out, rows, k, E, qt), "v2")
+    torch.cuda.synchronize()
+    want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    assert_parity(out.cpu().numpy(), want, "padded qt=%d" % qt)
+    if qt in (Q8_0, IQ3_S):
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 def test_mul_mat_id_detects_wrong_expert_and_wrong_row(hip_rt, orc):
@@ -276,6 +301,29 @@ def test_moe_chain_is_the_sequence_of_residual_layers(hip_rt, orc):
     for l in range(L):
         xr = xr + orc.moe_layer(raws[(l, "gate")], raws[(l, "up")], raws[(l, "down")], (IQ3_S,) * 3, xr, ids[l], w[l])
     assert_parity(xd.cpu().numpy(), xr, "chain")
+
+
+def test_chain_graph_replays_match_eager(hip_rt, orc):
+    """The chain captured as a HIP graph: three replays with different
+    inputs, eager work and synchronisations in between, each bit-identical to
+    the eager chain on the same inputs."""
+    from sabah.runtime import routing
+    from sabah.runtime.executor import ChainGraph, MoEExecutor
+    rng = np.random.default_rng(57)
+    E, D, F, K, L = 24, 512, 256, 4, 3
+    bank, _ = make_bank(orc, rng, (IQ3_S,) * 3, E, D, F, n_layers=L)
+    ex = MoEExecutor(bank, max_used=K)
+    cg = ChainGraph(ex, 1, K)
+    for rep in range(3):
+        ids, w = routing.zipf_routing(rng, 1, E, K, n_layers=L)
+        x0 = T(rng.standard_normal((1, D)).astype(np.float32))
+        xe = x0.clone()
+        ex.run_chain(xe, T(ids), T(w))
+        torch.cuda.synchronize()
+        got = cg.replay(x0, T(ids), T(w))
+        torch.cuda.synchronize()
+        assert torch.equal(got, xe), "replay %d" % rep
+        (x0 * 2.0).sum().item()                          # unrelated eager work between replays
 
 
 def test_full_size_iq3s_layer_on_synthetic_bank(hip_rt, orc):
