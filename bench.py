@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="finish with one device-to-device copy of this many MiB (a plain copy kernel of known "
+                         "size, to calibrate the FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -144,7 +147,7 @@ def main() -> int:
     }
     achieved = per_launch[dom] / (kernels[dom]["avg_us"] * 1e3)          # GB/s
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(W.name, dom),
                 "kernel": dom, "bytes_per_launch": per_launch[dom], "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
 
     cpu = None
@@ -169,7 +172,30 @@ def main() -> int:
         "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
     }
     print(json.dumps(line), flush=True)
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 18                                   # floats
+        a = torch.ones(n, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        print("copy probe: %d MiB read, %d MiB written" % (args.copy_probe_mib, args.copy_probe_mib),
+              file=sys.stderr, flush=True)
     return 0
+
+
+KERNEL_SYMBOL = {"gate_up": "k_gate_up", "down": "k_down_combine", "mmid": "k_mmid"}
+
+
+def measured_traffic(workload, kind):
+    """HBM bytes per launch of `kind` from the committed FETCH_SIZE / WRITE_SIZE
+    counter runs (calibrated against a plain copy), or None if not measured."""
+    path = os.path.join(ROOT, "profiles", "decode_kernels_%s_traffic.json" % workload)
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][KERNEL_SYMBOL[kind]]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np, dev):

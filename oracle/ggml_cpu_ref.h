@@ -10,7 +10,33 @@
  * third_party/llama.cpp.version:1-2) is not vendored in the reference, so the
  * algorithm is restated from its published form and anchored on the
  * reference's own call sites and format readers; each function below cites
- * them.  Function-level pinning is described in oracle/README.md.
+ * them.
+ *
+ * How each function is pinned (tests/test_oracle_formats.py,
+ * tests/test_oracle_tables.py, tests/test_golden_trace.py):
+ *   orc_fp16_to_fp32 / orc_fp32_to_fp16: every finite half; numpy's
+ *     round-to-nearest-even conversion on random values and exact ties.
+ *   orc_quantize_q8_0: hand-computed blocks; halves rounded away from zero
+ *     (quants.py:413-427, np_roundf 44-48); the all-zero block.
+ *   orc_quantize_q8_K: hand-computed blocks; ties to even; the scale takes
+ *     the sign of the first maximum; clamp at 127; zero block; bsums
+ *     (tools/rc4/opcheck.py:73-80).
+ *   orc_dequantize_row: known-answer blocks per format (d = 1, unit scales,
+ *     codebook rows, sign / qh / scale bits) from the closed forms of
+ *     sabah_rt.cu:2233-2423 and quants.py:412-435, 509-556, 586-606, 1091-1159.
+ *   the IQ3_S codebook: equal to both reference copies (sabah_iq_tables.h:
+ *     638-704 and quants.py:1094-1127 grid_hex) and to its recorded sha256.
+ *   orc_vec_dot: the float64 dot of the decoded operands (all formats); the
+ *     IQ3_S integer block sums exactly; the Q4_K min term through bsums.
+ *   orc_mul_mat_id / orc_moe_layer: brute-force loops; bad ids and geometry
+ *     rejected; a layer is the composition of its MUL_MAT_IDs; the shared
+ *     expert is added last; duplicate ids of the reference's recorded routing
+ *     trace give identical slot outputs.
+ *   orc_quantize_weights: round trip (its output only has to be valid input).
+ * Parity unpinned: the fp32 accumulation order inside orc_vec_dot for Q4_K
+ * and Q6_K (ggml's generic eight-lane order, restated from its published
+ * source, which cannot be built or run here).  Checks against those two use
+ * the floating-point tolerance, not bit equality.
  */
 #pragma once
 #include <stddef.h>
