@@ -75,67 +75,61 @@ __device__ inline void flag_error(unsigned int* err) {
 // slots' down matrices; one matrix for MUL_MAT_ID), or single rows when rows
 // are not packed.  Every tile holds the same number of units, in row-major
 // unit order, at contiguous bytes.  The workgroup walks them in passes of V
-// units per tile: a pass copies each tile's byte range HBM -> LDS, then all
-// four waves decode the staged units.
+// units per tile; a pass's tiles are staged in LDS, tile t at 16 * cpt * t,
+// starting `lead` (its HBM address mod 16) bytes into its first 16-byte
+// chunk, so staged bytes keep their HBM alignment mod 16.
 //
-// The copy uses direct-to-LDS loads (global_load_lds_dwordx4).  The
-// compiler makes any later LDS access of a wave wait for that wave's
-// outstanding direct-to-LDS loads, so the work is split by wave: waves 0-1
-// ("DMA waves") issue the copy, waves 2-3 ("worker waves") meanwhile
-// quantise the activations and build the IQ3_S tables.  A tile's bytes are
-// copied in 1 KB segments (one load instruction of a wave: 64 lanes x 16
-// consecutive bytes); a segment's address is wave-uniform.  Tile t occupies
-// segments [t*spt, (t+1)*spt) of the staging area, starting `lead` (its HBM
-// address mod 16) bytes into its first segment, so staged bytes keep their
-// HBM alignment mod 16; lanes past a tile's last 16-byte chunk re-load that
-// chunk into bytes that are never read.
+// Within a pass every wave works on its own: wave-round j (wave j % 4) owns
+// Q consecutive units of the pass (tile-major numbering), loads the 16-byte
+// chunks covering them into registers (lanes read consecutive chunks, so a
+// load instruction of a wave reads 1 KB of contiguous HBM), writes them to
+// their place in LDS and decodes its units - no workgroup barrier stands
+// between a wave's data arriving and its decode.  A wave-round spans at most
+// kMaxPieces tiles (Q <= 3 * units per tile).  Each lane issues exactly
+// StageIters<QT> loads (a static count, so waits for older loads stay
+// exact); lanes past the last chunk re-load it.  Chunks at the edge of two
+// wave-rounds are written by both, with the same bytes.
 // ---------------------------------------------------------------------------
-constexpr int kDmaWaves = 2;
-constexpr int kWorkBase = 64 * kDmaWaves;                       // first worker thread
-constexpr int kWorkThreads = kThreads - kWorkBase;
-constexpr int kSegBytes = 1024;
-constexpr int kStageSegs = 32;
-constexpr int kStageBytes = kSegBytes * kStageSegs;             // 32 KB per workgroup
+constexpr int kStageChunks = 2048;                            // 32 KB per workgroup
+constexpr int kStageBytes = 16 * kStageChunks;
 constexpr int kStageGuard = 16;
-constexpr int kMaxTiles = kStageSegs;                           // at least one segment per tile
-static_assert(kDmaWaves == 2, "stage_segments deals segments to two waves");
+constexpr int kMaxTiles = 64;
+constexpr int kMaxPieces = 4;
+constexpr int kWaveUnits = 64;
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
-// segments per tile of tile_bytes (any lead)
-__host__ __device__ inline int tile_segs(int tile_bytes) { return (tile_bytes + 30 + kSegBytes - 1) / kSegBytes; }
-// units per tile per pass: the largest V with n_mat * tile_segs(V * unit bytes) <= kStageSegs
+// chunks of a tile of tile_bytes at any lead
+__host__ __device__ inline int tile_chunks(int tile_bytes) { return (tile_bytes + 30) / 16; }
+// units per tile per pass: the largest V with n_mat * tile_chunks(V * unit bytes) <= kStageChunks
 __host__ __device__ inline int pass_units(int n_mat, int unit_bytes) {
-    return max(1, (kSegBytes * (kStageSegs / n_mat) - 30) / unit_bytes);
+    return max(1, (16 * (kStageChunks / n_mat) - 30) / unit_bytes);
 }
+// 16-byte loads per lane per wave-round: enough for kWaveUnits units over kMaxPieces tiles
+template <int QT>
+struct StageIters {
+    static constexpr int V = ((kWaveUnits * UnitFmt<QT>::BYTES + 30 * kMaxPieces + 15) / 16 + 63) / 64;
+};
 
-// DMA wave `wave` issues its share (every kDmaWaves-th segment) of the copy
-// of n tiles of pass_bytes each; tile t's pass starts at HBM address
-// tile_ptr(t) + b0 (tile_ptr is called with wave-uniform t).
-template <typename TilePtr>
-__device__ inline void stage_segments(uint8_t* stage, TilePtr tile_ptr, int n, int pass_bytes, int b0, int wave) {
-    const int spt = tile_segs(pass_bytes);
-    const int lane = (int)(threadIdx.x & 63u);
-    for (int t = 0; t < n; ++t) {
-        const uint8_t* p = tile_ptr(t) + b0;
-        const int lead = (int)(reinterpret_cast<uintptr_t>(p) & 15);
-        const int last = (lead + pass_bytes - 1) >> 4;
-        const uint8_t* base = p - lead;
-        for (int j = (t * spt + wave) & 1; j < spt; j += kDmaWaves) {   // segment t*spt + j is wave (t*spt + j) % 2's
-            const int c = min(64 * j + lane, last);
-            __builtin_amdgcn_global_load_lds((glb_void_t*)(base + 16 * c),
-                                             (lds_void_t*)(stage + kSegBytes * (t * spt + j)), 16, 0, 0);
-        }
-    }
+// Q8_0 rows need only be whole 32-element blocks: their last unit may hold 1..3 blocks
+__host__ __device__ inline int units_per_row(int qt, int k) { return qt == QT_Q8_0 ? (k + 127) / 128 : k / 256; }
+__host__ __device__ inline int contribs_per_row(int qt, int k) { return k / block_elems(qt); }   // ggml blocks
+__host__ __device__ inline int unit_bytes(int qt) { return qt == QT_Q8_0 ? 136 : (int)block_bytes(qt); }
+
+// Rows per workgroup: about one unit per lane, with the n_mat tiles staged in
+// one pass where a row fits.
+__host__ __device__ inline int rows_per_wg(int qt, int k, int n_mat) {
+    const int nus = units_per_row(qt, k);
+    const int by_lanes = kThreads / (n_mat * nus);
+    const int by_stage = (16 * (kStageChunks / n_mat) - 30) / (int)row_bytes(qt, k);
+    return max(1, min(by_lanes, by_stage));
 }
 
 // ---------------------------------------------------------------------------
-// LDS plan (identical on host and device):
-//   [IQ3_S tables][tile leads][guard | staging | guard][activations][partials]
+// LDS: static arrays hold what the decoder addresses with constant offsets
+// (the IQ3_S tables, the staging area); dynamic LDS holds the activation rows
+// and per-block partials:  [activations][partials]
 // ---------------------------------------------------------------------------
 struct Plan {
-    int off_lead, off_stage, off_act, act_bytes, n_act, off_part, bytes;
+    int off_act, act_bytes, n_act, off_part, bytes;
 };
 
 __host__ __device__ inline int align16i(int v) { return (v + 15) & ~15; }
@@ -143,32 +137,25 @@ __host__ __device__ inline int align16i(int v) { return (v + 15) & ~15; }
 // n_act activation rows of k elements for weight type qt; part = n_part floats
 __host__ __device__ inline Plan make_plan(int qt, int k, int n_act, int n_part) {
     Plan p{};
-    int o = (qt == QT_IQ3_S) ? kLdsTables : 0;
-    p.off_lead = o;
-    o += 4 * kMaxTiles;
-    p.off_stage = o + kStageGuard;
-    o += kStageGuard + kStageBytes + kStageGuard;
-    p.off_act = o;
+    p.off_act = 0;
     p.act_bytes = align16i((int)ActLayout(k, act_type(qt)).bytes);
     p.n_act = n_act;
-    o += p.act_bytes * n_act;
-    p.off_part = o;
-    o += align16i(4 * n_part);
-    p.bytes = o;
+    p.off_part = p.act_bytes * n_act;
+    p.bytes = p.off_part + align16i(4 * n_part);
     return p;
 }
 
-// Q8_0 rows need only be whole 32-element blocks: their last unit may hold 1..3 blocks
-__host__ __device__ inline int units_per_row(int qt, int k) { return qt == QT_Q8_0 ? (k + 127) / 128 : k / 256; }
-__host__ __device__ inline int contribs_per_row(int qt, int k) { return k / block_elems(qt); }   // ggml blocks
-
-// Rows per workgroup: about one unit per lane, with the n_mat tiles staged in
-// one pass where a row fits.
-__host__ __device__ inline int rows_per_wg(int qt, int k, int n_mat) {
-    const int nus = units_per_row(qt, k);
-    const int by_lanes = kThreads / (n_mat * nus);
-    const int by_stage = (kSegBytes * (kStageSegs / n_mat) - 30) / (int)row_bytes(qt, k);
-    return max(1, min(by_lanes, by_stage));
+// static LDS of a kernel instantiation: IQ3_S tables, then the staging area
+template <int QT>
+struct StaticLds {
+    static constexpr int TABLES = (QT == QT_IQ3_S) ? kLdsTables : 0;
+    static constexpr int STAGE = TABLES + kStageGuard;
+    static constexpr int BYTES = STAGE + kStageBytes + kStageGuard;
+};
+// total LDS of a launch (static + dynamic), for the host's limit check
+__host__ inline int launch_lds(int qt, const Plan& P) {
+    const int tables = (qt == QT_IQ3_S) ? kLdsTables : 0;
+    return tables + 2 * kStageGuard + kStageBytes + P.bytes;
 }
 
 // bytes of unit us of a row of k elements
@@ -181,21 +168,21 @@ __device__ inline int unit_len(int k, int us) {
 // dot of one unit (unit index us of its row) with activation row `act`; the
 // unit's per-block contributions go to part_row
 template <int QT>
-__device__ inline void unit_into_part(const UnitWindow<QT>& Wn, const uint8_t* smem, const uint8_t* act, int k, int us,
+__device__ inline void unit_into_part(const LdsWindow<QT>& Wn, const uint8_t* tabs, const uint8_t* act, int k, int us,
                                       float* part_row) {
     const ActLayout AL(k, act_type(QT));
     const float* dxa = reinterpret_cast<const float*>(act + AL.off_d);
     const int16_t* bsa = reinterpret_cast<const int16_t*>(act + AL.off_bsum);
     if constexpr (QT == QT_Q8_0) {
         const uint8_t* chunk = act + (us >> 1) * kActChunkStride + (us & 1) * 128;
-        const UnitDot<QT> r = unit_dot<QT>(Wn, smem, chunk, dxa + 4 * us, bsa);
+        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + 4 * us, bsa);
         const int nb = min(4, k / 32 - 4 * us);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (j < nb) part_row[4 * us + j] = r.c[j];
     } else {
         const uint8_t* chunk = act + us * kActChunkStride;
-        const UnitDot<QT> r = unit_dot<QT>(Wn, smem, chunk, dxa + us, bsa + 16 * us);
+        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + us, bsa + 16 * us);
         part_row[us] = r.c[0];
     }
 }
@@ -206,61 +193,201 @@ __device__ inline float row_sum(const float* part_row, int n) {
     return s;
 }
 
+// floor(a / b) for 0 <= a < 2^20 and a / b < 2^12, given r = rcp(b):
+// (a + 0.5) / b is at least 0.5 / b away from an integer, far more than the
+// rounding error of the product
+__device__ inline int div_small(int a, float r) { return (int)(((float)a + 0.5f) * r); }
+
 // One workgroup's tiles.  Tile t is matrix tile_ptr(t) from its first row on
 // (row0 already folded into the pointer): `nrows` rows of k elements at rb
 // bytes, so its unit v = r * NUS + us sits at byte r * rb + us * unit bytes.
-// Activations of tile t: act0 + t * act_stride (act_stride 0: one shared
-// row).  Contributions of unit (t, r, us) go to part + (t * part_rows + r) * NCB.
 template <int QT>
 struct TileWalk {
     static constexpr int UB = UnitFmt<QT>::BYTES;
     int n_mat, NUS, NCB, total, V;
     size_t rb;
+    float rcp_nus;
     __device__ TileWalk(int n_mat_, int nrows, size_t rb_, int k)
         : n_mat(n_mat_), NUS(units_per_row(QT, k)), NCB(contribs_per_row(QT, k)), total(nrows * NUS),
-          V(pass_units(n_mat_, UB)), rb(rb_) {}
-    __device__ int byte_of(int v) const { return (int)((size_t)(v / NUS) * rb) + (v % NUS) * UB; }
-    __device__ int pass_bytes(int v0) const { return byte_of(min(v0 + V, total)) - byte_of(v0); }
+          V(pass_units(n_mat_, UB)), rb(rb_), rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
+    __device__ int byte_of(int v) const {
+        const int r = div_small(v, rcp_nus);
+        return (int)((size_t)r * rb) + (v - r * NUS) * UB;
+    }
 };
 
-// DMA waves, before the first pass: record each tile's lead (lane l of wave 0
-// holds tile l's pointer in lane_tile) and issue the first pass's copy.
+// One wave-round: units [ua, ua + nu) of the pass (tile-major, nv units per
+// tile), as up to kMaxPieces tile pieces.  All fields are wave-uniform.
+struct WaveRound {
+    int np, nu, nch;                 // pieces, units, chunks
+    int t[kMaxPieces];               // tile of piece p
+    int upre[kMaxPieces];            // units before piece p
+    int vb[kMaxPieces];              // pass-relative unit of the piece's first unit, minus upre
+    int cpre[kMaxPieces];            // chunks before piece p
+    int lead[kMaxPieces];            // tile's pass start address mod 16
+    const uint8_t* gb[kMaxPieces];   // global address of the piece's chunk q is gb + 16 q
+    int lb[kMaxPieces];              // staging offset of the piece's chunk q is lb + 16 q
+};
+
 template <int QT, typename TilePtr>
-__device__ inline void tiles_begin(const TileWalk<QT>& T, uint8_t* stage, int* leads, const uint8_t* lane_tile,
-                                   TilePtr tile_ptr, int wave) {
-    if (threadIdx.x < (unsigned)T.n_mat) leads[threadIdx.x] = (int)(reinterpret_cast<uintptr_t>(lane_tile) & 15);
-    stage_segments(stage, tile_ptr, T.n_mat, T.pass_bytes(0), 0, wave);
+__device__ inline WaveRound make_round(const TileWalk<QT>& T, TilePtr tile_ptr, int v0, int nv, int cpt, int ua,
+                                       int ub) {
+    WaveRound W{};
+    W.nu = ub - ua;
+    const int b0 = T.byte_of(v0);
+    const int t0 = ua / nv;
+    int u = ua, c = 0, np = 0;
+#pragma unroll
+    for (int p = 0; p < kMaxPieces; ++p) {      // static indices: the fields stay in registers
+        const int t = t0 + p;
+        const bool live = u < ub;
+        const int va = u - t * nv, vbnd = min(ub, (t + 1) * nv) - t * nv;
+        const int xa = T.byte_of(v0 + va) - b0, xb = T.byte_of(v0 + vbnd) - b0;
+        const uint8_t* P = tile_ptr(live ? t : t0) + b0;
+        const int lead = (int)(reinterpret_cast<uintptr_t>(P) & 15);
+        const int c_lo = (lead + xa) >> 4, c_hi = (lead + xb - 1) >> 4;
+        W.t[p] = t;
+        W.upre[p] = u - ua;
+        W.vb[p] = va - (u - ua);
+        W.cpre[p] = c;
+        W.lead[p] = lead;
+        W.gb[p] = P - lead + 16 * (c_lo - c);
+        W.lb[p] = 16 * (cpt * t + c_lo - c);
+        if (live) {
+            c += c_hi - c_lo + 1;
+            u += vbnd - va;
+            ++np;
+        }
+    }
+    W.np = np;
+    W.nch = c;
+    return W;
 }
 
-// All waves: decode the staged pass, then walk the remaining passes.
-template <int QT, typename TilePtr>
-__device__ inline void tiles_finish(const TileWalk<QT>& T, const uint8_t* smem, uint8_t* stage, const int* leads,
-                                    TilePtr tile_ptr, int wave, int k, const uint8_t* act0, int act_stride,
-                                    int part_rows, float* part) {
-    for (int v0 = 0;;) {
-        const int nv = min(T.V, T.total - v0);
-        const int b0 = T.byte_of(v0);
-        const int spt = tile_segs(T.pass_bytes(v0));
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        for (int u = threadIdx.x; u < T.n_mat * nv; u += blockDim.x) {
-            const int t = u / nv, v = v0 + (u - t * nv);
-            const int r = v / T.NUS, us = v - r * T.NUS;
-            const int lead = (leads[t] + b0) & 15;
-            UnitWindow<QT> Wn;
-            Wn.load_lds(stage + kSegBytes * spt * t + lead + (T.byte_of(v) - b0));
-            unit_into_part<QT>(Wn, smem, act0 + t * act_stride, k, us, part + (t * part_rows + r) * T.NCB);
-        }
-        v0 += T.V;
-        __syncthreads();   // the pass's units are decoded (and its partials written)
-        if (v0 >= T.total) break;
-        if (wave < kDmaWaves) stage_segments(stage, tile_ptr, T.n_mat, T.pass_bytes(v0), T.byte_of(v0), wave);
+// The field of the piece that holds chunk (or unit) x, given the pieces'
+// chunk (or unit) prefixes: a chain of selects on the prefix comparisons.
+// (Selecting on a computed piece index instead lets the optimizer turn the
+// chain back into an indexed array, which then lives in scratch memory.)
+template <typename V>
+__device__ inline V pick(const V (&a)[kMaxPieces], const int (&pre)[kMaxPieces], int np, int x) {
+    V r = a[0];
+#pragma unroll
+    for (int j = 1; j < kMaxPieces; ++j) r = (j < np && x >= pre[j]) ? a[j] : r;
+    return r;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT>
+struct RoundRegs {
+    u32x4 d[StageIters<QT>::V];
+    int lds[StageIters<QT>::V];
+};
+
+// issue the wave-round's chunk loads (a static number per lane)
+template <int QT>
+__device__ inline void round_load(const WaveRound& W, RoundRegs<QT>& R) {
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    const int lane = (int)(threadIdx.x & 63u);
+#pragma unroll
+    for (int it = 0; it < StageIters<QT>::V; ++it) {
+        const int q = min(64 * it + lane, W.nch - 1);
+        R.d[it] = *(g_u32x4*)(pick(W.gb, W.cpre, W.np, q) + 16 * q);
+        R.lds[it] = pick(W.lb, W.cpre, W.np, q) + 16 * q;
     }
 }
 
-__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+template <int QT>
+__device__ inline void round_store(uint8_t* stage, const RoundRegs<QT>& R) {
+#pragma unroll
+    for (int it = 0; it < StageIters<QT>::V; ++it) *reinterpret_cast<u32x4*>(stage + R.lds[it]) = R.d[it];
+}
 
-// wave-uniform copy of lane `src`'s 64-bit pointer
+// decode the wave-round's units, one per lane; contributions of unit
+// (t, r, us) go to part + (t * part_rows + r) * NCB
+template <int QT>
+__device__ inline void round_decode(const TileWalk<QT>& T, const WaveRound& W, int v0, int cpt, const uint8_t* tabs,
+                                    const uint8_t* stage, int k, const uint8_t* act0, int act_stride, int part_rows,
+                                    float* part) {
+    const int i = (int)(threadIdx.x & 63u);
+    if (i >= W.nu) return;
+    const int t = pick(W.t, W.upre, W.np, i);
+    const int v = v0 + pick(W.vb, W.upre, W.np, i) + i;   // tile-relative unit (row-major over the rows)
+    const int r = div_small(v, T.rcp_nus), us = v - r * T.NUS;
+    const int b0 = T.byte_of(v0);
+    LdsWindow<QT> Wn;
+    Wn.load(stage + 16 * cpt * t + pick(W.lead, W.upre, W.np, i) + (int)((size_t)r * T.rb) + us * TileWalk<QT>::UB - b0);
+    unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, part + (t * part_rows + r) * T.NCB);
+}
+
+// All passes of a workgroup's tiles.  The first wave-round's loads must have
+// been issued by the caller (begin_tiles) before its own prologue, so the
+// prologue's waits do not wait for them; the caller's barrier after the
+// prologue makes activations and tables visible.
+template <int QT>
+struct TileRun {
+    TileWalk<QT> T;
+    int nv, cpt, Q, n_rounds;
+    WaveRound W;
+    RoundRegs<QT> R;
+};
+
+template <int QT>
+__device__ inline void set_pass(TileRun<QT>& S, int v0) {
+    S.nv = min(S.T.V, S.T.total - v0);
+    S.cpt = tile_chunks(S.T.byte_of(v0 + S.nv) - S.T.byte_of(v0));
+    S.Q = min(kWaveUnits, 3 * S.nv);
+    S.n_rounds = (S.T.n_mat * S.nv + S.Q - 1) / S.Q;
+}
+
+// Every wave issues its first wave-round's loads, also a wave with no units
+// in the first pass: it re-loads the pass's last unit (valid memory, bytes
+// its owner writes too) and decodes nothing, so the count of loads in flight
+// is the same on every wave.
+template <int QT, typename TilePtr>
+__device__ inline void tiles_begin(TileRun<QT>& S, TilePtr tile_ptr) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    set_pass(S, 0);
+    const int N = S.T.n_mat * S.nv;
+    const int ua = wave * S.Q, ub = min(ua + S.Q, N);
+    const int la = min(ua, N - 1);
+    S.W = make_round(S.T, tile_ptr, 0, S.nv, S.cpt, la, max(ub, la + 1));
+    S.W.nu = max(0, ub - ua);
+    round_load<QT>(S.W, S.R);
+}
+
+template <int QT, typename TilePtr>
+__device__ inline void tiles_finish(TileRun<QT>& S, TilePtr tile_ptr, const uint8_t* tabs, uint8_t* stage, int k,
+                                    const uint8_t* act0, int act_stride, int part_rows, float* part) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nwaves = (int)(blockDim.x >> 6);
+    bool loaded = true;                    // this wave's first round of the pass is in flight
+    for (int v0 = 0;;) {
+        if (loaded) {
+            for (int j = wave;;) {
+                round_store<QT>(stage, S.R);
+                round_decode<QT>(S.T, S.W, v0, S.cpt, tabs, stage, k, act0, act_stride, part_rows, part);
+                j += nwaves;
+                if (j >= S.n_rounds) break;
+                const int ua = j * S.Q, ub = min(ua + S.Q, S.T.n_mat * S.nv);
+                S.W = make_round(S.T, tile_ptr, v0, S.nv, S.cpt, ua, ub);
+                round_load<QT>(S.W, S.R);
+            }
+        }
+        __syncthreads();   // the pass is decoded (partials written, staging free)
+        v0 += S.nv;
+        if (v0 >= S.T.total) break;
+        set_pass(S, v0);
+        loaded = wave < S.n_rounds;
+        if (loaded) {
+            const int ua = wave * S.Q, ub = min(ua + S.Q, S.T.n_mat * S.nv);
+            S.W = make_round(S.T, tile_ptr, v0, S.nv, S.cpt, ua, ub);
+            round_load<QT>(S.W, S.R);
+        }
+    }
+}
+
+// 64-bit value of lane `src` of the wave, for a wave-uniform src
 __device__ inline const uint8_t* read_lane_ptr(const uint8_t* p, int src) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
@@ -268,9 +395,9 @@ __device__ inline const uint8_t* read_lane_ptr(const uint8_t* p, int src) {
     return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
 }
 
-// activation rounds prefetched by the worker waves (more are loaded late)
-constexpr int kRoundsX = 2;   // one row: up to 16 chunks of 256 (k <= 4096)
-constexpr int kRoundsH = 4;   // slot rows: up to 32 chunk-rows (n_slots * ceil(d_ff / 256))
+// activation rounds prefetched before the weights (more are loaded late)
+constexpr int kRoundsX = 1;   // one row: 16 chunks of 256 (k <= 4096)
+constexpr int kRoundsH = 2;   // slot rows: 32 chunk-rows (n_slots * ceil(d_ff / 256))
 
 // ---------------------------------------------------------------------------
 // MUL_MAT_ID (sabah_rt_mul_mat_id_v2 semantics, sabah_rt.cu:2791-2839):
@@ -292,29 +419,35 @@ struct MmidArgs {
     unsigned int* err;            // sticky error word, host-mapped; every writer stores 1
 };
 
+// The kernels' static LDS: IQ3_S tables (when QT is IQ3_S) and the staging
+// area with a guard on each side.
+#define SABAH_STATIC_LDS(QT)                                                              \
+    __shared__ __align__(16) uint8_t lds_static[StaticLds<QT>::BYTES];                    \
+    uint8_t* const tabs = lds_static;                                                    \
+    uint8_t* const stage = lds_static + StaticLds<QT>::STAGE;
+
 template <int QT>
 __global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
+    SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.k);
     const Plan P = make_plan(QT, a.k, 1, a.R * NCB);
     const int t = blockIdx.z, i = blockIdx.y, row0 = blockIdx.x * a.R;
     const int nrows = min(a.R, a.rows - row0);
     const size_t rb = row_bytes(QT, a.k);
-    const int wave = wave_id();
     float* out = reinterpret_cast<float*>(a.dst + (size_t)t * a.dst_token_stride + (size_t)i * a.dst_id_stride) + row0;
     uint8_t* act = smem + P.off_act;
     float* part = reinterpret_cast<float*>(smem + P.off_part);
-    uint8_t* stage = smem + P.off_stage;
-    int* leads = reinterpret_cast<int*>(smem + P.off_lead);
     const float* xr = reinterpret_cast<const float*>(a.x + (size_t)t * a.x_token_stride +
                                                      (size_t)(i % a.x_rows) * a.x_id_stride);
+    // activation and table loads first, then the weights, so the prologue's
+    // waits do not wait for the weights (loads complete in order); the expert
+    // id is a scalar load with its own counter
     const ActBatch xb{xr, 0, 1, a.k, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
-    GridRegs<kWorkThreads> gr;
-    if (wave >= kDmaWaves) {   // worker loads first; the expert id is a scalar load with its own counter
-        act_prefetch<kRoundsX>(xb, xa, kWorkBase);
-        if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kWorkThreads>((int)threadIdx.x - kWorkBase);
-    }
+    act_prefetch<kRoundsX>(xb, xa);
+    GridRegs<kThreads> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
     const uint8_t* w = expert_ptr(a.W, a.rt, t, i, a.n_ids);
     if (w == nullptr) {   // uniform across the workgroup
         flag_error(a.err);
@@ -324,14 +457,12 @@ __global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
     w += (size_t)row0 * a.row_stride;
     const bool packed = a.row_stride == rb;
     auto tile_ptr = [&](int r) { return packed ? w : w + (size_t)r * a.row_stride; };
-    const TileWalk<QT> T(packed ? 1 : nrows, packed ? nrows : 1, rb, a.k);
-    if (wave < kDmaWaves) {
-        tiles_begin(T, stage, leads, tile_ptr((int)threadIdx.x), tile_ptr, wave);
-    } else {
-        if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kWorkThreads>(smem, gr, (int)threadIdx.x - kWorkBase);
-        act_quantize<kRoundsX>(xb, xa, kWorkBase);
-    }
-    tiles_finish(T, smem, stage, leads, tile_ptr, wave, a.k, act, 0, packed ? a.R : 1, part);
+    TileRun<QT> S{TileWalk<QT>(packed ? 1 : nrows, packed ? nrows : 1, rb, a.k)};
+    tiles_begin(S, tile_ptr);
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    act_quantize<kRoundsX>(xb, xa);
+    __syncthreads();
+    tiles_finish(S, tile_ptr, tabs, stage, a.k, act, 0, packed ? a.R : 1, part);
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) out[r] = row_sum(part + r * NCB, NCB);
 }
 
@@ -354,25 +485,21 @@ __device__ inline float silu_f32(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, 
 
 template <int QT>
 __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
+    SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.d_model);
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * NCB);
     const int t = blockIdx.z, s = blockIdx.y, row0 = blockIdx.x * a.R;
     const int nrows = min(a.R, a.d_ff - row0);
     const size_t rb = row_bytes(QT, a.d_model);
-    const int wave = wave_id();
     float* h = a.h + ((size_t)t * a.n_slots + s) * a.d_ff + row0;
     uint8_t* act = smem + P.off_act;
     float* part = reinterpret_cast<float*>(smem + P.off_part);
-    uint8_t* stage = smem + P.off_stage;
-    int* leads = reinterpret_cast<int*>(smem + P.off_lead);
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
-    GridRegs<kWorkThreads> gr;
-    if (wave >= kDmaWaves) {
-        act_prefetch<kRoundsX>(xb, xa, kWorkBase);
-        if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kWorkThreads>((int)threadIdx.x - kWorkBase);
-    }
+    act_prefetch<kRoundsX>(xb, xa);
+    GridRegs<kThreads> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
     const uint8_t* wg = expert_ptr(a.G, a.rt, t, s, a.n_slots);
     const uint8_t* wu = expert_ptr(a.U, a.rt, t, s, a.n_slots);
     if (wg == nullptr || wu == nullptr) {
@@ -383,14 +510,12 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
     wg += (size_t)row0 * rb;
     wu += (size_t)row0 * rb;
     auto tile_ptr = [&](int m) { return m ? wu : wg; };
-    const TileWalk<QT> T(2, nrows, rb, a.d_model);
-    if (wave < kDmaWaves) {
-        tiles_begin(T, stage, leads, threadIdx.x ? wu : wg, tile_ptr, wave);
-    } else {
-        if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kWorkThreads>(smem, gr, (int)threadIdx.x - kWorkBase);
-        act_quantize<kRoundsX>(xb, xa, kWorkBase);
-    }
-    tiles_finish(T, smem, stage, leads, tile_ptr, wave, a.d_model, act, 0, a.R, part);
+    TileRun<QT> S{TileWalk<QT>(2, nrows, rb, a.d_model)};
+    tiles_begin(S, tile_ptr);
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    act_quantize<kRoundsX>(xb, xa);
+    __syncthreads();
+    tiles_finish(S, tile_ptr, tabs, stage, a.d_model, act, 0, a.R, part);
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
@@ -421,43 +546,38 @@ struct DownArgs {
 
 template <int QT>
 __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
+    SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.d_ff);
     const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * NCB);
     const int t = blockIdx.y, row0 = blockIdx.x * a.R;
     const int nrows = min(a.R, a.d_model - row0);
     const size_t rb = row_bytes(QT, a.d_ff);
-    const int wave = wave_id();
     uint8_t* act = smem + P.off_act;
     float* part = reinterpret_cast<float*>(smem + P.off_part);
-    uint8_t* stage = smem + P.off_stage;
-    int* leads = reinterpret_cast<int*>(smem + P.off_lead);
     // lane s of every wave holds slot s's tile (lanes past n_slots repeat the
     // last slot); a slot with an invalid id stages expert 0's rows, never
     // used: the output is poisoned.  The id loads go first, so waiting for
     // them does not wait for the activation loads.
     const int lane = (int)(threadIdx.x & 63u);
     const SlotWord sw = load_slot_word(a.D, a.rt, t, min(lane, a.n_slots - 1), a.n_slots);
+    __builtin_amdgcn_sched_barrier(0);
     const ActBatch hb{a.h + (size_t)t * a.n_slots * a.d_ff, (size_t)a.d_ff, a.n_slots, a.d_ff, act_type(QT), act,
                       P.act_bytes};
     ActRegs<kRoundsH> ha;
-    GridRegs<kWorkThreads> gr;
-    if (wave >= kDmaWaves) {
-        act_prefetch<kRoundsH>(hb, ha, kWorkBase);
-        if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kWorkThreads>((int)threadIdx.x - kWorkBase);
-    }
+    act_prefetch<kRoundsH>(hb, ha);
+    GridRegs<kThreads> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
     const uint8_t* e = resolve_slot_word(a.D, a.rt, sw);
     const bool bad = __any(e == nullptr);
     const uint8_t* mine = (e ? e : a.D.base) + (size_t)row0 * rb;
     auto tile_ptr = [&](int m) { return read_lane_ptr(mine, m); };
-    const TileWalk<QT> T(a.n_slots, nrows, rb, a.d_ff);
-    if (wave < kDmaWaves) {
-        tiles_begin(T, stage, leads, mine, tile_ptr, wave);
-    } else {
-        if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kWorkThreads>(smem, gr, (int)threadIdx.x - kWorkBase);
-        act_quantize<kRoundsH>(hb, ha, kWorkBase);
-    }
-    tiles_finish(T, smem, stage, leads, tile_ptr, wave, a.d_ff, act, P.act_bytes, a.R, part);
+    TileRun<QT> S{TileWalk<QT>(a.n_slots, nrows, rb, a.d_ff)};
+    tiles_begin(S, tile_ptr);
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    act_quantize<kRoundsH>(hb, ha);
+    __syncthreads();
+    tiles_finish(S, tile_ptr, tabs, stage, a.d_ff, act, P.act_bytes, a.R, part);
     float* o = a.out + (size_t)t * a.d_model + row0;
     if (bad) {
         flag_error(a.err);

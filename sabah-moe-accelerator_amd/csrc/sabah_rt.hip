@@ -127,11 +127,12 @@ void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
 // LDS a workgroup may allocate (the device's limit: 160 KB on gfx950)
 int g_max_lds = 65536;
 
-// Plans above 64 KB of dynamic LDS declare their size to the runtime first.
+// Launches above 64 KB of LDS (static + dynamic) declare their dynamic size to
+// the runtime first.
 template <typename K>
-hipError_t fit_lds(K kernel, int bytes) {
-    if (bytes > g_max_lds) return hipErrorInvalidConfiguration;
-    if (bytes > 65536) {
+hipError_t fit_lds(K kernel, int bytes, int total) {
+    if (total > g_max_lds) return hipErrorInvalidConfiguration;
+    if (total > 65536) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (e != hipSuccess) return e;
@@ -198,7 +199,7 @@ bool sync_ids_enabled() {
 template <int QT>
 hipError_t launch_mmid(const MmidArgs& a, hipStream_t st) {
     const Plan P = make_plan(QT, a.k, 1, a.R * contribs_per_row(QT, a.k));
-    if (const hipError_t e = fit_lds(k_mmid<QT>, P.bytes)) return e;
+    if (const hipError_t e = fit_lds(k_mmid<QT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)a.n_ids, (unsigned)a.n_tokens);
     launch_kernel(KK_MMID, k_mmid<QT>, grid, P.bytes, st, a);
     return hipGetLastError();
@@ -217,7 +218,7 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
 template <int QT>
 hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * contribs_per_row(QT, a.d_model));
-    if (const hipError_t e = fit_lds(k_gate_up<QT>, P.bytes)) return e;
+    if (const hipError_t e = fit_lds(k_gate_up<QT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.d_ff + a.R - 1) / a.R), (unsigned)a.n_slots, (unsigned)n_tokens);
     launch_kernel(KK_GATE_UP, k_gate_up<QT>, grid, P.bytes, st, a);
     return hipGetLastError();
@@ -236,7 +237,7 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
 template <int QT>
 hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
     const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * contribs_per_row(QT, a.d_ff));
-    if (const hipError_t e = fit_lds(k_down_combine<QT>, P.bytes)) return e;
+    if (const hipError_t e = fit_lds(k_down_combine<QT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
     launch_kernel(KK_DOWN, k_down_combine<QT>, grid, P.bytes, st, a);
     return hipGetLastError();

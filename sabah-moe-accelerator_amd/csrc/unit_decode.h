@@ -86,22 +86,6 @@ struct UnitWindow {
         W[NW - 2] = W[NW - 1] = 0u;
     }
 
-    // The same window read from a tile staged in LDS (the staging area has a
-    // 16-byte guard on both sides, so no bound checks are needed).
-    __device__ inline void load_lds(const uint8_t* unit_lds) {
-        const uint8_t* o = unit_lds + ORG;
-        const int mis = (int)((reinterpret_cast<uintptr_t>(o) - 4) & 7);
-        p = 4 + mis;
-        const u32x2* g = reinterpret_cast<const u32x2*>(o - p);
-#pragma unroll
-        for (int i = 0; i < NG; ++i) {
-            const u32x2 v = g[i];
-            W[2 * i] = v.x;
-            W[2 * i + 1] = v.y;
-        }
-        W[NW - 2] = W[NW - 1] = 0u;
-    }
-
     // F[-1 .. NF-1] at static indices: select the dword shift (p >= 8), then the
     // byte shift (p & 3 in {0, 2})
     __device__ inline void fields(uint32_t (&F)[NF], uint32_t& Fm1) const {
@@ -114,6 +98,29 @@ struct UnitWindow {
         Fm1 = __builtin_amdgcn_alignbyte(V[1], V[0], sh);
 #pragma unroll
         for (int i = 0; i < NF; ++i) F[i] = __builtin_amdgcn_alignbyte(V[i + 2], V[i + 1], sh);
+    }
+};
+
+// The same fields read from a unit staged in LDS: NF + 2 dwords from the
+// dword-aligned address at or below (origin - 4), then one byte shift
+// (origin mod 4) per field.  Bytes outside the unit are read but never used.
+template <int QT>
+struct LdsWindow {
+    static constexpr int ORG = UnitFmt<QT>::ORG;
+    static constexpr int NF = UnitFmt<QT>::NF;
+    uint32_t W[NF + 2];
+    uint32_t sh;
+    __device__ inline void load(const uint8_t* unit_lds) {
+        const uintptr_t o = reinterpret_cast<uintptr_t>(unit_lds + ORG) - 4;
+        sh = (uint32_t)(o & 3);
+        const uint32_t* g = reinterpret_cast<const uint32_t*>(o & ~(uintptr_t)3);
+#pragma unroll
+        for (int i = 0; i < NF + 2; ++i) W[i] = g[i];
+    }
+    __device__ inline void fields(uint32_t (&F)[NF], uint32_t& Fm1) const {
+        Fm1 = __builtin_amdgcn_alignbyte(W[1], W[0], sh);
+#pragma unroll
+        for (int i = 0; i < NF; ++i) F[i] = __builtin_amdgcn_alignbyte(W[i + 2], W[i + 1], sh);
     }
 };
 
@@ -193,12 +200,13 @@ __device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* 
         const uint32_t Q = F[2 * ib + (l >> 1)];
         const uint32_t T = (l >> 1) ? T1 : T0;
         const uint32_t pp = 2u * (uint32_t)(l & 1);
-        // bytes [qs_g, qhbit_g, qs_g+1, qhbit_g+1] -> two 9-bit codebook indices, x4 -> byte offsets
+        // bytes [qs_g, qhbit_g, qs_g+1, qhbit_g+1] -> two 9-bit codebook indices
         const uint32_t sel = (4u + pp) | (pp << 8) | ((5u + pp) << 16) | ((pp + 1u) << 24);
-        const uint32_t D = __builtin_amdgcn_perm(Q, T, sel) << 2;
-        const uint32_t g0 = lds_u32(smem, kLdsGrid + (D & 0xFFFFu));
-        const uint32_t g1 = lds_u32(smem, kLdsGrid + (D >> 16));
-        const uint4 sm = *reinterpret_cast<const uint4*>(smem + kLdsSign + 16u * ((S >> (8 * l)) & 0xFFu));
+        // each byte offset is one shift of a 16-bit or 8-bit field (one SDWA op)
+        const uint32_t D = __builtin_amdgcn_perm(Q, T, sel);
+        const uint32_t g0 = lds_u32(smem, kLdsGrid + ((D & 0xFFFFu) << 2));
+        const uint32_t g1 = lds_u32(smem, kLdsGrid + ((D >> 16) << 2));
+        const uint4 sm = *reinterpret_cast<const uint4*>(smem + kLdsSign + (((S >> (8 * l)) & 0xFFu) << 4));
         v[2 * l] = (g0 ^ sm.x) + sm.y;
         v[2 * l + 1] = (g1 ^ sm.z) + sm.w;
     }
@@ -278,8 +286,8 @@ struct UnitDot {
     float c[UnitFmt<QT>::CONTRIB];
 };
 
-template <int QT>
-__device__ inline UnitDot<QT> unit_dot(const UnitWindow<QT>& Wn, const uint8_t* smem, const uint8_t* chunk,
+template <int QT, typename Window>
+__device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, const uint8_t* chunk,
                                        const float* dx, const int16_t* bs) {
     uint32_t F[UnitFmt<QT>::NF];
     uint32_t Fm1;
