@@ -32,13 +32,34 @@ struct Routing {
     int n_experts;
 };
 
+// Ids and pointer tables are read through the constant address space: they
+// do not change during a kernel, and a workgroup-uniform read then becomes a
+// scalar load, which has its own counter (waiting for it never waits for the
+// vector loads issued before it).
+typedef __attribute__((address_space(4))) const int32_t c_int32;
+typedef __attribute__((address_space(4))) const uint64_t c_uint64;
+
+// A wave-uniform value pinned to a scalar register.  (Values that went
+// through a division or another vector op otherwise stay in vector registers,
+// and so does everything computed from them.)
+__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// a wave-uniform pointer held in scalar registers
+template <typename T>
+__device__ inline T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 __device__ inline int read_id(const Routing& R, int t, int s) {
-    return *reinterpret_cast<const int32_t*>(R.ids + (size_t)t * R.token_stride + (size_t)s * R.id_stride);
+    return *(c_int32*)uniform_ptr(R.ids + (size_t)t * R.token_stride + (size_t)s * R.id_stride);
 }
 
 // expert matrix of (token t, slot s), or nullptr for an id outside [0, n_experts)
 __device__ inline const uint8_t* expert_ptr(const ExpertSrc& E, const Routing& R, int t, int s, int n_slots) {
-    if (E.ptrs) return reinterpret_cast<const uint8_t*>(E.ptrs[(size_t)t * n_slots + s]);
+    if (E.ptrs) return reinterpret_cast<const uint8_t*>(*(c_uint64*)uniform_ptr(E.ptrs + (size_t)t * n_slots + s));
     const int e = R.ids ? read_id(R, t, s) : 0;
     if (e < 0 || e >= R.n_experts) return nullptr;
     return E.base + (size_t)e * E.expert_stride;
@@ -193,10 +214,14 @@ __device__ inline float row_sum(const float* part_row, int n) {
     return s;
 }
 
-// floor(a / b) for 0 <= a < 2^20 and a / b < 2^12, given r = rcp(b):
-// (a + 0.5) / b is at least 0.5 / b away from an integer, far more than the
-// rounding error of the product
+// floor(a / b) for 0 <= a < 2^21, given r = rcp(b) (v_rcp_f32, 1 ulp): the
+// product's relative error stays below 2^-22, so its absolute error is below
+// (a + 0.5) / b * 2^-22 < 0.5 / b, while (a + 0.5) / b is at least 0.5 / b
+// away from an integer
 __device__ inline int div_small(int a, float r) { return (int)(((float)a + 0.5f) * r); }
+// the same for wave-uniform operands, returned as a scalar
+__device__ inline int div_small_u(int a, float r) { return __builtin_amdgcn_readfirstlane(div_small(a, r)); }
+__device__ inline int div_small_u(int a, int b) { return div_small_u(a, __builtin_amdgcn_rcpf((float)b)); }
 
 // One workgroup's tiles.  Tile t is matrix tile_ptr(t) from its first row on
 // (row0 already folded into the pointer): `nrows` rows of k elements at rb
@@ -208,25 +233,35 @@ struct TileWalk {
     size_t rb;
     float rcp_nus;
     __device__ TileWalk(int n_mat_, int nrows, size_t rb_, int k)
-        : n_mat(n_mat_), NUS(units_per_row(QT, k)), NCB(contribs_per_row(QT, k)), total(nrows * NUS),
-          V(pass_units(n_mat_, UB)), rb(rb_), rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
+        : n_mat(uni(n_mat_)), NUS(uni(units_per_row(QT, k))), NCB(uni(contribs_per_row(QT, k))),
+          total(uni(nrows * units_per_row(QT, k))), V(uni(pass_units(n_mat_, UB))), rb(rb_),
+          rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
     __device__ int byte_of(int v) const {
         const int r = div_small(v, rcp_nus);
+        return (int)((size_t)r * rb) + (v - r * NUS) * UB;
+    }
+    // the same for a wave-uniform v, returned as a scalar
+    __device__ int byte_of_u(int v) const {
+        const int r = div_small_u(v, rcp_nus);
         return (int)((size_t)r * rb) + (v - r * NUS) * UB;
     }
 };
 
 // One wave-round: units [ua, ua + nu) of the pass (tile-major, nv units per
 // tile), as up to kMaxPieces tile pieces.  All fields are wave-uniform.
+// The round's 16-byte chunks are numbered across its pieces: chunk q of
+// piece p is read from gbase + goff[p] + 16 q and staged at lb[p] + 16 q.
 struct WaveRound {
     int np, nu, nch;                 // pieces, units, chunks
     int t[kMaxPieces];               // tile of piece p
     int upre[kMaxPieces];            // units before piece p
     int vb[kMaxPieces];              // pass-relative unit of the piece's first unit, minus upre
-    int cpre[kMaxPieces];            // chunks before piece p
     int lead[kMaxPieces];            // tile's pass start address mod 16
-    const uint8_t* gb[kMaxPieces];   // global address of the piece's chunk q is gb + 16 q
-    int lb[kMaxPieces];              // staging offset of the piece's chunk q is lb + 16 q
+    int cpre[kMaxPieces];            // chunks before piece p
+    int lb[kMaxPieces];
+    long long goff[kMaxPieces];
+    const uint8_t* gbase;
+    bool near;                       // every goff fits in 32 bits (pieces of one tensor)
 };
 
 template <int QT, typename TilePtr>
@@ -234,24 +269,29 @@ __device__ inline WaveRound make_round(const TileWalk<QT>& T, TilePtr tile_ptr, 
                                        int ub) {
     WaveRound W{};
     W.nu = ub - ua;
-    const int b0 = T.byte_of(v0);
-    const int t0 = ua / nv;
+    const int b0 = T.byte_of_u(v0);
+    const int t0 = div_small_u(ua, nv);
     int u = ua, c = 0, np = 0;
+    bool near = true;
 #pragma unroll
     for (int p = 0; p < kMaxPieces; ++p) {      // static indices: the fields stay in registers
         const int t = t0 + p;
         const bool live = u < ub;
         const int va = u - t * nv, vbnd = min(ub, (t + 1) * nv) - t * nv;
-        const int xa = T.byte_of(v0 + va) - b0, xb = T.byte_of(v0 + vbnd) - b0;
-        const uint8_t* P = tile_ptr(live ? t : t0) + b0;
+        const int xa = T.byte_of_u(v0 + va) - b0, xb = T.byte_of_u(v0 + vbnd) - b0;
+        const uint8_t* P = uniform_ptr(tile_ptr(live ? t : t0) + b0);
         const int lead = (int)(reinterpret_cast<uintptr_t>(P) & 15);
         const int c_lo = (lead + xa) >> 4, c_hi = (lead + xb - 1) >> 4;
+        const uint8_t* g = P - lead + 16 * (c_lo - c);
+        if (p == 0) W.gbase = g;
+        const long long off = (long long)(g - W.gbase);
+        near = near && off == (long long)(int)off;
         W.t[p] = t;
         W.upre[p] = u - ua;
         W.vb[p] = va - (u - ua);
-        W.cpre[p] = c;
         W.lead[p] = lead;
-        W.gb[p] = P - lead + 16 * (c_lo - c);
+        W.cpre[p] = c;
+        W.goff[p] = off;
         W.lb[p] = 16 * (cpt * t + c_lo - c);
         if (live) {
             c += c_hi - c_lo + 1;
@@ -259,8 +299,9 @@ __device__ inline WaveRound make_round(const TileWalk<QT>& T, TilePtr tile_ptr, 
             ++np;
         }
     }
-    W.np = np;
-    W.nch = c;
+    W.np = uni(np);
+    W.nch = uni(c);
+    W.near = near;
     return W;
 }
 
@@ -278,29 +319,44 @@ __device__ inline V pick(const V (&a)[kMaxPieces], const int (&pre)[kMaxPieces],
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Loads of a wave-round: each lane issues exactly StageIters loads (a static
+// count, so waits for older loads stay exact); lane L's load `it` reads chunk
+// 64 it + L of the round, and lanes past the last chunk re-read it.
 template <int QT>
 struct RoundRegs {
-    u32x4 d[StageIters<QT>::V];
-    int lds[StageIters<QT>::V];
+    static constexpr int N = StageIters<QT>::V;
+    u32x4 d[N];
+    int lds[N];
 };
 
-// issue the wave-round's chunk loads (a static number per lane)
 template <int QT>
 __device__ inline void round_load(const WaveRound& W, RoundRegs<QT>& R) {
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
     const int lane = (int)(threadIdx.x & 63u);
+    if (W.near) {                        // the usual case: 32-bit offsets from one base
+        int off32[kMaxPieces];
 #pragma unroll
-    for (int it = 0; it < StageIters<QT>::V; ++it) {
-        const int q = min(64 * it + lane, W.nch - 1);
-        R.d[it] = *(g_u32x4*)(pick(W.gb, W.cpre, W.np, q) + 16 * q);
-        R.lds[it] = pick(W.lb, W.cpre, W.np, q) + 16 * q;
+        for (int j = 0; j < kMaxPieces; ++j) off32[j] = (int)W.goff[j];
+#pragma unroll
+        for (int it = 0; it < RoundRegs<QT>::N; ++it) {
+            const int q = min(64 * it + lane, W.nch - 1);
+            R.d[it] = *(g_u32x4*)(W.gbase + pick(off32, W.cpre, W.np, q) + 16 * q);
+            R.lds[it] = pick(W.lb, W.cpre, W.np, q) + 16 * q;
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < RoundRegs<QT>::N; ++it) {
+            const int q = min(64 * it + lane, W.nch - 1);
+            R.d[it] = *(g_u32x4*)(W.gbase + pick(W.goff, W.cpre, W.np, q) + 16 * q);
+            R.lds[it] = pick(W.lb, W.cpre, W.np, q) + 16 * q;
+        }
     }
 }
 
 template <int QT>
 __device__ inline void round_store(uint8_t* stage, const RoundRegs<QT>& R) {
 #pragma unroll
-    for (int it = 0; it < StageIters<QT>::V; ++it) *reinterpret_cast<u32x4*>(stage + R.lds[it]) = R.d[it];
+    for (int it = 0; it < RoundRegs<QT>::N; ++it) *reinterpret_cast<u32x4*>(stage + R.lds[it]) = R.d[it];
 }
 
 // decode the wave-round's units, one per lane; contributions of unit
@@ -314,7 +370,7 @@ __device__ inline void round_decode(const TileWalk<QT>& T, const WaveRound& W, i
     const int t = pick(W.t, W.upre, W.np, i);
     const int v = v0 + pick(W.vb, W.upre, W.np, i) + i;   // tile-relative unit (row-major over the rows)
     const int r = div_small(v, T.rcp_nus), us = v - r * T.NUS;
-    const int b0 = T.byte_of(v0);
+    const int b0 = T.byte_of_u(v0);
     LdsWindow<QT> Wn;
     Wn.load(stage + 16 * cpt * t + pick(W.lead, W.upre, W.np, i) + (int)((size_t)r * T.rb) + us * TileWalk<QT>::UB - b0);
     unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, part + (t * part_rows + r) * T.NCB);
@@ -334,10 +390,10 @@ struct TileRun {
 
 template <int QT>
 __device__ inline void set_pass(TileRun<QT>& S, int v0) {
-    S.nv = min(S.T.V, S.T.total - v0);
-    S.cpt = tile_chunks(S.T.byte_of(v0 + S.nv) - S.T.byte_of(v0));
-    S.Q = min(kWaveUnits, 3 * S.nv);
-    S.n_rounds = (S.T.n_mat * S.nv + S.Q - 1) / S.Q;
+    S.nv = uni(min(S.T.V, S.T.total - v0));
+    S.cpt = uni(tile_chunks(S.T.byte_of_u(v0 + S.nv) - S.T.byte_of_u(v0)));
+    S.Q = uni(min(kWaveUnits, 3 * S.nv));
+    S.n_rounds = div_small_u(S.T.n_mat * S.nv + S.Q - 1, S.Q);
 }
 
 // Every wave issues its first wave-round's loads, also a wave with no units

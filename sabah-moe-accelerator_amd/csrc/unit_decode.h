@@ -110,10 +110,12 @@ struct LdsWindow {
     static constexpr int NF = UnitFmt<QT>::NF;
     uint32_t W[NF + 2];
     uint32_t sh;
+    // the address stays derived from the LDS pointer (no integer round trip),
+    // so the reads are LDS instructions, not flat ones
     __device__ inline void load(const uint8_t* unit_lds) {
-        const uintptr_t o = reinterpret_cast<uintptr_t>(unit_lds + ORG) - 4;
-        sh = (uint32_t)(o & 3);
-        const uint32_t* g = reinterpret_cast<const uint32_t*>(o & ~(uintptr_t)3);
+        const uint8_t* o = unit_lds + ORG - 4;
+        sh = (uint32_t)(reinterpret_cast<uintptr_t>(o) & 3);
+        const uint32_t* g = reinterpret_cast<const uint32_t*>(o - sh);
 #pragma unroll
         for (int i = 0; i < NF + 2; ++i) W[i] = g[i];
     }
@@ -129,21 +131,19 @@ __device__ inline float h2f(uint32_t bits16) { return __half2float(__ushort_as_h
 __device__ inline int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 // ---------------------------------------------------------------------------
-// LDS tables for IQ3_S
-//   grid  512 x u32 at LDS byte 0     (expanded codebook)
-//   sgn   256 x u32x4 at LDS byte 2048: for sign byte b, {m(lo), t(lo), m(hi), t(hi)}
-//         with t(n) = nibble bits spread to bytes (0x01), m(n) = t * 0xFF, so
-//         (mag ^ m) + t negates exactly the bytes whose sign bit is set
+// LDS table for IQ3_S: the 512-entry codebook (u32: four 3-bit levels
+// expanded to bytes) at LDS byte 0.  Signs are applied in registers: for a
+// sign nibble n, t = n's bits spread to bytes (0x01) and m = t * 0xFF, so
+// (mag ^ m) + t negates exactly the bytes whose sign bit is set (magnitudes
+// are odd and below 128, so no byte carries into the next).
 // ---------------------------------------------------------------------------
 constexpr int kLdsGrid = 0;
-constexpr int kLdsSign = 2048;
-constexpr int kLdsTables = 2048 + 4096;
+constexpr int kLdsTables = 2048;
 
 __device__ inline uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
 
-// The IQ3_S tables in LDS, built by NT threads (w = 0 .. NT-1 of them):
-// the 512-entry codebook (loaded early into registers, written later) and
-// the 256-entry sign table (computed).
+// The IQ3_S codebook in LDS, written by NT threads (w = 0 .. NT-1 of them)
+// from registers loaded early.
 template <int NT>
 struct GridRegs {
     uint32_t e[512 / NT];
@@ -158,15 +158,8 @@ __device__ inline GridRegs<NT> load_grid_regs(int w) {
 template <int NT>
 __device__ inline void store_iq3s_tables(uint8_t* smem, const GridRegs<NT>& g, int w) {
     uint32_t* grid = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
-    uint4* sgn = reinterpret_cast<uint4*>(smem + kLdsSign);
 #pragma unroll
     for (int i = 0; i < 512 / NT; ++i) grid[w + NT * i] = g.e[i];
-#pragma unroll
-    for (int i = 0; i < 256 / NT; ++i) {
-        const uint32_t b = (uint32_t)(w + NT * i);
-        const uint32_t tl = spread4(b & 15u), th = spread4(b >> 4);
-        sgn[b] = make_uint4(tl * 0xFFu, tl, th * 0xFFu, th);
-    }
 }
 // all 256 threads of the workgroup
 __device__ inline void stage_iq3s_tables(uint8_t* smem) {
@@ -206,9 +199,9 @@ __device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* 
         const uint32_t D = __builtin_amdgcn_perm(Q, T, sel);
         const uint32_t g0 = lds_u32(smem, kLdsGrid + ((D & 0xFFFFu) << 2));
         const uint32_t g1 = lds_u32(smem, kLdsGrid + ((D >> 16) << 2));
-        const uint4 sm = *reinterpret_cast<const uint4*>(smem + kLdsSign + (((S >> (8 * l)) & 0xFFu) << 4));
-        v[2 * l] = (g0 ^ sm.x) + sm.y;
-        v[2 * l + 1] = (g1 ^ sm.z) + sm.w;
+        const uint32_t t0 = spread4((S >> (8 * l)) & 15u), t1 = spread4((S >> (8 * l + 4)) & 15u);
+        v[2 * l] = (g0 ^ (t0 * 0xFFu)) + t0;
+        v[2 * l + 1] = (g1 ^ (t1 * 0xFFu)) + t1;
     }
     return 2 * (int)((F[26] >> (4 * ib)) & 15u) + 1;
 }
