@@ -41,6 +41,8 @@ __device__ inline uint32_t row16_min(uint32_t v) {
     return v;
 }
 
+__device__ inline int sdot4_i8(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
 __device__ inline uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
            ((uint32_t)(d & 0xff) << 24);
@@ -51,41 +53,77 @@ struct Act16 {
     float v[16];
 };
 
+__device__ inline float row16_min(float v) {
+    v = fminf(v, __uint_as_float(dpp<kDppXor1>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(dpp<kDppXor2>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(v))));
+    v = fminf(v, __uint_as_float(dpp<kDppMirror>(__float_as_uint(v))));
+    return v;
+}
+
+// ggml's nearest_int: v + 1.5 * 2^23 rounds v to an integer (nearest, ties
+// to even) for |v| < 2^22, leaving it in the low mantissa bits; the float's
+// bits are then 0x4B400000 + nearest_int(v), so the low byte is the int8.
+constexpr float kRoundMagic = 12582912.0f;
+constexpr uint32_t kRoundMagicBits = 0x4B400000u;
+
+// bytes 0 of a, b, c, d -> one dword (a in byte 0)
+__device__ inline uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0C0C0400u);   // [a.0, b.0, 0, 0]
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000C0Cu);   // [0, 0, c.0, d.0]
+    return ab | cd;
+}
+
 // Quantise the chunk held by one 16-lane row (lane l holds elements 16l..16l+15)
 // into act (the row's ActLayout block), chunk index c.
+//
+// The scale comes from the first element of largest magnitude, with its sign.
+// Unless both +amax and -amax occur in the chunk, that sign is the sign of
+// whichever of the chunk's maximum and minimum reaches amax; only a chunk
+// holding both looks for the first one by index.  |iscale * x| <= 127 (1 + 2^-22)
+// rounds to at most 127, so ggml's clamp at 127 never applies.
 __device__ inline void row16_quant_q8K(const Act16& a, int c, uint8_t* act, const ActLayout& L) {
     const uint32_t l = threadIdx.x & 15u;
-    float amax_l = 0.0f;
+    float mx_l = a.v[0], mn_l = a.v[0];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) amax_l = fmaxf(amax_l, fabsf(a.v[j]));
-    const float amax = row16_max(amax_l);
-    // first element whose magnitude is amax, with its sign: key = index << 1 | sign
-    uint32_t key = 0xFFFFFFFFu;
+    for (int j = 1; j < 16; ++j) {
+        mx_l = fmaxf(mx_l, a.v[j]);
+        mn_l = fminf(mn_l, a.v[j]);
+    }
+    const float rmax = row16_max(mx_l), rmin = row16_min(mn_l);
+    const float amax = fmaxf(rmax, -rmin);
+    float mx = rmax == amax ? amax : -amax;
+    if (rmax == amax && rmin == -amax && amax != 0.0f) {     // both signs reach amax: the first one decides
+        uint32_t key = 0xFFFFFFFFu;
 #pragma unroll
-    for (int j = 15; j >= 0; --j)
-        if (fabsf(a.v[j]) == amax) key = ((16u * l + (uint32_t)j) << 1) | (__float_as_uint(a.v[j]) >> 31);
-    key = row16_min(key);
-    int q[16];
+        for (int j = 15; j >= 0; --j)
+            if (fabsf(a.v[j]) == amax) key = ((16u * l + (uint32_t)j) << 1) | (__float_as_uint(a.v[j]) >> 31);
+        key = row16_min(key);
+        mx = (key & 1u) ? -amax : amax;
+    }
+    uint32_t b[16];
     float d = 0.0f;
     if (amax != 0.0f) {
-        const float mx = (key & 1u) ? -amax : amax;          // the first max's signed value
         const float iscale = __fdiv_rn(-127.0f, mx);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = min(127, (int)rintf(__fmul_rn(iscale, a.v[j])));
+        for (int j = 0; j < 16; ++j) b[j] = __float_as_uint(__fadd_rn(__fmul_rn(iscale, a.v[j]), kRoundMagic));
         d = __fdiv_rn(1.0f, iscale);
     } else {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = 0;
+        for (int j = 0; j < 16; ++j) b[j] = kRoundMagicBits;
     }
     uint4 packed;
-    packed.x = pack4_i8(q[0], q[1], q[2], q[3]);
-    packed.y = pack4_i8(q[4], q[5], q[6], q[7]);
-    packed.z = pack4_i8(q[8], q[9], q[10], q[11]);
-    packed.w = pack4_i8(q[12], q[13], q[14], q[15]);
+    packed.x = low_bytes4(b[0], b[1], b[2], b[3]);
+    packed.y = low_bytes4(b[4], b[5], b[6], b[7]);
+    packed.z = low_bytes4(b[8], b[9], b[10], b[11]);
+    packed.w = low_bytes4(b[12], b[13], b[14], b[15]);
     reinterpret_cast<uint4*>(act + c * kActChunkStride)[l] = packed;
+    // bsum = sum of the sixteen int8 values
     int s = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s += q[j];
+    s = sdot4_i8(packed.x, 0x01010101u, s);
+    s = sdot4_i8(packed.y, 0x01010101u, s);
+    s = sdot4_i8(packed.z, 0x01010101u, s);
+    s = sdot4_i8(packed.w, 0x01010101u, s);
     reinterpret_cast<int16_t*>(act + L.off_bsum)[c * 16 + l] = (int16_t)s;
     if (l == 0) reinterpret_cast<float*>(act + L.off_d)[c] = d;
 }

@@ -93,3 +93,28 @@ def random_blocks(rng, qt: int, n_rows: int, k: int) -> np.ndarray:
     elif qt == 14:                          # Q6_K: d at 208
         raw[:, :, 208:210] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
     return raw.reshape(n_rows, nb * bb)
+
+
+def unfused_rounding_row(k: int, amax: float = 3.0) -> np.ndarray:
+    """A row of k fp32 values (k a multiple of 256) whose q8_K bytes depend on
+    rounding the product iscale*x before ggml's round-to-int add: each 256-block
+    opens with +amax (so iscale = fl(-127/amax)), then holds values x for which
+    rint(fl(iscale*x)) != rint(iscale*x) (exact).  A fused multiply-add gets
+    every one of them wrong by one."""
+    iscale = np.float32(-127.0) / np.float32(amax)
+    hits = []
+    for h in np.arange(-126.5, 127.0, 1.0):
+        c0 = np.float32(h / float(iscale))
+        for c in (np.nextafter(c0, np.float32(-9), dtype=np.float32), c0, np.nextafter(c0, np.float32(9), dtype=np.float32)):
+            if not abs(c) < amax:
+                continue
+            exact = float(iscale) * float(c)          # 24 x 24 bits: exact in float64
+            if np.rint(np.float32(iscale * c)) != np.rint(exact):
+                hits.append(c)
+    assert len(hits) >= 32, len(hits)
+    per = 255
+    row = np.empty(k, np.float32)
+    for b in range(k // 256):
+        row[256 * b] = amax
+        row[256 * b + 1:256 * (b + 1)] = [hits[(b * per + i) % len(hits)] for i in range(per)]
+    return row

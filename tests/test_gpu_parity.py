@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_parity, random_blocks
+from helpers import assert_parity, random_blocks, unfused_rounding_row
 
 pytestmark = pytest.mark.gpu
 
@@ -62,6 +62,7 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
     x[5] = 0.75                                             # constant row
     x[6, ::2] = 0.0
     x[7] *= 1e4
+    x[8] = unfused_rounding_row(k)                          # q8_K bytes that a fused multiply-add changes
     ab = orc.act_row_bytes(qt, k)
     y = torch.zeros(9, ab, dtype=torch.uint8, device=DEV)
     hip_rt.check(hip_rt.lib().sabah_quantize_act(vp(T(x)), vp(y), qt, 9, k, stream()), "quantize_act")

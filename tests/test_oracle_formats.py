@@ -10,7 +10,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from helpers import dequant_act, f16, max_rel, random_blocks
+from helpers import dequant_act, f16, max_rel, random_blocks, unfused_rounding_row
 
 Q8_0, Q4_K, Q6_K, Q8_K, IQ3_S = 8, 12, 14, 15, 21
 
@@ -181,6 +181,18 @@ def test_q8_K_constant_zero_block_and_bsums(orc):
     q = y[4:260].view(np.int8).astype(np.int64)
     assert np.array_equal(y[260:292].view(np.int16), q.reshape(16, 16).sum(axis=1))
     assert np.abs(q).max() == 127
+
+
+def test_q8_K_rounds_the_product_before_the_round_to_int_add(orc):
+    # ggml's nearest_int(iscale * x): the product is an fp32 value of its own,
+    # so values whose exact product rounds the other way stay on the fp32 side.
+    x = unfused_rounding_row(256)
+    y = orc.quantize_q8_K(x)
+    iscale = np.float32(-127.0) / np.float32(3.0)
+    q = y[4:260].view(np.int8).astype(np.int64)
+    assert np.array_equal(q, np.rint(iscale * x).astype(np.int64))          # fp32 product, RNE
+    fused = np.rint(x.astype(np.float64) * float(iscale)).astype(np.int64)  # one rounding
+    assert np.all(fused[1:] != q[1:])
 
 
 # ---------------------------------------------------------------------------
