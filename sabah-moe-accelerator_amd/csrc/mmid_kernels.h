@@ -95,40 +95,47 @@ __device__ inline void flag_error(unsigned int* err) {
 // [row0, row0 + nrows) of n_mat expert matrices (gate and up; the routed
 // slots' down matrices; one matrix for MUL_MAT_ID), or single rows when rows
 // are not packed.  Every tile holds the same number of units, in row-major
-// unit order, at contiguous bytes.  The workgroup walks them in passes of V
+// unit order, at contiguous bytes.  The workgroup walks them in passes of nv
 // units per tile; a pass's tiles are staged in LDS, tile t at 16 * cpt * t,
 // starting `lead` (its HBM address mod 16) bytes into its first 16-byte
 // chunk, so staged bytes keep their HBM alignment mod 16.
 //
-// Within a pass every wave works on its own: wave-round j (wave j % 4) owns
-// Q consecutive units of the pass (tile-major numbering), loads the 16-byte
-// chunks covering them into registers (lanes read consecutive chunks, so a
-// load instruction of a wave reads 1 KB of contiguous HBM), writes them to
-// their place in LDS and decodes its units - no workgroup barrier stands
-// between a wave's data arriving and its decode.  A wave-round spans at most
-// kMaxPieces tiles (Q <= 3 * units per tile).  Each lane issues exactly
-// StageIters<QT> loads (a static count, so waits for older loads stay
-// exact); lanes past the last chunk re-load it.  Chunks at the edge of two
-// wave-rounds are written by both, with the same bytes.
+// Loads: each tile has LPT = kThreads / n_mat lanes, and lane j of a tile
+// reads the tile's chunks j, j + LPT, j + 2 LPT, ... - exactly StageIters
+// of them (a static count, so waits for older loads stay exact): a lane past
+// the tile's last chunk re-reads it, and lanes beyond n_mat * LPT re-read the
+// last tile's chunks.  Consecutive lanes read consecutive chunks, so a load
+// instruction of a wave reads up to 1 KB of contiguous HBM.  The load plan
+// is a few integer operations per lane.  Once every lane has written its
+// chunks to LDS and the workgroup has synchronised, lane g decodes units g,
+// g + kThreads, ... of the pass (tile-major numbering).  The next pass's
+// loads are issued before the current pass is decoded.
 // ---------------------------------------------------------------------------
 constexpr int kStageChunks = 2048;                            // 32 KB per workgroup
 constexpr int kStageBytes = 16 * kStageChunks;
 constexpr int kStageGuard = 16;
 constexpr int kMaxTiles = 64;
-constexpr int kMaxPieces = 4;
-constexpr int kWaveUnits = 64;
+
+// 16-byte loads per lane per pass
+__host__ __device__ constexpr int stage_iters(int qt) {
+    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : 9;
+}
+template <int QT>
+struct StageIters {
+    static constexpr int V = stage_iters(QT);
+};
 
 // chunks of a tile of tile_bytes at any lead
 __host__ __device__ inline int tile_chunks(int tile_bytes) { return (tile_bytes + 30) / 16; }
-// units per tile per pass: the largest V with n_mat * tile_chunks(V * unit bytes) <= kStageChunks
-__host__ __device__ inline int pass_units(int n_mat, int unit_bytes) {
-    return max(1, (16 * (kStageChunks / n_mat) - 30) / unit_bytes);
+// chunks one tile may stage per pass: its share of the stage, and no more
+// than its lanes load
+__host__ __device__ inline int tile_chunk_cap(int qt, int n_mat) {
+    return min(kStageChunks / n_mat, stage_iters(qt) * (kThreads / n_mat));
 }
-// 16-byte loads per lane per wave-round: enough for kWaveUnits units over kMaxPieces tiles
-template <int QT>
-struct StageIters {
-    static constexpr int V = ((kWaveUnits * UnitFmt<QT>::BYTES + 30 * kMaxPieces + 15) / 16 + 63) / 64;
-};
+// units per tile per pass: the largest V with tile_chunks(V * unit bytes) <= tile_chunk_cap
+__host__ __device__ inline int pass_units(int qt, int n_mat, int unit_bytes) {
+    return max(1, (16 * tile_chunk_cap(qt, n_mat) - 30) / unit_bytes);
+}
 
 // Q8_0 rows need only be whole 32-element blocks: their last unit may hold 1..3 blocks
 __host__ __device__ inline int units_per_row(int qt, int k) { return qt == QT_Q8_0 ? (k + 127) / 128 : k / 256; }
@@ -140,7 +147,7 @@ __host__ __device__ inline int unit_bytes(int qt) { return qt == QT_Q8_0 ? 136 :
 __host__ __device__ inline int rows_per_wg(int qt, int k, int n_mat) {
     const int nus = units_per_row(qt, k);
     const int by_lanes = kThreads / (n_mat * nus);
-    const int by_stage = (16 * (kStageChunks / n_mat) - 30) / (int)row_bytes(qt, k);
+    const int by_stage = (16 * tile_chunk_cap(qt, n_mat) - 30) / (int)row_bytes(qt, k);
     return max(1, min(by_lanes, by_stage));
 }
 
@@ -166,17 +173,19 @@ __host__ __device__ inline Plan make_plan(int qt, int k, int n_act, int n_part) 
     return p;
 }
 
-// static LDS of a kernel instantiation: IQ3_S tables, then the staging area
+// static LDS of a kernel instantiation: IQ3_S tables, the staged tiles'
+// leads, then the staging area with a guard on each side
 template <int QT>
 struct StaticLds {
     static constexpr int TABLES = (QT == QT_IQ3_S) ? kLdsTables : 0;
-    static constexpr int STAGE = TABLES + kStageGuard;
+    static constexpr int LEADS = TABLES;
+    static constexpr int STAGE = LEADS + 4 * kMaxTiles + kStageGuard;
     static constexpr int BYTES = STAGE + kStageBytes + kStageGuard;
 };
 // total LDS of a launch (static + dynamic), for the host's limit check
 __host__ inline int launch_lds(int qt, const Plan& P) {
     const int tables = (qt == QT_IQ3_S) ? kLdsTables : 0;
-    return tables + 2 * kStageGuard + kStageBytes + P.bytes;
+    return tables + 4 * kMaxTiles + 2 * kStageGuard + kStageBytes + P.bytes;
 }
 
 // bytes of unit us of a row of k elements
@@ -234,7 +243,7 @@ struct TileWalk {
     float rcp_nus;
     __device__ TileWalk(int n_mat_, int nrows, size_t rb_, int k)
         : n_mat(uni(n_mat_)), NUS(uni(units_per_row(QT, k))), NCB(uni(contribs_per_row(QT, k))),
-          total(uni(nrows * units_per_row(QT, k))), V(uni(pass_units(n_mat_, UB))), rb(rb_),
+          total(uni(nrows * units_per_row(QT, k))), V(uni(pass_units(QT, n_mat_, UB))), rb(rb_),
           rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
     __device__ int byte_of(int v) const {
         const int r = div_small(v, rcp_nus);
@@ -247,207 +256,112 @@ struct TileWalk {
     }
 };
 
-// One wave-round: units [ua, ua + nu) of the pass (tile-major, nv units per
-// tile), as up to kMaxPieces tile pieces.  All fields are wave-uniform.
-// The round's 16-byte chunks are numbered across its pieces: chunk q of
-// piece p is read from gbase + goff[p] + 16 q and staged at lb[p] + 16 q.
-struct WaveRound {
-    int np, nu, nch;                 // pieces, units, chunks
-    int t[kMaxPieces];               // tile of piece p
-    int upre[kMaxPieces];            // units before piece p
-    int vb[kMaxPieces];              // pass-relative unit of the piece's first unit, minus upre
-    int lead[kMaxPieces];            // tile's pass start address mod 16
-    int cpre[kMaxPieces];            // chunks before piece p
-    int lb[kMaxPieces];
-    long long goff[kMaxPieces];
-    const uint8_t* gbase;
-    bool near;                       // every goff fits in 32 bits (pieces of one tensor)
-};
-
-template <int QT, typename TilePtr>
-__device__ inline WaveRound make_round(const TileWalk<QT>& T, TilePtr tile_ptr, int v0, int nv, int cpt, int ua,
-                                       int ub) {
-    WaveRound W{};
-    W.nu = ub - ua;
-    const int b0 = T.byte_of_u(v0);
-    const int t0 = div_small_u(ua, nv);
-    int u = ua, c = 0, np = 0;
-    bool near = true;
-#pragma unroll
-    for (int p = 0; p < kMaxPieces; ++p) {      // static indices: the fields stay in registers
-        const int t = t0 + p;
-        const bool live = u < ub;
-        const int va = u - t * nv, vbnd = min(ub, (t + 1) * nv) - t * nv;
-        const int xa = T.byte_of_u(v0 + va) - b0, xb = T.byte_of_u(v0 + vbnd) - b0;
-        const uint8_t* P = uniform_ptr(tile_ptr(live ? t : t0) + b0);
-        const int lead = (int)(reinterpret_cast<uintptr_t>(P) & 15);
-        const int c_lo = (lead + xa) >> 4, c_hi = (lead + xb - 1) >> 4;
-        const uint8_t* g = P - lead + 16 * (c_lo - c);
-        if (p == 0) W.gbase = g;
-        const long long off = (long long)(g - W.gbase);
-        near = near && off == (long long)(int)off;
-        W.t[p] = t;
-        W.upre[p] = u - ua;
-        W.vb[p] = va - (u - ua);
-        W.lead[p] = lead;
-        W.cpre[p] = c;
-        W.goff[p] = off;
-        W.lb[p] = 16 * (cpt * t + c_lo - c);
-        if (live) {
-            c += c_hi - c_lo + 1;
-            u += vbnd - va;
-            ++np;
-        }
-    }
-    W.np = uni(np);
-    W.nch = uni(c);
-    W.near = near;
-    return W;
-}
-
-// The field of the piece that holds chunk (or unit) x, given the pieces'
-// chunk (or unit) prefixes: a chain of selects on the prefix comparisons.
-// (Selecting on a computed piece index instead lets the optimizer turn the
-// chain back into an indexed array, which then lives in scratch memory.)
-template <typename V>
-__device__ inline V pick(const V (&a)[kMaxPieces], const int (&pre)[kMaxPieces], int np, int x) {
-    V r = a[0];
-#pragma unroll
-    for (int j = 1; j < kMaxPieces; ++j) r = (j < np && x >= pre[j]) ? a[j] : r;
-    return r;
-}
-
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// Loads of a wave-round: each lane issues exactly StageIters loads (a static
-// count, so waits for older loads stay exact); lane L's load `it` reads chunk
-// 64 it + L of the round, and lanes past the last chunk re-read it.
-template <int QT>
-struct RoundRegs {
-    static constexpr int N = StageIters<QT>::V;
-    u32x4 d[N];
-    int lds[N];
-};
-
-template <int QT>
-__device__ inline void round_load(const WaveRound& W, RoundRegs<QT>& R) {
-    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
-    const int lane = (int)(threadIdx.x & 63u);
-    if (W.near) {                        // the usual case: 32-bit offsets from one base
-        int off32[kMaxPieces];
-#pragma unroll
-        for (int j = 0; j < kMaxPieces; ++j) off32[j] = (int)W.goff[j];
-#pragma unroll
-        for (int it = 0; it < RoundRegs<QT>::N; ++it) {
-            const int q = min(64 * it + lane, W.nch - 1);
-            R.d[it] = *(g_u32x4*)(W.gbase + pick(off32, W.cpre, W.np, q) + 16 * q);
-            R.lds[it] = pick(W.lb, W.cpre, W.np, q) + 16 * q;
-        }
-    } else {
-#pragma unroll
-        for (int it = 0; it < RoundRegs<QT>::N; ++it) {
-            const int q = min(64 * it + lane, W.nch - 1);
-            R.d[it] = *(g_u32x4*)(W.gbase + pick(W.goff, W.cpre, W.np, q) + 16 * q);
-            R.lds[it] = pick(W.lb, W.cpre, W.np, q) + 16 * q;
-        }
-    }
-}
-
-template <int QT>
-__device__ inline void round_store(uint8_t* stage, const RoundRegs<QT>& R) {
-#pragma unroll
-    for (int it = 0; it < RoundRegs<QT>::N; ++it) *reinterpret_cast<u32x4*>(stage + R.lds[it]) = R.d[it];
-}
-
-// decode the wave-round's units, one per lane; contributions of unit
-// (t, r, us) go to part + (t * part_rows + r) * NCB
-template <int QT>
-__device__ inline void round_decode(const TileWalk<QT>& T, const WaveRound& W, int v0, int cpt, const uint8_t* tabs,
-                                    const uint8_t* stage, int k, const uint8_t* act0, int act_stride, int part_rows,
-                                    float* part) {
-    const int i = (int)(threadIdx.x & 63u);
-    if (i >= W.nu) return;
-    const int t = pick(W.t, W.upre, W.np, i);
-    const int v = v0 + pick(W.vb, W.upre, W.np, i) + i;   // tile-relative unit (row-major over the rows)
-    const int r = div_small(v, T.rcp_nus), us = v - r * T.NUS;
-    const int b0 = T.byte_of_u(v0);
-    LdsWindow<QT> Wn;
-    Wn.load(stage + 16 * cpt * t + pick(W.lead, W.upre, W.np, i) + (int)((size_t)r * T.rb) + us * TileWalk<QT>::UB - b0);
-    unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, part + (t * part_rows + r) * T.NCB);
-}
-
-// All passes of a workgroup's tiles.  The first wave-round's loads must have
-// been issued by the caller (begin_tiles) before its own prologue, so the
-// prologue's waits do not wait for them; the caller's barrier after the
-// prologue makes activations and tables visible.
+// one pass of the workgroup's tiles
 template <int QT>
 struct TileRun {
+    static constexpr int N = StageIters<QT>::V;
     TileWalk<QT> T;
-    int nv, cpt, Q, n_rounds;
-    WaveRound W;
-    RoundRegs<QT> R;
+    int v0, nv, cpt, b0, span;        // pass (uniform): first unit, units per tile, chunks per tile,
+                                      // byte of unit v0, bytes of nv units
+    int lpt, lt, lj;                  // lanes per tile; this lane's load tile and its index in it
+    const uint8_t* src;               // this lane's load tile (the tile's first row)
+    u32x4 d[N];
+    int q[N];                         // chunk of each load, within the tile
+    int lead;                         // the load tile's pass start address mod 16
 };
 
 template <int QT>
 __device__ inline void set_pass(TileRun<QT>& S, int v0) {
+    S.v0 = v0;
     S.nv = uni(min(S.T.V, S.T.total - v0));
-    S.cpt = uni(tile_chunks(S.T.byte_of_u(v0 + S.nv) - S.T.byte_of_u(v0)));
-    S.Q = uni(min(kWaveUnits, 3 * S.nv));
-    S.n_rounds = div_small_u(S.T.n_mat * S.nv + S.Q - 1, S.Q);
+    S.b0 = S.T.byte_of_u(v0);
+    S.span = uni(S.T.byte_of_u(v0 + S.nv) - S.b0);
+    S.cpt = uni(tile_chunks(S.span));
 }
 
-// Every wave issues its first wave-round's loads, also a wave with no units
-// in the first pass: it re-loads the pass's last unit (valid memory, bytes
-// its owner writes too) and decodes nothing, so the count of loads in flight
-// is the same on every wave.
-template <int QT, typename TilePtr>
-__device__ inline void tiles_begin(TileRun<QT>& S, TilePtr tile_ptr) {
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    set_pass(S, 0);
-    const int N = S.T.n_mat * S.nv;
-    const int ua = wave * S.Q, ub = min(ua + S.Q, N);
-    const int la = min(ua, N - 1);
-    S.W = make_round(S.T, tile_ptr, 0, S.nv, S.cpt, la, max(ub, la + 1));
-    S.W.nu = max(0, ub - ua);
-    round_load<QT>(S.W, S.R);
-}
-
-template <int QT, typename TilePtr>
-__device__ inline void tiles_finish(TileRun<QT>& S, TilePtr tile_ptr, const uint8_t* tabs, uint8_t* stage, int k,
-                                    const uint8_t* act0, int act_stride, int part_rows, float* part) {
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int nwaves = (int)(blockDim.x >> 6);
-    bool loaded = true;                    // this wave's first round of the pass is in flight
-    for (int v0 = 0;;) {
-        if (loaded) {
-            for (int j = wave;;) {
-                round_store<QT>(stage, S.R);
-                round_decode<QT>(S.T, S.W, v0, S.cpt, tabs, stage, k, act0, act_stride, part_rows, part);
-                j += nwaves;
-                if (j >= S.n_rounds) break;
-                const int ua = j * S.Q, ub = min(ua + S.Q, S.T.n_mat * S.nv);
-                S.W = make_round(S.T, tile_ptr, v0, S.nv, S.cpt, ua, ub);
-                round_load<QT>(S.W, S.R);
-            }
-        }
-        __syncthreads();   // the pass is decoded (partials written, staging free)
-        v0 += S.nv;
-        if (v0 >= S.T.total) break;
-        set_pass(S, v0);
-        loaded = wave < S.n_rounds;
-        if (loaded) {
-            const int ua = wave * S.Q, ub = min(ua + S.Q, S.T.n_mat * S.nv);
-            S.W = make_round(S.T, tile_ptr, v0, S.nv, S.cpt, ua, ub);
-            round_load<QT>(S.W, S.R);
-        }
+template <int QT>
+__device__ inline void pass_load(TileRun<QT>& S) {
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    const uint8_t* P = S.src + S.b0;
+    S.lead = (int)(reinterpret_cast<uintptr_t>(P) & 15);
+    const uint8_t* g = P - S.lead;
+    const int last = (S.lead + S.span - 1) >> 4;       // the tile's last chunk of the pass
+#pragma unroll
+    for (int it = 0; it < S.N; ++it) {
+        S.q[it] = min(S.lj + S.lpt * it, last);
+        S.d[it] = *(g_u32x4*)(g + 16 * S.q[it]);
     }
 }
 
-// 64-bit value of lane `src` of the wave, for a wave-uniform src
-__device__ inline const uint8_t* read_lane_ptr(const uint8_t* p, int src) {
+template <int QT>
+__device__ inline void pass_store(const TileRun<QT>& S, uint8_t* stage, int* leads) {
+    uint8_t* dst = stage + 16 * S.cpt * S.lt;
+#pragma unroll
+    for (int it = 0; it < S.N; ++it) *reinterpret_cast<u32x4*>(dst + 16 * S.q[it]) = S.d[it];
+    if (S.lj == 0) leads[S.lt] = S.lead;
+}
+
+// decode the pass's units, kThreads apart per lane; contributions of unit
+// (t, r, us) go to part + (t * part_rows + r) * NCB
+template <int QT>
+__device__ inline void pass_decode(const TileRun<QT>& S, const uint8_t* tabs, const uint8_t* stage, const int* leads,
+                                   int k, const uint8_t* act0, int act_stride, int part_rows, float* part) {
+    const int n = S.T.n_mat * S.nv;
+    const float rcp_nv = __builtin_amdgcn_rcpf((float)S.nv);
+    for (int u = (int)threadIdx.x; u < n; u += kThreads) {
+        const int t = div_small(u, rcp_nv);
+        const int v = S.v0 + (u - t * S.nv);             // tile-relative unit (row-major over the rows)
+        const int r = div_small(v, S.T.rcp_nus), us = v - r * S.T.NUS;
+        LdsWindow<QT> Wn;
+        Wn.load(stage + 16 * S.cpt * t + leads[t] + (int)((size_t)r * S.T.rb) + us * TileWalk<QT>::UB - S.b0);
+        unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, part + (t * part_rows + r) * S.T.NCB);
+    }
+}
+
+// Issue the first pass's loads.  tile_ptr(t) is the first row of tile t, for
+// a per-lane t.  The caller issues its own prologue loads before this and
+// waits for them after it (loads complete in order), then calls tiles_finish.
+template <int QT, typename TilePtr>
+__device__ inline void tiles_begin(TileRun<QT>& S, TilePtr tile_ptr) {
+    const int g = (int)threadIdx.x;
+    S.lpt = uni(kThreads / S.T.n_mat);
+    const int lt = div_small(g, __builtin_amdgcn_rcpf((float)S.lpt));
+    const bool idle = lt >= S.T.n_mat;
+    S.lt = idle ? S.T.n_mat - 1 : lt;
+    S.lj = idle ? S.lpt - 1 : g - lt * S.lpt;
+    S.src = tile_ptr(S.lt);
+    set_pass(S, 0);
+    pass_load(S);
+}
+
+// Stage and decode every pass.  The workgroup barrier after the stores also
+// publishes what the caller's prologue wrote to LDS (activations, tables);
+// the one after each decode frees the stage and publishes the partials.
+template <int QT>
+__device__ inline void tiles_finish(TileRun<QT>& S, const uint8_t* tabs, uint8_t* stage, int* leads, int k,
+                                    const uint8_t* act0, int act_stride, int part_rows, float* part) {
+    for (;;) {
+        pass_store(S, stage, leads);
+        __syncthreads();
+        const TileRun<QT> C = S;                 // this pass (the registers of the next one are reused)
+        const int next = C.v0 + C.nv;
+        if (next < S.T.total) {
+            set_pass(S, next);
+            pass_load(S);
+        }
+        pass_decode(C, tabs, stage, leads, k, act0, act_stride, part_rows, part);
+        __syncthreads();
+        if (next >= S.T.total) break;
+    }
+}
+
+// 64-bit value of lane `src` (0..63, per lane) of the wave
+__device__ inline const uint8_t* lane_ptr(const uint8_t* p, int src) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
     return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
 }
 
@@ -475,11 +389,12 @@ struct MmidArgs {
     unsigned int* err;            // sticky error word, host-mapped; every writer stores 1
 };
 
-// The kernels' static LDS: IQ3_S tables (when QT is IQ3_S) and the staging
-// area with a guard on each side.
+// The kernels' static LDS: IQ3_S tables (when QT is IQ3_S), the staged
+// tiles' leads and the staging area.
 #define SABAH_STATIC_LDS(QT)                                                              \
     __shared__ __align__(16) uint8_t lds_static[StaticLds<QT>::BYTES];                    \
     uint8_t* const tabs = lds_static;                                                    \
+    int* const leads = reinterpret_cast<int*>(lds_static + StaticLds<QT>::LEADS);        \
     uint8_t* const stage = lds_static + StaticLds<QT>::STAGE;
 
 template <int QT>
@@ -517,8 +432,7 @@ __global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
     tiles_begin(S, tile_ptr);
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsX>(xb, xa);
-    __syncthreads();
-    tiles_finish(S, tile_ptr, tabs, stage, a.k, act, 0, packed ? a.R : 1, part);
+    tiles_finish(S, tabs, stage, leads, a.k, act, 0, packed ? a.R : 1, part);
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) out[r] = row_sum(part + r * NCB, NCB);
 }
 
@@ -570,8 +484,7 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
     tiles_begin(S, tile_ptr);
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsX>(xb, xa);
-    __syncthreads();
-    tiles_finish(S, tile_ptr, tabs, stage, a.d_model, act, 0, a.R, part);
+    tiles_finish(S, tabs, stage, leads, a.d_model, act, 0, a.R, part);
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
@@ -627,13 +540,12 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     const uint8_t* e = resolve_slot_word(a.D, a.rt, sw);
     const bool bad = __any(e == nullptr);
     const uint8_t* mine = (e ? e : a.D.base) + (size_t)row0 * rb;
-    auto tile_ptr = [&](int m) { return read_lane_ptr(mine, m); };
+    auto tile_ptr = [&](int m) { return lane_ptr(mine, m); };
     TileRun<QT> S{TileWalk<QT>(a.n_slots, nrows, rb, a.d_ff)};
     tiles_begin(S, tile_ptr);
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsH>(hb, ha);
-    __syncthreads();
-    tiles_finish(S, tile_ptr, tabs, stage, a.d_ff, act, P.act_bytes, a.R, part);
+    tiles_finish(S, tabs, stage, leads, a.d_ff, act, P.act_bytes, a.R, part);
     float* o = a.out + (size_t)t * a.d_model + row0;
     if (bad) {
         flag_error(a.err);

@@ -131,19 +131,27 @@ __device__ inline float h2f(uint32_t bits16) { return __half2float(__ushort_as_h
 __device__ inline int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 // ---------------------------------------------------------------------------
-// LDS table for IQ3_S: the 512-entry codebook (u32: four 3-bit levels
-// expanded to bytes) at LDS byte 0.  Signs are applied in registers: for a
-// sign nibble n, t = n's bits spread to bytes (0x01) and m = t * 0xFF, so
-// (mag ^ m) + t negates exactly the bytes whose sign bit is set (magnitudes
-// are odd and below 128, so no byte carries into the next).
+// LDS table for IQ3_S: the 512-entry codebook (u32: four magnitudes, one per
+// byte) with every sign pattern already applied.  Entry qs + 256 * h, where
+// h = n + 16 * b for a sign nibble n and ninth index bit b, holds
+// grid[qs + 256 * b] with byte j negated where bit j of n is set; 8192 u32 at
+// LDS byte 0.  A lookup's byte address is the 16-bit value [qs, h] times 4,
+// and one v_perm builds that value for two lookups at once.
 // ---------------------------------------------------------------------------
 constexpr int kLdsGrid = 0;
-constexpr int kLdsTables = 2048;
+constexpr int kLdsTables = 8192 * 4;
 
 __device__ inline uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
 
-// The IQ3_S codebook in LDS, written by NT threads (w = 0 .. NT-1 of them)
-// from registers loaded early.
+// v_perm selector that negates byte j of a codebook word g where bit j of n
+// is set, taking that byte from g ^ 0xFEFEFEFE (source 0) instead of g
+// (source 1): for odd g, -g = g ^ 0xFE (two's complement ~(g - 1), and
+// g - 1 = g ^ 1).  n * 0x810204 puts bit j of n at bit 8j + 2 (the partial
+// products do not overlap for n < 16), turning selector byte j into j + 4.
+__host__ __device__ constexpr uint32_t sign_sel(uint32_t n) { return ((n * 0x00810204u) & 0x04040404u) | 0x03020100u; }
+
+// The signed codebook in LDS, written by NT threads (w = 0 .. NT-1 of them)
+// from codebook registers loaded early.
 template <int NT>
 struct GridRegs {
     uint32_t e[512 / NT];
@@ -157,9 +165,15 @@ __device__ inline GridRegs<NT> load_grid_regs(int w) {
 }
 template <int NT>
 __device__ inline void store_iq3s_tables(uint8_t* smem, const GridRegs<NT>& g, int w) {
-    uint32_t* grid = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
+    uint32_t* tab = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
 #pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) grid[w + NT * i] = g.e[i];
+    for (int i = 0; i < 512 / NT; ++i) {
+        const int idx = w + NT * i;                       // codebook index qs + 256 * b
+        uint32_t* row = tab + (idx & 255) + 4096 * (idx >> 8);
+        const uint32_t neg = g.e[i] ^ 0xFEFEFEFEu;
+#pragma unroll
+        for (int n = 0; n < 16; ++n) row[256 * n] = __builtin_amdgcn_perm(neg, g.e[i], sign_sel((uint32_t)n));
+    }
 }
 // all 256 threads of the workgroup
 __device__ inline void stage_iq3s_tables(uint8_t* smem) {
@@ -186,22 +200,25 @@ __device__ inline void act8(const uint8_t* chunk, int j, uint32_t (&A)[8]) {
 // packed int8 weights of item ib (8 dwords) and its scale
 __device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* smem, uint32_t (&v)[8]) {
     const uint32_t qh = (F[16 + (ib >> 2)] >> (8 * (ib & 3))) & 0xFFu;
-    const uint32_t T0 = spread4(qh & 15u), T1 = spread4(qh >> 4);
-    const uint32_t S = F[18 + ib];
+    const uint32_t S = F[18 + ib];           // sign nibble of grid g at bits 4g..4g+3
+    // H[k] byte j: h of grid g = 4k + j (its sign nibble | bit g of qh << 4)
+    uint32_t H[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t x = __builtin_amdgcn_perm(S, S, k ? 0x0C030C02u : 0x0C010C00u);   // [S.b2k, 0, S.b2k+1, 0]
+        const uint32_t y = (x | (x << 4)) & 0x0F0F0F0Fu;                                 // one nibble per byte
+        // bit j of the qh nibble to bit 8j + 4 (a 24-bit multiply: the shift is not folded into a 32-bit one)
+        H[k] = y | (__umul24(k ? qh & 0xF0u : (qh & 15u) << 4, 0x00204081u) & 0x10101010u);
+    }
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
         const uint32_t Q = F[2 * ib + (l >> 1)];
-        const uint32_t T = (l >> 1) ? T1 : T0;
         const uint32_t pp = 2u * (uint32_t)(l & 1);
-        // bytes [qs_g, qhbit_g, qs_g+1, qhbit_g+1] -> two 9-bit codebook indices
+        // [qs_g, h_g, qs_g+1, h_g+1] for g = 2l: two 16-bit table indices
         const uint32_t sel = (4u + pp) | (pp << 8) | ((5u + pp) << 16) | ((pp + 1u) << 24);
-        // each byte offset is one shift of a 16-bit or 8-bit field (one SDWA op)
-        const uint32_t D = __builtin_amdgcn_perm(Q, T, sel);
-        const uint32_t g0 = lds_u32(smem, kLdsGrid + ((D & 0xFFFFu) << 2));
-        const uint32_t g1 = lds_u32(smem, kLdsGrid + ((D >> 16) << 2));
-        const uint32_t t0 = spread4((S >> (8 * l)) & 15u), t1 = spread4((S >> (8 * l + 4)) & 15u);
-        v[2 * l] = (g0 ^ (t0 * 0xFFu)) + t0;
-        v[2 * l + 1] = (g1 ^ (t1 * 0xFFu)) + t1;
+        const uint32_t D = __builtin_amdgcn_perm(Q, H[l >> 1], sel);
+        v[2 * l] = lds_u32(smem, kLdsGrid + ((D & 0xFFFFu) << 2));
+        v[2 * l + 1] = lds_u32(smem, kLdsGrid + (D >> 14));      // h < 32: bits 14, 15 of D are 0
     }
     return 2 * (int)((F[26] >> (4 * ib)) & 15u) + 1;
 }
@@ -296,7 +313,7 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
             int s = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
-            bsum += ls * s;
+            bsum += __mul24(ls, s);              // |s| <= 32 * 15 * 127 < 2^23
         }
         r.c[0] = __fmul_rn(__fmul_rn(h2f(Fm1 >> 16), dx[0]), (float)bsum);
     } else if constexpr (QT == QT_Q4_K) {
@@ -311,8 +328,8 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
             for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
             int sc, mn;
             q4k_scale_min(F, j, sc, mn);
-            isum += sc * s;
-            msum += mn * ((int)bs[2 * j] + (int)bs[2 * j + 1]);
+            isum += __mul24(sc, s);             // sc, mn < 64; |s| < 2^16
+            msum += __mul24(mn, (int)bs[2 * j] + (int)bs[2 * j + 1]);
         }
         const float d = h2f(F[0]), dmin = h2f(F[0] >> 16);
         r.c[0] = __fsub_rn(__fmul_rn(__fmul_rn(d, dx[0]), (float)isum), __fmul_rn(__fmul_rn(dmin, dx[0]), (float)msum));
@@ -331,7 +348,7 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
             // sum (q - 32) * q8 = sum q * q8 - 32 * bsum over each 16-element half
             sa -= 32 * (int)bs[2 * j];
             sb -= 32 * (int)bs[2 * j + 1];
-            isum += q6k_scale(F, 2 * j) * sa + q6k_scale(F, 2 * j + 1) * sb;
+            isum += __mul24(q6k_scale(F, 2 * j), sa) + __mul24(q6k_scale(F, 2 * j + 1), sb);   // |sa|, |sb| < 2^18
         }
         r.c[0] = __fmul_rn(__fmul_rn(h2f(F[52]), dx[0]), (float)isum);
     } else {   // Q8_0: four independent blocks
