@@ -171,6 +171,20 @@ int sabah_moe_layer(const sabah_moe_layer_desc *layer, const float *d_x, const i
 int sabah_moe_chain(const sabah_moe_layer_desc *layers, int n_layers, float *d_x,
                     const int32_t *d_ids, const float *d_w, int n_used, int n_tokens, void *stream);
 
+/* The same layer as sabah_moe_layer (same arguments, bit-identical results),
+ * computed group-major for a batch of tokens (prefill): the (token, slot)
+ * pairs are grouped by expert on the device, and each routed expert's rows
+ * are read once and applied to all of its pairs with int8 MFMA.  No
+ * reference counterpart: the reference's kernel re-reads an expert per
+ * (token, slot) (sabah_rt.cu:2791-2839); the grouping follows upstream
+ * ggml's sorted MUL_MAT_ID fallback (ggml-cuda.cu:1985-2082).  Needs IQ3_S
+ * gate/up/down, d_model a multiple of 512 up to 2048, d_ff a multiple of 256
+ * up to 1024, n_experts <= 4096; returns -1 otherwise.  An out-of-range id
+ * makes its token's output NaN and fails the next call, as in sabah_moe_layer. */
+int sabah_moe_prefill_layer(const sabah_moe_layer_desc *layer, const float *d_x, const int32_t *d_ids,
+                            const float *d_w, int n_used, int n_tokens, float *d_out, const float *d_resid,
+                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

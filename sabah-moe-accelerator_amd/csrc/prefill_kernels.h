@@ -1,0 +1,400 @@
+// Group-major MoE layer for a batch of tokens (prefill).
+//
+// The token-major kernels read every routed expert matrix once per (token,
+// slot) that selects it, as the reference's kernel does (grid z = n_tokens,
+// sabah_rt.cu:2791-2839).  Here the (token, slot) pairs are grouped by expert
+// on the device, and each expert's rows are read once per layer and applied
+// to all of its pairs with int8 MFMA (v_mfma_i32_16x16x32_i8: 16 rows x 16
+// pairs x one 32-element sub-block per instruction).  The semantics are
+// upstream ggml's sorted MUL_MAT_ID fallback (ggml-cuda.cu:1985-2082): group
+// by expert, per-expert matrix product, scatter back, weighted combine.
+//
+// The integer block sums are exact, and every fp32 step (block scale times
+// block sum, the serial sum over blocks, SwiGLU, the slot-ordered combine)
+// is the token-major path's, so the results are bit-identical to it.
+//
+// Kernels of one layer, in stream order:
+//   k_group_pairs     ids -> per-expert offsets and the pairs in group order
+//   k_quant_rows      x -> q8_K rows (ActLayout), one per token
+//   k_grouped_gate_up h[pos] = silu(Wg[e] . q8(x[t])) * (Wu[e] . q8(x[t]))
+//   k_quant_rows      h -> q8_K rows, one per grouped pair
+//   k_grouped_down    y[pos] = Wd[e] . q8(h[pos])
+//   k_combine         out[t] = [resid +] ((y0 w0 + y1 w1) + ...) [+ shared]
+// Supported: IQ3_S gate, up and down; d_model / 256 even and <= 8; d_ff / 256 <= 4.
+#pragma once
+#include "mmid_kernels.h"
+
+namespace sabah {
+
+constexpr int kGroupThreads = 1024;
+constexpr int kPairTile = 16;                 // pairs per MFMA column tile
+constexpr int kGuRows = 16;                   // gate/up rows per workgroup (one MFMA row tile)
+constexpr int kDownRows = 64;                 // down rows per workgroup (four MFMA row tiles)
+constexpr int kGuBlocksPerWave = 4;           // 256-blocks of k per gate/up wave (two waves per matrix)
+constexpr int kDownBlocks = 4;                // 256-blocks of k per down wave (one wave per row tile)
+
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Grouping.  Pair p = t * k + s.  off[e] .. off[e+1] are expert e's positions;
+// pair_of[pos] is the pair at a position and pos_of[p] the position of a
+// pair (-1 for an id outside [0, n_experts), which also sets the error word).
+// The order of pairs inside a group is not fixed (LDS atomics): it changes no
+// value, only where a pair's rows are kept.
+// ---------------------------------------------------------------------------
+struct GroupArgs {
+    const int32_t* ids;           // [n_tokens][k]
+    int n_tokens, k, n_experts;
+    int* off;                     // [n_experts + 1]
+    int* pair_of;                 // [n_tokens * k]
+    int* pos_of;                  // [n_tokens * k]
+    unsigned int* err;
+};
+
+// exclusive scan of one int per thread over the workgroup; tmp holds blockDim.x ints
+__device__ inline int block_exclusive_scan(int v, int* tmp, int& total) {
+    const int i = (int)threadIdx.x, n = (int)blockDim.x;
+    tmp[i] = v;
+    __syncthreads();
+    for (int o = 1; o < n; o <<= 1) {
+        const int x = i >= o ? tmp[i - o] : 0;
+        __syncthreads();
+        tmp[i] += x;
+        __syncthreads();
+    }
+    total = tmp[n - 1];
+    const int r = tmp[i] - v;
+    __syncthreads();
+    return r;
+}
+
+// one workgroup of kGroupThreads; dynamic LDS: 2 * n_experts + kGroupThreads ints
+__global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
+    extern __shared__ int glds[];
+    const int E = a.n_experts, P = a.n_tokens * a.k;
+    int* cnt = glds;
+    int* fill = glds + E;
+    int* tmp = glds + 2 * E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int e = a.ids[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // each thread scans a contiguous run of seg experts
+    const int seg = (E + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int e0 = min(E, (int)threadIdx.x * seg), e1 = min(E, e0 + seg);
+    int s = 0;
+    for (int e = e0; e < e1; ++e) s += cnt[e];
+    int total;
+    int run = block_exclusive_scan(s, tmp, total);
+    for (int e = e0; e < e1; ++e) {
+        fill[e] = run;
+        a.off[e] = run;
+        run += cnt[e];
+    }
+    if (threadIdx.x == 0) a.off[E] = total;
+    __syncthreads();
+    bool bad = false;
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int e = a.ids[p];
+        if (e >= 0 && e < E) {
+            const int pos = atomicAdd(&fill[e], 1);
+            a.pair_of[pos] = p;
+            a.pos_of[p] = pos;
+        } else {
+            a.pos_of[p] = -1;
+            bad = true;
+        }
+    }
+    if (bad) *reinterpret_cast<volatile unsigned int*>(a.err) = 1u;
+}
+
+// ---------------------------------------------------------------------------
+// q8 rows in the kernels' activation layout (ActLayout), n_rows rows of k
+// floats.  Each workgroup quantises 16 chunk-rows (one per 16-lane row).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_quant_rows(const float* __restrict__ x, int n_rows, int k, int at,
+                                                         uint8_t* __restrict__ out, int out_stride) {
+    const int nch = k / 256;
+    const int q = blockIdx.x * (kThreads / 16) + (int)(threadIdx.x >> 4);
+    if (q >= n_rows * nch) return;                       // whole 16-lane rows leave together
+    const int r = q / nch, c = q - r * nch;
+    const ActBatch B{x, (size_t)k, n_rows, k, at, out, out_stride};
+    Act16 v;
+    load16(x + (size_t)r * k, c * 256 + 16 * (int)(threadIdx.x & 15u), k, act_vec(B), v);
+    quant_chunk(B, v, q);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA operands.  For v_mfma_i32_16x16x32_i8, lane l holds row (A) or column
+// (B) l % 16 and the eight k-values 8 (l / 16) .. +7 of the 32; the int32
+// result's lane l holds column l % 16 and rows 4 (l / 16) .. +3.
+// ---------------------------------------------------------------------------
+
+// IQ3_S A operand: the eight weights of row `unit`'s sub-block `sub` that lane
+// quarter q holds (grid groups 2q, 2q + 1), from the staged unit bytes and the
+// signed codebook table
+__device__ inline long iq3s_a_operand(const uint8_t* unit, const uint8_t* tabs, int sub, int q) {
+    const uint32_t qs = unit[2 + 8 * sub + 2 * q] | (uint32_t)unit[3 + 8 * sub + 2 * q] << 8;   // any alignment
+    const uint32_t qh = unit[66 + sub] >> (2 * q);
+    const uint32_t sg = unit[74 + 4 * sub + q];
+    const uint32_t i0 = (qs & 0xFFu) + 256u * ((sg & 15u) + 16u * (qh & 1u));
+    const uint32_t i1 = (qs >> 8) + 256u * ((sg >> 4) + 16u * ((qh >> 1) & 1u));
+    const uint32_t g0 = lds_u32(tabs, kLdsGrid + 4u * i0), g1 = lds_u32(tabs, kLdsGrid + 4u * i1);
+    return (long)(((uint64_t)g1 << 32) | g0);
+}
+
+// per (matrix, sub-block, row) scale 2 * nibble + 1 and per (matrix, block, row) d of
+// the staged IQ3_S tiles: unit u = (m * nrows + r) * nb + b
+__device__ inline void iq3s_scale_tables(const uint8_t* stage, int cpt, const int* leads, int n_mat, int nrows,
+                                         int nb, size_t rb, uint8_t* ls_tab, float* dw_tab) {
+    for (int u = threadIdx.x; u < n_mat * nrows * nb; u += blockDim.x) {
+        const int b = u % nb, mr = u / nb, r = mr % nrows, m = mr / nrows;
+        const uint8_t* unit = stage + 16 * cpt * m + leads[m] + (size_t)r * rb + 110 * b;
+        dw_tab[(m * nb + b) * nrows + r] = h2f(unit[0] | (uint32_t)unit[1] << 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            ls_tab[((m * nb + b) * 8 + j) * nrows + r] = (uint8_t)(2 * ((unit[106 + j / 2] >> (4 * (j & 1))) & 15) + 1);
+    }
+}
+
+// the staged tiles' loads only (no decode): tiles_begin issued them
+template <int QT>
+__device__ inline void tiles_stage(TileRun<QT>& S, uint8_t* stage, int* leads) {
+    pass_store(S, stage, leads);
+}
+
+// 16 rows x 16 pairs over blocks [b0, b1) of a row: per block, the exact int32
+// block sum sum_sub ls * (W_sub . x_sub), then c = (d_w * d_x) * bsum.  A holds
+// the rows' decoded sub-blocks (block-major), xrow the pair's q8_K row (this
+// lane's column), dx its block scales.  c[blk][i] for the lane's rows 4q + i.
+template <int NBMAX>
+__device__ inline void mfma_blocks(const long (&A)[NBMAX][8], int b0, int b1, const uint8_t* xrow, bool valid,
+                                   const float* dxrow, const uint8_t* ls_tab, const float* dw_tab, int nrows,
+                                   int rbase, int q, float (&c)[NBMAX][4]) {
+#pragma unroll
+    for (int j = 0; j < NBMAX; ++j) {
+        const int b = b0 + j;
+        if (b >= b1) break;
+        int bs[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int sub = 0; sub < 8; ++sub) {
+            const long xb = valid ? *reinterpret_cast<const long*>(xrow + b * kActChunkStride + 32 * sub + 8 * q) : 0;
+            v4i32 z = {0, 0, 0, 0};
+            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[j][sub], xb, z, 0, 0, 0);
+            const uint32_t ls4 = *reinterpret_cast<const uint32_t*>(ls_tab + (b * 8 + sub) * nrows + rbase + 4 * q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bs[i] += __mul24((int)((ls4 >> (8 * i)) & 0xFFu), d[i]);
+        }
+        const float dx = valid ? dxrow[b] : 0.0f;
+        const float4 dw = *reinterpret_cast<const float4*>(dw_tab + b * nrows + rbase + 4 * q);
+        c[j][0] = __fmul_rn(__fmul_rn(dw.x, dx), (float)bs[0]);
+        c[j][1] = __fmul_rn(__fmul_rn(dw.y, dx), (float)bs[1]);
+        c[j][2] = __fmul_rn(__fmul_rn(dw.z, dx), (float)bs[2]);
+        c[j][3] = __fmul_rn(__fmul_rn(dw.w, dx), (float)bs[3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped gate/up + SwiGLU.  grid = (d_ff / 16, n_experts), 256 threads.
+// Wave w: matrix w >> 1 (gate, up), blocks of k [nb0, nb) for w & 1, else
+// [0, nb0).  Each wave decodes its 16 rows x blocks once into registers and
+// runs them against every 16-pair tile of the expert; the two halves meet
+// in LDS, in block order, before SwiGLU.
+// ---------------------------------------------------------------------------
+struct GroupedGateUpArgs {
+    const uint8_t *gate, *up;     // bank bases [n_experts][d_ff][row bytes]
+    size_t expert_stride;
+    const int* off;
+    const int* pair_of;
+    int k;                        // slots per token: pair p is token p / k
+    const uint8_t* xq;            // q8_K rows per token, xq_stride bytes apart
+    int xq_stride;
+    float* h;                     // [pairs in group order][d_ff]
+    int d_model, d_ff;
+};
+
+__global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs a) {
+    constexpr int QT = QT_IQ3_S;
+    const int e = blockIdx.y;
+    const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
+    if (n_e == 0) return;                                  // uniform: the whole workgroup leaves
+    SABAH_STATIC_LDS(QT)
+    __shared__ __align__(16) uint8_t ls_tab[2 * 8 * kGuBlocksPerWave * 2 * kGuRows];
+    __shared__ __align__(16) float dw_tab[2 * kGuBlocksPerWave * 2 * kGuRows];
+    __shared__ __align__(16) float part[2][kGuBlocksPerWave][kGuRows][kPairTile];
+    __shared__ __align__(16) float gu[2][kGuRows][kPairTile];
+    const int row0 = blockIdx.x * kGuRows;
+    const int nb = a.d_model / 256, nb0 = nb / 2;
+    const size_t rb = row_bytes(QT, a.d_model);
+    GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    const uint8_t* wg = a.gate + (size_t)e * a.expert_stride + (size_t)row0 * rb;
+    const uint8_t* wu = a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
+    auto tile_ptr = [&](int m) { return m ? wu : wg; };
+    TileRun<QT> S{TileWalk<QT>(2, kGuRows, rb, a.d_model)};
+    tiles_begin(S, tile_ptr);
+    store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    tiles_stage(S, stage, leads);
+    __syncthreads();
+    iq3s_scale_tables(stage, S.cpt, leads, 2, kGuRows, nb, rb, ls_tab, dw_tab);
+
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    const int m = wave >> 1, half = wave & 1, r = lane & 15, q = lane >> 4;
+    const int b0 = half ? nb0 : 0, b1 = half ? nb : nb0;
+    long A[kGuBlocksPerWave][8];
+    {
+        const uint8_t* rowp = stage + 16 * S.cpt * m + leads[m] + (size_t)r * rb;
+#pragma unroll
+        for (int j = 0; j < kGuBlocksPerWave; ++j)
+#pragma unroll
+            for (int sub = 0; sub < 8; ++sub)
+                A[j][sub] = b0 + j < b1 ? iq3s_a_operand(rowp + 110 * (b0 + j), tabs, sub, q) : 0;
+    }
+    __syncthreads();                                        // scale tables written
+    const ActLayout XL(a.d_model, QT_Q8_K);
+    const uint8_t* lsm = ls_tab + m * (nb * 8 * kGuRows);
+    const float* dwm = dw_tab + m * (nb * kGuRows);
+    for (int pt = 0; pt < n_e; pt += kPairTile) {
+        const int cnt = min(kPairTile, n_e - pt);
+        const int j = lane & 15;
+        const bool valid = j < cnt;
+        const int t = a.pair_of[g0 + pt + min(j, cnt - 1)] / a.k;
+        const uint8_t* xrow = a.xq + (size_t)t * a.xq_stride;
+        float c[kGuBlocksPerWave][4];
+        mfma_blocks<kGuBlocksPerWave>(A, b0, b1, xrow, valid, reinterpret_cast<const float*>(xrow + XL.off_d), lsm,
+                                      dwm, kGuRows, 0, q, c);
+        if (half) {
+#pragma unroll
+            for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
+                if (b0 + jj < b1)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) part[m][jj][4 * q + i][j] = c[jj][i];
+        }
+        __syncthreads();
+        if (!half) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
+                    if (jj < b1 - b0) acc = __fadd_rn(acc, c[jj][i]);
+                for (int jj = 0; jj < nb - nb0; ++jj) acc = __fadd_rn(acc, part[m][jj][4 * q + i][j]);
+                gu[m][4 * q + i][j] = acc;
+            }
+        }
+        __syncthreads();
+        {
+            const int rr = (int)threadIdx.x >> 4, jj = (int)threadIdx.x & 15;
+            if (jj < cnt)
+                a.h[(size_t)(g0 + pt + jj) * a.d_ff + row0 + rr] = __fmul_rn(silu_f32(gu[0][rr][jj]), gu[1][rr][jj]);
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped down.  grid = (d_model / 64, n_experts), 256 threads; wave w owns
+// rows 16 w .. 16 w + 15 of the workgroup's 64, over the whole of k.
+// ---------------------------------------------------------------------------
+struct GroupedDownArgs {
+    const uint8_t* down;          // bank base [n_experts][d_model][row bytes]
+    size_t expert_stride;
+    const int* off;
+    const uint8_t* hq;            // q8_K rows per grouped pair, hq_stride bytes apart
+    int hq_stride;
+    float* y;                     // [pairs in group order][d_model]
+    int d_model, d_ff;
+};
+
+__global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
+    constexpr int QT = QT_IQ3_S;
+    const int e = blockIdx.y;
+    const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
+    if (n_e == 0) return;
+    SABAH_STATIC_LDS(QT)
+    __shared__ __align__(16) uint8_t ls_tab[8 * kDownBlocks * kDownRows];
+    __shared__ __align__(16) float dw_tab[kDownBlocks * kDownRows];
+    const int row0 = blockIdx.x * kDownRows;
+    const int nb = a.d_ff / 256;
+    const size_t rb = row_bytes(QT, a.d_ff);
+    GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    const uint8_t* wd = a.down + (size_t)e * a.expert_stride + (size_t)row0 * rb;
+    auto tile_ptr = [&](int) { return wd; };
+    TileRun<QT> S{TileWalk<QT>(1, kDownRows, rb, a.d_ff)};
+    tiles_begin(S, tile_ptr);
+    store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    tiles_stage(S, stage, leads);
+    __syncthreads();
+    iq3s_scale_tables(stage, S.cpt, leads, 1, kDownRows, nb, rb, ls_tab, dw_tab);
+
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    const int r = lane & 15, q = lane >> 4, rbase = 16 * wave;
+    long A[kDownBlocks][8];
+    {
+        const uint8_t* rowp = stage + leads[0] + (size_t)(rbase + r) * rb;
+#pragma unroll
+        for (int j = 0; j < kDownBlocks; ++j)
+#pragma unroll
+            for (int sub = 0; sub < 8; ++sub) A[j][sub] = j < nb ? iq3s_a_operand(rowp + 110 * j, tabs, sub, q) : 0;
+    }
+    __syncthreads();
+    const ActLayout HL(a.d_ff, QT_Q8_K);
+    for (int pt = 0; pt < n_e; pt += kPairTile) {
+        const int cnt = min(kPairTile, n_e - pt);
+        const int j = lane & 15;
+        const bool valid = j < cnt;
+        const int pos = g0 + pt + min(j, cnt - 1);
+        const uint8_t* hrow = a.hq + (size_t)pos * a.hq_stride;
+        float c[kDownBlocks][4];
+        mfma_blocks<kDownBlocks>(A, 0, nb, hrow, valid, reinterpret_cast<const float*>(hrow + HL.off_d), ls_tab,
+                                 dw_tab, kDownRows, rbase, q, c);
+        if (valid) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < kDownBlocks; ++jj)
+                    if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
+                a.y[(size_t)pos * a.d_model + row0 + rbase + 4 * q + i] = acc;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Combine in slot order, as k_down_combine does:
+//   out[t][i] = [resid[t][i] +] ((y(t,0)[i] w0 + y(t,1)[i] w1) + ...) [+ shared[t][i]]
+// grid = (ceil(d_model / 256), n_tokens); a token with an invalid id gets NaN.
+// ---------------------------------------------------------------------------
+struct CombineArgs {
+    const float* y;               // [pairs in group order][d_model]
+    const int* pos_of;            // [n_tokens * k]
+    const float* w;               // [n_tokens][k]
+    const float* shared;          // optional [n_tokens][d_model]
+    const float* resid;           // optional [n_tokens][d_model]
+    float* out;                   // [n_tokens][d_model] (may alias resid)
+    int k, d_model;
+};
+
+__global__ __launch_bounds__(kThreads) void k_combine(CombineArgs a) {
+    const int t = blockIdx.y, i = blockIdx.x * kThreads + (int)threadIdx.x;
+    if (i >= a.d_model) return;
+    const int* pos = a.pos_of + (size_t)t * a.k;
+    const float* wt = a.w + (size_t)t * a.k;
+    bool bad = false;
+    for (int s = 0; s < a.k; ++s) bad |= pos[s] < 0;
+    float* o = a.out + (size_t)t * a.d_model + i;
+    if (bad) {
+        *o = __builtin_nanf("");
+        return;
+    }
+    float acc = __fmul_rn(a.y[(size_t)pos[0] * a.d_model + i], wt[0]);
+    for (int s = 1; s < a.k; ++s) acc = __fadd_rn(acc, __fmul_rn(a.y[(size_t)pos[s] * a.d_model + i], wt[s]));
+    if (a.shared) acc = __fadd_rn(acc, a.shared[(size_t)t * a.d_model + i]);
+    if (a.resid) acc = __fadd_rn(a.resid[(size_t)t * a.d_model + i], acc);
+    *o = acc;
+}
+
+}  // namespace sabah

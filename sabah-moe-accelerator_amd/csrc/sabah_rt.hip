@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "mmid_kernels.h"
+#include "prefill_kernels.h"
 #include "synth_kernels.h"
 #include "sabah_rt.h"
 
@@ -53,13 +54,15 @@ struct Scratch {
     size_t bytes = 0;
 };
 Scratch g_scratch_h, g_scratch_hs, g_scratch_ys;
+// grouped (prefill) layer: offsets, pair maps, q8 rows of x and h, h and y in group order
+Scratch g_scratch_goff, g_scratch_gpair, g_scratch_gxq, g_scratch_gh, g_scratch_ghq, g_scratch_gy;
 uint16_t* g_nearest_dev = nullptr;   // IQ3_S encoder table, uploaded on first use
 
 // Optional HIP-event timing of every kernel the library launches, by kernel
 // kind (the reference's SABAH_LLAMA_EVENTS probe, sabah_rt.cu:118-151): each
 // dispatch records its own start/stop event pair (launch_kernel); elapsed
 // times are collected when the caller asks for them.
-enum KernelKind { KK_MMID = 0, KK_GATE_UP = 1, KK_DOWN = 2, KK_CHAIN = 3, KK_COUNT = 4 };
+enum KernelKind { KK_MMID = 0, KK_GATE_UP = 1, KK_DOWN = 2, KK_CHAIN = 3, KK_GGATE_UP = 4, KK_GDOWN = 5, KK_COUNT = 6 };
 struct EvPair {
     hipEvent_t a, b;
     int kind;
@@ -305,7 +308,8 @@ SABAH_API int sabah_rt_init(int device) {
 SABAH_API int sabah_rt_shutdown(void) {
     if (g_device < 0) return 0;
     if (g_stream) (void)hipStreamSynchronize(g_stream);
-    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys}) {
+    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys, &g_scratch_goff, &g_scratch_gpair, &g_scratch_gxq,
+                       &g_scratch_gh, &g_scratch_ghq, &g_scratch_gy}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->bytes = 0;
@@ -601,48 +605,56 @@ SABAH_API int sabah_moe_block(const float* d_x, float* d_out, float* d_h, const 
                      g_stream);
 }
 
+// dense shared expert of a layer: gate/up + SwiGLU -> hs, down -> ys; *ys_out
+// is ys (added by the routed combine), or nullptr when the layer has none
+static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_tokens, hipStream_t st,
+                         const float** ys_out) {
+    *ys_out = nullptr;
+    if (!L->shared_gate) return 0;
+    const int D = L->d_model;
+    const int Fs = L->d_ff_shared;
+    float* hs = static_cast<float*>(scratch(g_scratch_hs, sizeof(float) * (size_t)n_tokens * Fs, st));
+    float* ys = static_cast<float*>(scratch(g_scratch_ys, sizeof(float) * (size_t)n_tokens * D, st));
+    if (!hs || !ys) return -1;
+    GateUpArgs gs{};
+    gs.G = {reinterpret_cast<const uint8_t*>(L->shared_gate), nullptr, 0};
+    gs.U = {reinterpret_cast<const uint8_t*>(L->shared_up), nullptr, 0};
+    gs.rt = {nullptr, 0, 0, 1};
+    gs.x = d_x;
+    gs.h = hs;
+    gs.n_slots = 1;
+    gs.d_model = D;
+    gs.d_ff = Fs;
+    gs.R = rows_gate_up(L->qt_shared_gate, D);
+    gs.err = g_err_dev;
+    if (!ck(dispatch_gate_up(L->qt_shared_gate, gs, n_tokens, st), "shared gate/up launch")) return -1;
+    MmidArgs a{};
+    a.W = {reinterpret_cast<const uint8_t*>(L->shared_down), nullptr, 0};
+    a.rt = {nullptr, 0, 0, 1};
+    a.row_stride = row_bytes(L->qt_shared_down, Fs);
+    a.x = reinterpret_cast<const uint8_t*>(hs);
+    a.x_id_stride = (size_t)Fs * 4;
+    a.x_token_stride = (size_t)Fs * 4;
+    a.x_rows = 1;
+    a.n_ids = 1;
+    a.n_tokens = n_tokens;
+    a.dst = reinterpret_cast<uint8_t*>(ys);
+    a.dst_id_stride = (size_t)D * 4;
+    a.dst_token_stride = (size_t)D * 4;
+    a.rows = D;
+    a.k = Fs;
+    a.R = rows_mmid(L->qt_shared_down, Fs, true);
+    a.err = g_err_dev;
+    if (!ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch")) return -1;
+    *ys_out = ys;
+    return 0;
+}
+
 static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const int32_t* d_ids, const float* d_w,
                         int n_used, int n_tokens, float* d_out, const float* d_resid, hipStream_t st) {
     const int D = L->d_model, F = L->d_ff;
     const float* shared = nullptr;
-    if (L->shared_gate) {
-        // dense shared expert: gate/up + SwiGLU -> hs, down -> ys (added by the routed combine)
-        const int Fs = L->d_ff_shared;
-        float* hs = static_cast<float*>(scratch(g_scratch_hs, sizeof(float) * (size_t)n_tokens * Fs, st));
-        float* ys = static_cast<float*>(scratch(g_scratch_ys, sizeof(float) * (size_t)n_tokens * D, st));
-        if (!hs || !ys) return -1;
-        GateUpArgs gs{};
-        gs.G = {reinterpret_cast<const uint8_t*>(L->shared_gate), nullptr, 0};
-        gs.U = {reinterpret_cast<const uint8_t*>(L->shared_up), nullptr, 0};
-        gs.rt = {nullptr, 0, 0, 1};
-        gs.x = d_x;
-        gs.h = hs;
-        gs.n_slots = 1;
-        gs.d_model = D;
-        gs.d_ff = Fs;
-        gs.R = rows_gate_up(L->qt_shared_gate, D);
-        gs.err = g_err_dev;
-        if (!ck(dispatch_gate_up(L->qt_shared_gate, gs, n_tokens, st), "shared gate/up launch")) return -1;
-        MmidArgs a{};
-        a.W = {reinterpret_cast<const uint8_t*>(L->shared_down), nullptr, 0};
-        a.rt = {nullptr, 0, 0, 1};
-        a.row_stride = row_bytes(L->qt_shared_down, Fs);
-        a.x = reinterpret_cast<const uint8_t*>(hs);
-        a.x_id_stride = (size_t)Fs * 4;
-        a.x_token_stride = (size_t)Fs * 4;
-        a.x_rows = 1;
-        a.n_ids = 1;
-        a.n_tokens = n_tokens;
-        a.dst = reinterpret_cast<uint8_t*>(ys);
-        a.dst_id_stride = (size_t)D * 4;
-        a.dst_token_stride = (size_t)D * 4;
-        a.rows = D;
-        a.k = Fs;
-        a.R = rows_mmid(L->qt_shared_down, Fs, true);
-        a.err = g_err_dev;
-        if (!ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch")) return -1;
-        shared = ys;
-    }
+    if (shared_expert(L, d_x, n_tokens, st, &shared)) return -1;
     float* h = static_cast<float*>(scratch(g_scratch_h, sizeof(float) * (size_t)n_tokens * n_used * F, st));
     if (!h) return -1;
     const Routing rt{reinterpret_cast<const uint8_t*>(d_ids), 4, (size_t)n_used * 4, L->n_experts};
@@ -706,6 +718,89 @@ SABAH_API int sabah_moe_chain(const sabah_moe_layer_desc* layers, int n_layers, 
     g_layer_calls += (unsigned long long)n_layers;
     g_lookups += (unsigned long long)n_layers * per;
     return 0;
+}
+
+// ===========================================================================
+// group-major layer for a batch of tokens (prefill)
+// ===========================================================================
+static bool grouped_shape_ok(const sabah_moe_layer_desc* L) {
+    const int D = L->d_model, F = L->d_ff;
+    return L->qt_gate == QT_IQ3_S && L->qt_up == QT_IQ3_S && L->qt_down == QT_IQ3_S && D % 512 == 0 &&
+           D / 256 <= 2 * kGuBlocksPerWave && F % 256 == 0 && F / 256 <= kDownBlocks && D % kDownRows == 0 &&
+           L->n_experts <= 4096;
+}
+
+static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const int32_t* d_ids, const float* d_w,
+                          int n_used, int n_tokens, float* d_out, const float* d_resid, hipStream_t st) {
+    const int D = L->d_model, F = L->d_ff, E = L->n_experts;
+    const size_t P = (size_t)n_tokens * n_used;
+    const ActLayout XL(D, QT_Q8_K), HL(F, QT_Q8_K);
+    const int xq_stride = (int)XL.bytes, hq_stride = (int)HL.bytes;
+    int* off = static_cast<int*>(scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
+    int* pair_of = static_cast<int*>(scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
+    uint8_t* xq = static_cast<uint8_t*>(scratch(g_scratch_gxq, (size_t)xq_stride * n_tokens, st));
+    float* h = static_cast<float*>(scratch(g_scratch_gh, sizeof(float) * P * F, st));
+    uint8_t* hq = static_cast<uint8_t*>(scratch(g_scratch_ghq, (size_t)hq_stride * P, st));
+    float* y = static_cast<float*>(scratch(g_scratch_gy, sizeof(float) * P * D, st));
+    if (!off || !pair_of || !xq || !h || !hq || !y) return -1;
+    int* pos_of = pair_of + P;
+    const float* shared = nullptr;
+    if (shared_expert(L, d_x, n_tokens, st, &shared)) return -1;
+
+    GroupArgs ga{d_ids, n_tokens, n_used, E, off, pair_of, pos_of, g_err_dev};
+    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);
+    const int xq_rows = n_tokens * (D / 256);
+    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, n_tokens, D,
+                       (int)QT_Q8_K, xq, xq_stride);
+    GroupedGateUpArgs gu{};
+    gu.gate = static_cast<const uint8_t*>(L->gate);
+    gu.up = static_cast<const uint8_t*>(L->up);
+    gu.expert_stride = row_bytes(QT_IQ3_S, D) * (size_t)F;
+    gu.off = off;
+    gu.pair_of = pair_of;
+    gu.k = n_used;
+    gu.xq = xq;
+    gu.xq_stride = xq_stride;
+    gu.h = h;
+    gu.d_model = D;
+    gu.d_ff = F;
+    launch_kernel(KK_GGATE_UP, k_grouped_gate_up, dim3((unsigned)(F / kGuRows), (unsigned)E), 0, st, gu);
+    const size_t hq_rows = P * (size_t)(F / 256);
+    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((hq_rows + 15) / 16)), dim3(kThreads), 0, st, h, (int)P, F,
+                       (int)QT_Q8_K, hq, hq_stride);
+    GroupedDownArgs dn{};
+    dn.down = static_cast<const uint8_t*>(L->down);
+    dn.expert_stride = row_bytes(QT_IQ3_S, F) * (size_t)D;
+    dn.off = off;
+    dn.hq = hq;
+    dn.hq_stride = hq_stride;
+    dn.y = y;
+    dn.d_model = D;
+    dn.d_ff = F;
+    launch_kernel(KK_GDOWN, k_grouped_down, dim3((unsigned)(D / kDownRows), (unsigned)E), 0, st, dn);
+    CombineArgs cb{y, pos_of, d_w, shared, d_resid, d_out, n_used, D};
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)((D + kThreads - 1) / kThreads), (unsigned)n_tokens), dim3(kThreads), 0,
+                       st, cb);
+    return ck(hipGetLastError(), "grouped layer launch") ? 0 : -1;
+}
+
+SABAH_API int sabah_moe_prefill_layer(const sabah_moe_layer_desc* layer, const float* d_x, const int32_t* d_ids,
+                                      const float* d_w, int n_used, int n_tokens, float* d_out, const float* d_resid,
+                                      void* stream) {
+    if (check_layer_desc(layer)) return -1;
+    if (!d_x || !d_ids || !d_w || !d_out || n_used <= 0 || n_tokens < 0) return fail("invalid MoE layer arguments");
+    if (!grouped_shape_ok(layer))
+        return fail("grouped MoE layer: needs IQ3_S gate/up/down, d_model a multiple of 512 up to %d, d_ff a "
+                    "multiple of 256 up to %d, n_experts <= 4096 (got types %d/%d/%d, d_model=%d d_ff=%d E=%d)",
+                    512 * kGuBlocksPerWave, 256 * kDownBlocks, layer->qt_gate, layer->qt_up, layer->qt_down,
+                    layer->d_model, layer->d_ff, layer->n_experts);
+    if ((size_t)n_tokens * n_used > (size_t)1 << 24) return fail("grouped MoE layer: too many (token, slot) pairs");
+    if (g_device < 0) return fail("sabah_rt_init has not been called");
+    if (!check_sticky()) return -1;
+    if (n_tokens == 0) return 0;
+    ++g_layer_calls;
+    g_lookups += (unsigned long long)n_tokens * n_used;
+    return moe_prefill_on(layer, d_x, d_ids, d_w, n_used, n_tokens, d_out, d_resid, pick_stream(stream));
 }
 
 // ===========================================================================

@@ -128,6 +128,19 @@ class MoEExecutor:
                  "moe_layer")
         return out
 
+    def run_prefill_layer(self, layer: int, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor,
+                          out: torch.Tensor | None = None, resid: torch.Tensor | None = None) -> torch.Tensor:
+        """run_layer computed group-major (sabah_moe_prefill_layer): the (token, slot)
+        pairs grouped by expert on the device, each expert's rows read once."""
+        if out is None:
+            out = torch.empty_like(x)
+        desc = self.bank.layer_desc(layer, self.shared)
+        T, k = ids.shape
+        rt.check(rt.lib().sabah_moe_prefill_layer(ctypes.byref(desc), _vp(x), _vp(ids), _vp(w), k, T, _vp(out),
+                                                  _vp(resid) if resid is not None else None,
+                                                  _stream(self.device)), "moe_prefill_layer")
+        return out
+
     def layer_descs(self) -> ctypes.Array:
         arr = (rt.MoeLayerDesc * self.bank.n_layers)()
         for l in range(self.bank.n_layers):

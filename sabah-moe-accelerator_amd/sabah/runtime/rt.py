@@ -79,6 +79,7 @@ SIGNATURES = {
     "sabah_moe_block": ([c_vp, c_vp, c_vp, c_vp, c_vp, c_i, c_i, c_i, c_i, c_i, c_i, c_i], c_i),
     "sabah_moe_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
     "sabah_moe_chain": ([ctypes.POINTER(MoeLayerDesc), c_i, c_vp, c_vp, c_vp, c_i, c_i, c_vp], c_i),
+    "sabah_moe_prefill_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
 }
 
 # harness-only exports (not part of the drop-in header)
@@ -90,7 +91,7 @@ EXTRA_SIGNATURES = {
     "sabah_rt_get_kernel_timing": ([c_i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_u64), c_i], c_i),
 }
 
-KERNEL_KINDS = {"mmid": 0, "gate_up": 1, "down": 2, "chain": 3}
+KERNEL_KINDS = {"mmid": 0, "gate_up": 1, "down": 2, "chain": 3, "grouped_gate_up": 4, "grouped_down": 5}
 
 
 def kernel_timing(kind: str, reset: bool = False) -> tuple[float, int]:
