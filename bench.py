@@ -64,6 +64,8 @@ def main() -> int:
     from sabah.runtime.workloads import WORKLOADS
 
     W = WORKLOADS[args.workload]
+    if W.n_tokens > 1:
+        return bench_batch(args, W)
     dev = torch.device("cuda:0")
     rt.init(0)
     t0 = time.time()
@@ -184,7 +186,163 @@ def main() -> int:
     return 0
 
 
-KERNEL_SYMBOL = {"gate_up": "k_gate_up", "down": "k_down_combine", "mmid": "k_mmid"}
+KERNEL_SYMBOL = {"gate_up": "k_gate_up", "down": "k_down_combine", "mmid": "k_mmid",
+                 "grouped_gate_up": "k_grouped_gate_up", "grouped_down": "k_grouped_down"}
+INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
+
+
+def bench_batch(args, W):
+    """One MoE layer over a batch of tokens (prefill / small-batch decode).
+
+    IQ3_S layers run group-major (sabah_moe_prefill_layer: pairs grouped by
+    expert, each expert read once, int8 MFMA); other formats run token-major
+    (sabah_moe_layer).  The bank holds 8 layers of the workload's shape and
+    the steps rotate through them, so a step never finds the previous step's
+    experts in the 256 MB last-level cache.  `value` is the step's algorithmic
+    bytes / wall time: every distinct routed expert matrix once, the shared
+    expert, x in, out, and h written and read back."""
+    import numpy as np
+    import torch
+
+    from sabah.runtime import rt
+    from sabah.runtime.bank import DenseExpert, ExpertBank
+    from sabah.runtime.executor import MoEExecutor
+
+    dev = torch.device("cuda:0")
+    rt.init(0)
+    n_rot = 8
+    qts = {"gate": W.qt_gate, "up": W.qt_up, "down": W.qt_down}
+    bank = ExpertBank(n_rot, W.n_experts, W.d_model, W.d_ff, qts, device="cuda:0")
+    bank.fill_synthetic(seed=args.seed)
+    shared = None
+    if W.shared_d_ff:
+        shared = DenseExpert(W.d_model, W.shared_d_ff, W.qt_shared, device="cuda:0")
+        shared.fill_synthetic(seed=args.seed + 1)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(args.seed)
+    P = min(args.pool, 16)
+    ids_np, w_np = W.route(rng, n_layers=P)                           # [P, T, k]
+    x_np = rng.standard_normal((W.n_tokens, W.d_model)).astype(np.float32)
+    ids = torch.from_numpy(ids_np).to(dev)
+    wts = torch.from_numpy(w_np).to(dev)
+    x = torch.from_numpy(x_np).to(dev)
+    out = torch.empty_like(x)
+    ex = MoEExecutor(bank, max_used=W.top_k, max_tokens=W.n_tokens, shared=shared)
+    grouped = W.qt_gate == W.qt_up == W.qt_down == rt.QTYPE["IQ3_S"]
+    run = ex.run_prefill_layer if grouped else ex.run_layer
+    T, k = W.n_tokens, W.top_k
+    U = [len(np.unique(ids_np[p])) for p in range(P)]
+    act = 4 * T * W.d_model * 2 + 2 * 4 * T * k * W.d_ff
+    step_bytes = [U[p] * W.expert_bytes() + W.shared_bytes() + act for p in range(P)]
+
+    def step(i, fn):
+        fn(i % n_rot, x, ids[i % P], wts[i % P], out=out)
+
+    def timed(fn, steps):
+        for i in range(args.warmup):
+            step(i, fn)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for i in range(args.warmup, args.warmup + steps):
+            step(i, fn)
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1)
+
+    steps = max(1, args.steps)
+    ms = timed(run, steps)
+    nbytes = sum(step_bytes[i % P] for i in range(args.warmup, args.warmup + steps))
+    gbs = nbytes / (ms * 1e6)
+    # bit-identity of the grouped layer with the token-major one, and its per-kernel times
+    parity = None
+    ms_token_major = None
+    if grouped:
+        a = ex.run_prefill_layer(0, x, ids[0], wts[0]).clone()
+        b = ex.run_layer(0, x, ids[0], wts[0])
+        torch.cuda.synchronize()
+        parity = {"grouped_equals_token_major": bool(torch.equal(a, b))}
+        ms_token_major = timed(ex.run_layer, max(1, steps // 4)) / max(1, steps // 4)
+    L = rt.lib()
+    L.sabah_rt_set_kernel_timing(1)
+    for kind in rt.KERNEL_KINDS:
+        rt.kernel_timing(kind, reset=True)
+    timed(run, steps)
+    L.sabah_rt_set_kernel_timing(0)
+    kernels = {}
+    for kind in rt.KERNEL_KINDS:
+        kms, n = rt.kernel_timing(kind)
+        if n:
+            kernels[kind] = {"launches": n, "avg_us": round(1000.0 * kms / n, 3), "total_ms": kms}
+    dom = max(kernels, key=lambda q: kernels[q]["total_ms"])
+    u_mean = float(np.mean(U))
+    pairs = T * k
+    per_launch = {
+        "grouped_gate_up": u_mean * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * pairs * W.d_ff,
+        "grouped_down": u_mean * W.matrix_bytes("down") + 4 * pairs * W.d_ff,
+        "gate_up": k * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * W.d_model + 4 * k * W.d_ff,
+        "down": k * W.matrix_bytes("down") + 4 * k * W.d_ff + 4 * (2 * W.d_model + k),
+        "mmid": 0,
+    }[dom]
+    achieved = per_launch / (kernels[dom]["avg_us"] * 1e3)
+    flops = 2.0 * pairs * 3 * W.d_model * W.d_ff
+    us_step = 1000.0 * ms / steps
+    line = {
+        "metric": "MUL_MAT_ID expert GB/s (% HBM peak), one MoE layer over a token batch, 1 GPU",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8",
+        "compute": ("int8 MFMA (v_mfma_i32_16x16x32_i8) on IQ3_S weights decoded to int8 x q8_K activations, "
+                    "fp32 scales and accumulation" if grouped else
+                    "int8 x int8 -> int32 dot products, fp32 scales and accumulation"),
+        "data": "synthetic (N(0,0.02) weights quantised on device; seeded routing)",
+        "config": {"workload": W.name, "n_experts": W.n_experts, "top_k": k, "d_model": W.d_model, "d_ff": W.d_ff,
+                   "n_tokens": T, "quant": "%d/%d/%d" % (W.qt_gate, W.qt_up, W.qt_down),
+                   "shared_d_ff": W.shared_d_ff, "mode": "group-major (sabah_moe_prefill_layer)" if grouped
+                   else "token-major (sabah_moe_layer)"},
+        "us_per_layer": round(us_step, 2), "tok_s": round(T / (us_step * 1e-6), 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "unique_experts": {"mean": u_mean, "min": min(U), "max": max(U)},
+        "int8_tops": round(flops / (us_step * 1e-6) / 1e12, 2),
+        "mfma_frac": round(flops / (us_step * 1e-6) / 1e12 / INT8_PEAK_TOPS, 5) if grouped else None,
+        "token_major_us_per_layer": round(1000.0 * ms_token_major, 2) if ms_token_major else None,
+        "kernels": {q: {"launches": v["launches"], "avg_us": v["avg_us"]} for q, v in kernels.items()},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                     "bytes_per_launch": int(per_launch), "avg_launch_us": kernels[dom]["avg_us"]},
+        "cpu_baseline": None if args.no_cpu else cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np),
+        "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np):
+    """The oracle's layer (token-major, as ggml's CPU MUL_MAT_ID) on the host's
+    cores, over a sample of the batch's tokens whose routed experts are read
+    back from HBM."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    n = 8
+    e_ids = ids_np[0, :n]
+    used = np.unique(e_ids)
+    remap = {int(e): i for i, e in enumerate(used)}
+    sub = {r: np.stack([bank.read_expert(0, r, int(e)) for e in used]) for r in ("gate", "up", "down")}
+    lid = np.vectorize(remap.get)(e_ids).astype(np.int32)
+    qts = (W.qt_gate, W.qt_up, W.qt_down)
+    t0 = time.perf_counter()
+    tokens = 0
+    while True:
+        O.moe_layer(sub["gate"], sub["up"], sub["down"], qts, x_np[:n], lid, w_np[0, :n], n_threads=threads)
+        tokens += n
+        if time.perf_counter() - t0 >= args.cpu_seconds / 3:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(tokens * W.top_k * W.expert_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "tok_s": round(tokens / dt, 2),
+            "sample": "%d tokens of the batch, their %d routed experts read back from HBM, %.1f s "
+                      "(token-major: each (token, slot) reads its expert)" % (tokens, len(used), dt)}
 
 
 def measured_traffic(workload, kind):

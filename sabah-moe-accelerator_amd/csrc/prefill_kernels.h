@@ -166,14 +166,35 @@ __device__ inline void tiles_stage(TileRun<QT>& S, uint8_t* stage, int* leads) {
     pass_store(S, stage, leads);
 }
 
-// 16 rows x 16 pairs over blocks [b0, b1) of a row: per block, the exact int32
-// block sum sum_sub ls * (W_sub . x_sub), then c = (d_w * d_x) * bsum.  A holds
-// the rows' decoded sub-blocks (block-major), xrow the pair's q8_K row (this
-// lane's column), dx its block scales.  c[blk][i] for the lane's rows 4q + i.
+// One pair's activation words for blocks [b0, b1) of a row (this lane's MFMA
+// column and k-quarter q), and the blocks' scales.  Loaded ahead of the
+// MFMAs that use them, so their latency is paid once.
 template <int NBMAX>
-__device__ inline void mfma_blocks(const long (&A)[NBMAX][8], int b0, int b1, const uint8_t* xrow, bool valid,
-                                   const float* dxrow, const uint8_t* ls_tab, const float* dw_tab, int nrows,
-                                   int rbase, int q, float (&c)[NBMAX][4]) {
+struct XRegs {
+    long X[NBMAX][8];
+    float dx[NBMAX];
+};
+template <int NBMAX>
+__device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const float* dxrow, int b0, int b1, int q) {
+#pragma unroll
+    for (int j = 0; j < NBMAX; ++j) {
+        const int b = min(b0 + j, b1 - 1);                 // blocks past b1 re-read the last one (unused)
+#pragma unroll
+        for (int sub = 0; sub < 8; ++sub)
+            R.X[j][sub] = *reinterpret_cast<const long*>(xrow + b * kActChunkStride + 32 * sub + 8 * q);
+        R.dx[j] = dxrow[b];
+    }
+}
+
+// 16 rows x 16 pairs over blocks [b0, b1) of a row: per block, the exact int32
+// block sum sum_sub ls * (W_sub . x_sub), then c = (d_w * d_x) * bsum.  rowp is
+// the lane's staged weight row (decoded into the A operand as it is used);
+// lanes of a pair past the tile (valid false) multiply zeros.  c[blk][i] is
+// for the lane's rows 4q + i.
+template <int NBMAX>
+__device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int b0, int b1, const XRegs<NBMAX>& R,
+                                   bool valid, const uint8_t* ls_tab, const float* dw_tab, int nrows, int rbase, int q,
+                                   float (&c)[NBMAX][4]) {
 #pragma unroll
     for (int j = 0; j < NBMAX; ++j) {
         const int b = b0 + j;
@@ -181,28 +202,28 @@ __device__ inline void mfma_blocks(const long (&A)[NBMAX][8], int b0, int b1, co
         int bs[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int sub = 0; sub < 8; ++sub) {
-            const long xb = valid ? *reinterpret_cast<const long*>(xrow + b * kActChunkStride + 32 * sub + 8 * q) : 0;
             v4i32 z = {0, 0, 0, 0};
-            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[j][sub], xb, z, 0, 0, 0);
+            const long A = iq3s_a_operand(rowp + 110 * b, tabs, sub, q);
+            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, valid ? R.X[j][sub] : 0, z, 0, 0, 0);
             const uint32_t ls4 = *reinterpret_cast<const uint32_t*>(ls_tab + (b * 8 + sub) * nrows + rbase + 4 * q);
 #pragma unroll
             for (int i = 0; i < 4; ++i) bs[i] += __mul24((int)((ls4 >> (8 * i)) & 0xFFu), d[i]);
         }
-        const float dx = valid ? dxrow[b] : 0.0f;
+        const float dxv = valid ? R.dx[j] : 0.0f;
         const float4 dw = *reinterpret_cast<const float4*>(dw_tab + b * nrows + rbase + 4 * q);
-        c[j][0] = __fmul_rn(__fmul_rn(dw.x, dx), (float)bs[0]);
-        c[j][1] = __fmul_rn(__fmul_rn(dw.y, dx), (float)bs[1]);
-        c[j][2] = __fmul_rn(__fmul_rn(dw.z, dx), (float)bs[2]);
-        c[j][3] = __fmul_rn(__fmul_rn(dw.w, dx), (float)bs[3]);
+        c[j][0] = __fmul_rn(__fmul_rn(dw.x, dxv), (float)bs[0]);
+        c[j][1] = __fmul_rn(__fmul_rn(dw.y, dxv), (float)bs[1]);
+        c[j][2] = __fmul_rn(__fmul_rn(dw.z, dxv), (float)bs[2]);
+        c[j][3] = __fmul_rn(__fmul_rn(dw.w, dxv), (float)bs[3]);
     }
 }
 
 // ---------------------------------------------------------------------------
 // Grouped gate/up + SwiGLU.  grid = (d_ff / 16, n_experts), 256 threads.
 // Wave w: matrix w >> 1 (gate, up), blocks of k [nb0, nb) for w & 1, else
-// [0, nb0).  Each wave decodes its 16 rows x blocks once into registers and
-// runs them against every 16-pair tile of the expert; the two halves meet
-// in LDS, in block order, before SwiGLU.
+// [0, nb0).  Each wave runs its 16 rows x blocks against every 16-pair tile
+// of the expert, decoding the staged rows into MFMA operands as it goes; the
+// two halves meet in LDS, in block order, before SwiGLU.
 // ---------------------------------------------------------------------------
 struct GroupedGateUpArgs {
     const uint8_t *gate, *up;     // bank bases [n_experts][d_ff][row bytes]
@@ -229,42 +250,37 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
     const int row0 = blockIdx.x * kGuRows;
     const int nb = a.d_model / 256, nb0 = nb / 2;
     const size_t rb = row_bytes(QT, a.d_model);
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    const int m = wave >> 1, half = wave & 1, r = lane & 15, q = lane >> 4, j = lane & 15;
+    const int b0 = half ? nb0 : 0, b1 = half ? nb : nb0;
+    const ActLayout XL(a.d_model, QT_Q8_K);
     GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
     const uint8_t* wg = a.gate + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     const uint8_t* wu = a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
-    auto tile_ptr = [&](int m) { return m ? wu : wg; };
+    auto tile_ptr = [&](int mm) { return mm ? wu : wg; };
     TileRun<QT> S{TileWalk<QT>(2, kGuRows, rb, a.d_model)};
     tiles_begin(S, tile_ptr);
+    auto pair_x = [&](int pt, XRegs<kGuBlocksPerWave>& R) {
+        const int cnt = min(kPairTile, n_e - pt);
+        const int t = a.pair_of[g0 + pt + min(j, cnt - 1)] / a.k;
+        const uint8_t* xrow = a.xq + (size_t)t * a.xq_stride;
+        load_x(R, xrow, reinterpret_cast<const float*>(xrow + XL.off_d), b0, b1, q);
+    };
     store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     tiles_stage(S, stage, leads);
     __syncthreads();
     iq3s_scale_tables(stage, S.cpt, leads, 2, kGuRows, nb, rb, ls_tab, dw_tab);
-
-    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
-    const int m = wave >> 1, half = wave & 1, r = lane & 15, q = lane >> 4;
-    const int b0 = half ? nb0 : 0, b1 = half ? nb : nb0;
-    long A[kGuBlocksPerWave][8];
-    {
-        const uint8_t* rowp = stage + 16 * S.cpt * m + leads[m] + (size_t)r * rb;
-#pragma unroll
-        for (int j = 0; j < kGuBlocksPerWave; ++j)
-#pragma unroll
-            for (int sub = 0; sub < 8; ++sub)
-                A[j][sub] = b0 + j < b1 ? iq3s_a_operand(rowp + 110 * (b0 + j), tabs, sub, q) : 0;
-    }
+    XRegs<kGuBlocksPerWave> XR;
+    const uint8_t* rowp = stage + 16 * S.cpt * m + leads[m] + (size_t)r * rb;
     __syncthreads();                                        // scale tables written
-    const ActLayout XL(a.d_model, QT_Q8_K);
     const uint8_t* lsm = ls_tab + m * (nb * 8 * kGuRows);
     const float* dwm = dw_tab + m * (nb * kGuRows);
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
-        const int j = lane & 15;
         const bool valid = j < cnt;
-        const int t = a.pair_of[g0 + pt + min(j, cnt - 1)] / a.k;
-        const uint8_t* xrow = a.xq + (size_t)t * a.xq_stride;
+        pair_x(pt, XR);
         float c[kGuBlocksPerWave][4];
-        mfma_blocks<kGuBlocksPerWave>(A, b0, b1, xrow, valid, reinterpret_cast<const float*>(xrow + XL.off_d), lsm,
-                                      dwm, kGuRows, 0, q, c);
+        mfma_blocks<kGuBlocksPerWave>(rowp, tabs, b0, b1, XR, valid, lsm, dwm, kGuRows, 0, q, c);
         if (half) {
 #pragma unroll
             for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
@@ -319,37 +335,33 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
     const int row0 = blockIdx.x * kDownRows;
     const int nb = a.d_ff / 256;
     const size_t rb = row_bytes(QT, a.d_ff);
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    const int r = lane & 15, q = lane >> 4, rbase = 16 * wave, j = lane & 15;
+    const ActLayout HL(a.d_ff, QT_Q8_K);
     GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
     const uint8_t* wd = a.down + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     auto tile_ptr = [&](int) { return wd; };
     TileRun<QT> S{TileWalk<QT>(1, kDownRows, rb, a.d_ff)};
     tiles_begin(S, tile_ptr);
+    auto pair_x = [&](int pt, XRegs<kDownBlocks>& R) {
+        const int cnt = min(kPairTile, n_e - pt);
+        const uint8_t* hrow = a.hq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.hq_stride;
+        load_x(R, hrow, reinterpret_cast<const float*>(hrow + HL.off_d), 0, nb, q);
+    };
     store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     tiles_stage(S, stage, leads);
     __syncthreads();
     iq3s_scale_tables(stage, S.cpt, leads, 1, kDownRows, nb, rb, ls_tab, dw_tab);
-
-    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
-    const int r = lane & 15, q = lane >> 4, rbase = 16 * wave;
-    long A[kDownBlocks][8];
-    {
-        const uint8_t* rowp = stage + leads[0] + (size_t)(rbase + r) * rb;
-#pragma unroll
-        for (int j = 0; j < kDownBlocks; ++j)
-#pragma unroll
-            for (int sub = 0; sub < 8; ++sub) A[j][sub] = j < nb ? iq3s_a_operand(rowp + 110 * j, tabs, sub, q) : 0;
-    }
+    const uint8_t* rowp = stage + leads[0] + (size_t)(rbase + r) * rb;
     __syncthreads();
-    const ActLayout HL(a.d_ff, QT_Q8_K);
+    XRegs<kDownBlocks> XR;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
-        const int j = lane & 15;
         const bool valid = j < cnt;
         const int pos = g0 + pt + min(j, cnt - 1);
-        const uint8_t* hrow = a.hq + (size_t)pos * a.hq_stride;
+        pair_x(pt, XR);
         float c[kDownBlocks][4];
-        mfma_blocks<kDownBlocks>(A, 0, nb, hrow, valid, reinterpret_cast<const float*>(hrow + HL.off_d), ls_tab,
-                                 dw_tab, kDownRows, rbase, q, c);
+        mfma_blocks<kDownBlocks>(rowp, tabs, 0, nb, XR, valid, ls_tab, dw_tab, kDownRows, rbase, q, c);
         if (valid) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
