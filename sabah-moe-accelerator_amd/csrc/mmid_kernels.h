@@ -132,6 +132,11 @@ __host__ __device__ inline int tile_chunks(int tile_bytes) { return (tile_bytes 
 __host__ __device__ inline int tile_chunk_cap(int qt, int n_mat) {
     return min(kStageChunks / n_mat, stage_iters(qt) * (kThreads / n_mat));
 }
+// passes of at most vmax units each, all of about the same size
+__host__ __device__ inline int even_passes(int total, int vmax) {
+    const int np = (total + vmax - 1) / vmax;
+    return (total + np - 1) / np;
+}
 // units per tile per pass: the largest V with tile_chunks(V * unit bytes) <= tile_chunk_cap
 __host__ __device__ inline int pass_units(int qt, int n_mat, int unit_bytes) {
     return max(1, (16 * tile_chunk_cap(qt, n_mat) - 30) / unit_bytes);
@@ -243,7 +248,7 @@ struct TileWalk {
     float rcp_nus;
     __device__ TileWalk(int n_mat_, int nrows, size_t rb_, int k)
         : n_mat(uni(n_mat_)), NUS(uni(units_per_row(QT, k))), NCB(uni(contribs_per_row(QT, k))),
-          total(uni(nrows * units_per_row(QT, k))), V(uni(pass_units(QT, n_mat_, UB))), rb(rb_),
+          total(uni(nrows * units_per_row(QT, k))), V(uni(even_passes(total, pass_units(QT, n_mat_, UB)))), rb(rb_),
           rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
     __device__ int byte_of(int v) const {
         const int r = div_small(v, rcp_nus);

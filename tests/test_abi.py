@@ -92,3 +92,27 @@ def test_metrics_before_any_call():
     from sabah.runtime import rt
     m = rt.metrics()
     assert m["misses"] == 0 and m["evictions"] == 0 and m["bytes_fetched"] == 0
+
+
+def _desc(qt_gate=21, qt_up=21, qt_down=21, d_model=2048, d_ff=768, n_experts=512):
+    from sabah.runtime import rt
+    d = rt.MoeLayerDesc()
+    d.gate, d.up, d.down = 1, 1, 1                     # never dereferenced: the checks come first
+    d.qt_gate, d.qt_up, d.qt_down = qt_gate, qt_up, qt_down
+    d.d_model, d.d_ff, d.n_experts = d_model, d_ff, n_experts
+    return d
+
+
+@pytest.mark.parametrize("kw", [dict(qt_gate=12, qt_up=12, qt_down=14), dict(d_model=2560), dict(d_model=4096),
+                                dict(d_ff=1280), dict(n_experts=8192)])
+def test_prefill_layer_rejects_shapes_it_does_not_group_without_a_device(kw):
+    """The grouped layer takes IQ3_S, d_model a multiple of 512 up to 2048, d_ff a
+    multiple of 256 up to 1024 and n_experts <= 4096; anything else is refused
+    before the device is touched."""
+    from sabah.runtime import rt
+    L = rt.lib()
+    d = _desc(**kw)
+    vp = ctypes.c_void_p
+    rc = L.sabah_moe_prefill_layer(ctypes.byref(d), vp(1), vp(1), vp(1), 10, 4, vp(1), None, None)
+    assert rc == -1
+    assert "grouped MoE layer" in rt.last_error() or "unsupported type mix" in rt.last_error()
