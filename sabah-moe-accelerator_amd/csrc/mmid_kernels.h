@@ -498,6 +498,104 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Gate/up + SwiGLU in two rounds per wave, for packed IQ3_S rows whose units
+// per row divide 128.  R = 2 RR rows, RR = 128 / units per row: a round is RR
+// gate and RR up rows, 256 units, one per lane.  Wave w loads, stages and
+// decodes by itself the 64 contiguous units (tile w >> 1, half w & 1) of each
+// round, so a wave decodes as soon as its own bytes are in.  Both rounds'
+// loads are issued up front: round 0 is decoded while round 1 is in flight.
+// grid = (ceil(d_ff / R), n_slots, n_tokens)
+// ---------------------------------------------------------------------------
+constexpr int kRoundUnits = 64;
+// 16-byte chunks of one wave's round at any lead
+template <int QT>
+struct WaveRoundChunks {
+    static constexpr int V = (kRoundUnits * UnitFmt<QT>::BYTES + 30) / 16;
+};
+__host__ __device__ inline bool gate_up_rounds_ok(int qt, int d_model) {
+    const int nus = units_per_row(qt, d_model);
+    return qt == QT_IQ3_S && d_model % 256 == 0 && nus <= 128 && 128 % nus == 0;
+}
+__host__ __device__ inline int rows_gate_up_rounds(int qt, int d_model) { return 256 / units_per_row(qt, d_model); }
+
+template <int QT>
+__global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
+    constexpr int UB = UnitFmt<QT>::BYTES;
+    constexpr int N = StageIters<QT>::V;
+    constexpr int WCH = WaveRoundChunks<QT>::V;
+    static_assert(WCH <= 64 * N && 4 * 16 * WCH <= kStageBytes, "a wave's round must fit its loads and the stage");
+    SABAH_STATIC_LDS(QT)
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int NUS = units_per_row(QT, a.d_model), NCB = contribs_per_row(QT, a.d_model);
+    const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * NCB);
+    const int t = blockIdx.z, s = blockIdx.y, row0 = blockIdx.x * a.R;
+    const int nrows = min(a.R, a.d_ff - row0);
+    const size_t rb = row_bytes(QT, a.d_model);
+    float* h = a.h + ((size_t)t * a.n_slots + s) * a.d_ff + row0;
+    uint8_t* act = smem + P.off_act;
+    float* part = reinterpret_cast<float*>(smem + P.off_part);
+    const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
+    ActRegs<kRoundsX> xa;
+    act_prefetch<kRoundsX>(xb, xa);
+    GridRegs<kThreads> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    const uint8_t* wg = expert_ptr(a.G, a.rt, t, s, a.n_slots);
+    const uint8_t* wu = expert_ptr(a.U, a.rt, t, s, a.n_slots);
+    if (wg == nullptr || wu == nullptr) {
+        flag_error(a.err);
+        for (int r = threadIdx.x; r < nrows; r += blockDim.x) h[r] = __builtin_nanf("");
+        return;
+    }
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63u);
+    const int m = wave >> 1;
+    const uint8_t* tile = (m ? wu : wg) + (size_t)row0 * rb;
+    const int nvalid = nrows * NUS;                         // the tile's units in this workgroup
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    u32x4 d[2][N];
+    int q[2][N], lead[2], v0[2];
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+        v0[rd] = 128 * rd + 64 * (wave & 1);
+        const int nu = min(kRoundUnits, nvalid - v0[rd]);
+        const uint8_t* p = tile + (nu > 0 ? (size_t)v0[rd] * UB : 0);
+        lead[rd] = (int)(reinterpret_cast<uintptr_t>(p) & 15);
+        const uint8_t* g = p - lead[rd];
+        const int last = nu > 0 ? (lead[rd] + nu * UB - 1) >> 4 : 0;
+#pragma unroll
+        for (int it = 0; it < N; ++it) {
+            q[rd][it] = min(lane + 64 * it, last);
+            d[rd][it] = *(g_u32x4*)(g + 16 * q[rd][it]);
+        }
+    }
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    act_quantize<kRoundsX>(xb, xa);
+    __syncthreads();                                        // activations and tables ready
+    uint8_t* region = stage + 16 * WCH * wave;
+    const float rcp_nus = __builtin_amdgcn_rcpf((float)NUS);
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+        // the wave's own chunks: LDS operations of one wave complete in order,
+        // so its reads below see these writes, and round 1's writes come after
+        // round 0's reads
+#pragma unroll
+        for (int it = 0; it < N; ++it) *reinterpret_cast<u32x4*>(region + 16 * q[rd][it]) = d[rd][it];
+        if (lane < nvalid - v0[rd]) {
+            const int v = v0[rd] + lane;
+            const int r = div_small(v, rcp_nus), us = v - r * NUS;
+            LdsWindow<QT> Wn;
+            Wn.load(region + lead[rd] + lane * UB);
+            unit_into_part<QT>(Wn, tabs, act, a.d_model, us, part + (m * a.R + r) * NCB);
+        }
+    }
+    __syncthreads();                                        // partials complete
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        const float g = row_sum(part + r * NCB, NCB);
+        const float up = row_sum(part + (a.R + r) * NCB, NCB);
+        h[r] = __fmul_rn(silu_f32(g), up);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Fused down projection + routed combine (ggml: MUL_MAT_ID on h, ggml_mul by
 // the router weights, ggml_add over the slots in slot order), plus optional
 // shared-expert rows and residual:

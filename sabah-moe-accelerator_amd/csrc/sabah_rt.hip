@@ -148,7 +148,7 @@ hipError_t fit_lds(K kernel, int bytes, int total) {
 int rows_mmid(int qt, int k, bool packed) {
     return packed ? rows_per_wg(qt, k, 1) : std::min(kMaxTiles, rows_per_wg(qt, k, 1));
 }
-int rows_gate_up(int qt, int k) { return rows_per_wg(qt, k, 2); }
+int rows_gate_up(int qt, int k) { return gate_up_rounds_ok(qt, k) ? rows_gate_up_rounds(qt, k) : rows_per_wg(qt, k, 2); }
 int rows_down(int qt, int k, int n_slots) { return rows_per_wg(qt, k, n_slots); }
 
 bool check_sticky() {
@@ -221,8 +221,15 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
 template <int QT>
 hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * contribs_per_row(QT, a.d_model));
-    if (const hipError_t e = fit_lds(k_gate_up<QT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.d_ff + a.R - 1) / a.R), (unsigned)a.n_slots, (unsigned)n_tokens);
+    if constexpr (QT == QT_IQ3_S) {
+        if (gate_up_rounds_ok(QT, a.d_model) && a.R == rows_gate_up_rounds(QT, a.d_model)) {
+            if (const hipError_t e = fit_lds(k_gate_up_rounds<QT>, P.bytes, launch_lds(QT, P))) return e;
+            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT>, grid, P.bytes, st, a);
+            return hipGetLastError();
+        }
+    }
+    if (const hipError_t e = fit_lds(k_gate_up<QT>, P.bytes, launch_lds(QT, P))) return e;
     launch_kernel(KK_GATE_UP, k_gate_up<QT>, grid, P.bytes, st, a);
     return hipGetLastError();
 }

@@ -286,6 +286,25 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     assert_parity(out.cpu().numpy(), want, name)
 
 
+@pytest.mark.parametrize("D,F", [(512, 544), (1024, 800)])
+def test_iq3s_gate_up_with_a_partial_last_row_tile(hip_rt, orc, D, F):
+    """IQ3_S gate/up runs in two rounds of 256 units per workgroup (R = 256 /
+    units per row rows); d_ff here leaves the last workgroup a part of a round
+    (and, at 512 / 544, waves with no units at all)."""
+    from sabah.runtime import routing
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(D + F)
+    E, K, Tn, qts = 12, 4, 3, (IQ3_S, IQ3_S, Q8_0)
+    bank, raws = make_bank(orc, rng, qts, E, D, F)
+    ids, w = routing.uniform_routing(rng, Tn, E, K)
+    x = rng.standard_normal((Tn, D)).astype(np.float32)
+    ex = MoEExecutor(bank, max_used=K)
+    out = ex.run_layer(0, T(x), T(ids), T(w))
+    torch.cuda.synchronize()
+    want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], qts, x, ids, w)
+    assert_parity(out.cpu().numpy(), want, "partial row tile D=%d F=%d" % (D, F))
+
+
 def test_moe_chain_is_the_sequence_of_residual_layers(hip_rt, orc):
     from sabah.runtime import routing
     from sabah.runtime.executor import MoEExecutor
