@@ -17,6 +17,16 @@
 
 namespace sabah {
 
+// floor(a / b) for 0 <= a < 2^21, given r = rcp(b) (v_rcp_f32, 1 ulp): the
+// product's relative error stays below 2^-22, so its absolute error is below
+// (a + 0.5) / b * 2^-22 < 0.5 / b, while (a + 0.5) / b is at least 0.5 / b
+// away from an integer
+__device__ inline int div_small(int a, float r) { return (int)(((float)a + 0.5f) * r); }
+// the same for wave-uniform operands, returned as a scalar
+__device__ inline int div_small_u(int a, float r) { return __builtin_amdgcn_readfirstlane(div_small(a, r)); }
+__device__ inline int div_small_u(int a, int b) { return div_small_u(a, __builtin_amdgcn_rcpf((float)b)); }
+
+
 template <int CTRL>
 __device__ inline uint32_t dpp(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
@@ -200,18 +210,19 @@ template <int ROUNDS>
 __device__ inline void act_prefetch(const ActBatch& B, ActRegs<ROUNDS>& R, int w0 = 0) {
     const int slot = ((int)threadIdx.x - w0) >> 4, nslots = ((int)blockDim.x - w0) >> 4, l = threadIdx.x & 15;
     const int nch = (B.k + 255) / 256, nq = B.n_rows * nch;
+    const float rcp_nch = __builtin_amdgcn_rcpf((float)nch);
     const bool vec = act_vec(B);
 #pragma unroll
     for (int i = 0; i < ROUNDS; ++i) {
         const int q = min(slot + nslots * i, nq - 1);
-        const int r = q / nch, c = q - r * nch;
+        const int r = div_small(q, rcp_nch), c = q - r * nch;
         load16(B.x + (size_t)r * B.row_stride, c * 256 + 16 * l, B.k, vec, R.a[i]);
     }
 }
 
 __device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q) {
     const int nch = (B.k + 255) / 256;
-    const int r = q / nch, c = q - r * nch;
+    const int r = div_small(q, __builtin_amdgcn_rcpf((float)nch)), c = q - r * nch;
     const ActLayout L(B.k, B.at);
     const bool in = c * 256 + 16 * (int)(threadIdx.x & 15u) < B.k;
     Act16 a;
@@ -231,8 +242,9 @@ __device__ inline void act_quantize(const ActBatch& B, const ActRegs<ROUNDS>& R,
         if (q < nq) quant_chunk(B, R.a[i], q);
     }
     const bool vec = act_vec(B);
+    const float rcp_nch = __builtin_amdgcn_rcpf((float)nch);
     for (int q = slot + nslots * ROUNDS; q < nq; q += nslots) {
-        const int r = q / nch, c = q - r * nch;
+        const int r = div_small(q, rcp_nch), c = q - r * nch;
         Act16 a;
         load16(B.x + (size_t)r * B.row_stride, c * 256 + 16 * l, B.k, vec, a);
         quant_chunk(B, a, q);

@@ -65,6 +65,21 @@ __device__ inline const uint8_t* expert_ptr(const ExpertSrc& E, const Routing& R
     return E.base + (size_t)e * E.expert_stride;
 }
 
+// The gate and up matrices of (token t, slot s): one id read serves both (or
+// both table entries are requested before either is waited for)
+__device__ inline void expert_pair(const ExpertSrc& G, const ExpertSrc& U, const Routing& R, int t, int s,
+                                   int n_slots, const uint8_t*& g, const uint8_t*& u) {
+    if (G.ptrs || U.ptrs) {
+        g = expert_ptr(G, R, t, s, n_slots);
+        u = expert_ptr(U, R, t, s, n_slots);
+        return;
+    }
+    const int e = R.ids ? read_id(R, t, s) : 0;
+    const bool ok = e >= 0 && e < R.n_experts;
+    g = ok ? G.base + (size_t)e * G.expert_stride : nullptr;
+    u = ok ? U.base + (size_t)e * U.expert_stride : nullptr;
+}
+
 // Per-lane form for a table or id array that is present (E.ptrs or R.ids):
 // the routing word of (t, s) is read with two unconditional 4-byte loads
 // (the id is read twice), and resolved in a separate step, so a kernel can
@@ -136,6 +151,16 @@ __host__ __device__ inline int tile_chunk_cap(int qt, int n_mat) {
 __host__ __device__ inline int even_passes(int total, int vmax) {
     const int np = (total + vmax - 1) / vmax;
     return (total + np - 1) / np;
+}
+// the device forms of tile_chunk_cap / pass_units / even_passes: the same
+// values through div_small (a generic integer division is some forty
+// instructions on the kernels' critical path)
+__device__ inline int tile_chunk_cap_d(int qt, int n_mat) {
+    return min(div_small_u(kStageChunks, n_mat), stage_iters(qt) * div_small_u(kThreads, n_mat));
+}
+__device__ inline int even_passes_d(int total, int vmax) {
+    const int np = div_small_u(total + vmax - 1, vmax);
+    return div_small_u(total + np - 1, np);
 }
 // units per tile per pass: the largest V with tile_chunks(V * unit bytes) <= tile_chunk_cap
 __host__ __device__ inline int pass_units(int qt, int n_mat, int unit_bytes) {
@@ -228,15 +253,6 @@ __device__ inline float row_sum(const float* part_row, int n) {
     return s;
 }
 
-// floor(a / b) for 0 <= a < 2^21, given r = rcp(b) (v_rcp_f32, 1 ulp): the
-// product's relative error stays below 2^-22, so its absolute error is below
-// (a + 0.5) / b * 2^-22 < 0.5 / b, while (a + 0.5) / b is at least 0.5 / b
-// away from an integer
-__device__ inline int div_small(int a, float r) { return (int)(((float)a + 0.5f) * r); }
-// the same for wave-uniform operands, returned as a scalar
-__device__ inline int div_small_u(int a, float r) { return __builtin_amdgcn_readfirstlane(div_small(a, r)); }
-__device__ inline int div_small_u(int a, int b) { return div_small_u(a, __builtin_amdgcn_rcpf((float)b)); }
-
 // One workgroup's tiles.  Tile t is matrix tile_ptr(t) from its first row on
 // (row0 already folded into the pointer): `nrows` rows of k elements at rb
 // bytes, so its unit v = r * NUS + us sits at byte r * rb + us * unit bytes.
@@ -248,7 +264,8 @@ struct TileWalk {
     float rcp_nus;
     __device__ TileWalk(int n_mat_, int nrows, size_t rb_, int k)
         : n_mat(uni(n_mat_)), NUS(uni(units_per_row(QT, k))), NCB(uni(contribs_per_row(QT, k))),
-          total(uni(nrows * units_per_row(QT, k))), V(uni(even_passes(total, pass_units(QT, n_mat_, UB)))), rb(rb_),
+          total(uni(nrows * units_per_row(QT, k))),
+          V(even_passes_d(total, max(1, (16 * tile_chunk_cap_d(QT, n_mat_) - 30) / UB))), rb(rb_),
           rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
     __device__ int byte_of(int v) const {
         const int r = div_small(v, rcp_nus);
@@ -331,7 +348,7 @@ __device__ inline void pass_decode(const TileRun<QT>& S, const uint8_t* tabs, co
 template <int QT, typename TilePtr>
 __device__ inline void tiles_begin(TileRun<QT>& S, TilePtr tile_ptr) {
     const int g = (int)threadIdx.x;
-    S.lpt = uni(kThreads / S.T.n_mat);
+    S.lpt = div_small_u(kThreads, S.T.n_mat);
     const int lt = div_small(g, __builtin_amdgcn_rcpf((float)S.lpt));
     const bool idle = lt >= S.T.n_mat;
     S.lt = idle ? S.T.n_mat - 1 : lt;
@@ -475,8 +492,8 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
     act_prefetch<kRoundsX>(xb, xa);
     GridRegs<kThreads> gr;
     if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
-    const uint8_t* wg = expert_ptr(a.G, a.rt, t, s, a.n_slots);
-    const uint8_t* wu = expert_ptr(a.U, a.rt, t, s, a.n_slots);
+    const uint8_t *wg, *wu;
+    expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
         for (int r = threadIdx.x; r < nrows; r += blockDim.x) h[r] = __builtin_nanf("");
@@ -539,8 +556,8 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
     act_prefetch<kRoundsX>(xb, xa);
     GridRegs<kThreads> gr;
     if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
-    const uint8_t* wg = expert_ptr(a.G, a.rt, t, s, a.n_slots);
-    const uint8_t* wu = expert_ptr(a.U, a.rt, t, s, a.n_slots);
+    const uint8_t *wg, *wu;
+    expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
         for (int r = threadIdx.x; r < nrows; r += blockDim.x) h[r] = __builtin_nanf("");
