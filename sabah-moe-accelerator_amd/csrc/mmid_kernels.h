@@ -135,9 +135,11 @@ constexpr int kMaxTiles = 64;
 __host__ __device__ constexpr int stage_iters(int qt) {
     return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : 9;
 }
-template <int QT>
+// the same load count spread over nt threads
+__host__ __device__ constexpr int stage_iters_nt(int qt, int nt) { return (stage_iters(qt) * kThreads + nt - 1) / nt; }
+template <int QT, int NT = kThreads>
 struct StageIters {
-    static constexpr int V = stage_iters(QT);
+    static constexpr int V = stage_iters_nt(QT, NT);
 };
 
 // chunks of a tile of tile_bytes at any lead
@@ -155,8 +157,8 @@ __host__ __device__ inline int even_passes(int total, int vmax) {
 // the device forms of tile_chunk_cap / pass_units / even_passes: the same
 // values through div_small (a generic integer division is some forty
 // instructions on the kernels' critical path)
-__device__ inline int tile_chunk_cap_d(int qt, int n_mat) {
-    return min(div_small_u(kStageChunks, n_mat), stage_iters(qt) * div_small_u(kThreads, n_mat));
+__device__ inline int tile_chunk_cap_d(int qt, int n_mat, int nt) {
+    return min(div_small_u(kStageChunks, n_mat), stage_iters_nt(qt, nt) * div_small_u(nt, n_mat));
 }
 __device__ inline int even_passes_d(int total, int vmax) {
     const int np = div_small_u(total + vmax - 1, vmax);
@@ -256,7 +258,7 @@ __device__ inline float row_sum(const float* part_row, int n) {
 // One workgroup's tiles.  Tile t is matrix tile_ptr(t) from its first row on
 // (row0 already folded into the pointer): `nrows` rows of k elements at rb
 // bytes, so its unit v = r * NUS + us sits at byte r * rb + us * unit bytes.
-template <int QT>
+template <int QT, int NT = kThreads>
 struct TileWalk {
     static constexpr int UB = UnitFmt<QT>::BYTES;
     int n_mat, NUS, NCB, total, V;
@@ -265,7 +267,7 @@ struct TileWalk {
     __device__ TileWalk(int n_mat_, int nrows, size_t rb_, int k)
         : n_mat(uni(n_mat_)), NUS(uni(units_per_row(QT, k))), NCB(uni(contribs_per_row(QT, k))),
           total(uni(nrows * units_per_row(QT, k))),
-          V(even_passes_d(total, max(1, (16 * tile_chunk_cap_d(QT, n_mat_) - 30) / UB))), rb(rb_),
+          V(even_passes_d(total, max(1, (16 * tile_chunk_cap_d(QT, n_mat_, NT) - 30) / UB))), rb(rb_),
           rcp_nus(__builtin_amdgcn_rcpf((float)units_per_row(QT, k))) {}
     __device__ int byte_of(int v) const {
         const int r = div_small(v, rcp_nus);
@@ -280,11 +282,11 @@ struct TileWalk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// one pass of the workgroup's tiles
-template <int QT>
+// one pass of the workgroup's tiles (NT threads)
+template <int QT, int NT = kThreads>
 struct TileRun {
-    static constexpr int N = StageIters<QT>::V;
-    TileWalk<QT> T;
+    static constexpr int N = StageIters<QT, NT>::V;
+    TileWalk<QT, NT> T;
     int v0, nv, cpt, b0, span;        // pass (uniform): first unit, units per tile, chunks per tile,
                                       // byte of unit v0, bytes of nv units
     int lpt, lt, lj;                  // lanes per tile; this lane's load tile and its index in it
@@ -294,8 +296,8 @@ struct TileRun {
     int lead;                         // the load tile's pass start address mod 16
 };
 
-template <int QT>
-__device__ inline void set_pass(TileRun<QT>& S, int v0) {
+template <int QT, int NT>
+__device__ inline void set_pass(TileRun<QT, NT>& S, int v0) {
     S.v0 = v0;
     S.nv = uni(min(S.T.V, S.T.total - v0));
     S.b0 = S.T.byte_of_u(v0);
@@ -303,8 +305,8 @@ __device__ inline void set_pass(TileRun<QT>& S, int v0) {
     S.cpt = uni(tile_chunks(S.span));
 }
 
-template <int QT>
-__device__ inline void pass_load(TileRun<QT>& S) {
+template <int QT, int NT>
+__device__ inline void pass_load(TileRun<QT, NT>& S) {
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
     const uint8_t* P = S.src + S.b0;
     S.lead = (int)(reinterpret_cast<uintptr_t>(P) & 15);
@@ -317,38 +319,58 @@ __device__ inline void pass_load(TileRun<QT>& S) {
     }
 }
 
-template <int QT>
-__device__ inline void pass_store(const TileRun<QT>& S, uint8_t* stage, int* leads) {
+template <int QT, int NT>
+__device__ inline void pass_store(const TileRun<QT, NT>& S, uint8_t* stage, int* leads) {
     uint8_t* dst = stage + 16 * S.cpt * S.lt;
 #pragma unroll
     for (int it = 0; it < S.N; ++it) *reinterpret_cast<u32x4*>(dst + 16 * S.q[it]) = S.d[it];
     if (S.lj == 0) leads[S.lt] = S.lead;
 }
 
-// decode the pass's units, kThreads apart per lane; contributions of unit
-// (t, r, us) go to part + (t * part_rows + r) * NCB
-template <int QT>
-__device__ inline void pass_decode(const TileRun<QT>& S, const uint8_t* tabs, const uint8_t* stage, const int* leads,
-                                   int k, const uint8_t* act0, int act_stride, int part_rows, float* part) {
+// decode the pass's units, NT apart per lane (with 512 IQ3_S threads, a unit
+// per lane pair: each lane sums half its items and the pair adds the two
+// exact integer sums); contributions of unit (t, r, us) go to
+// part + (t * part_rows + r) * NCB
+template <int QT, int NT>
+__device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs, const uint8_t* stage,
+                                   const int* leads, int k, const uint8_t* act0, int act_stride, int part_rows,
+                                   float* part) {
+    constexpr bool SPLIT = QT == QT_IQ3_S && NT == 2 * kThreads;
+    constexpr int PER = SPLIT ? 2 : 1;                  // lanes per unit
     const int n = S.T.n_mat * S.nv;
     const float rcp_nv = __builtin_amdgcn_rcpf((float)S.nv);
-    for (int u = (int)threadIdx.x; u < n; u += kThreads) {
+    const int half = SPLIT ? (int)(threadIdx.x & 1u) : 0;
+    for (int u = (int)threadIdx.x / PER; u < n; u += NT / PER) {     // both lanes of a pair iterate together
         const int t = div_small(u, rcp_nv);
         const int v = S.v0 + (u - t * S.nv);             // tile-relative unit (row-major over the rows)
         const int r = div_small(v, S.T.rcp_nus), us = v - r * S.T.NUS;
         LdsWindow<QT> Wn;
         Wn.load(stage + 16 * S.cpt * t + leads[t] + (int)((size_t)r * S.T.rb) + us * TileWalk<QT>::UB - S.b0);
-        unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, part + (t * part_rows + r) * S.T.NCB);
+        float* prow = part + (t * part_rows + r) * S.T.NCB;
+        if constexpr (SPLIT) {
+            const uint8_t* act = act0 + t * act_stride;
+            const ActLayout AL(k, QT_Q8_K);
+            uint32_t F[UnitFmt<QT>::NF];
+            uint32_t Fm1;
+            Wn.fields(F, Fm1);
+            int bs = iq3s_half_bsum(F, tabs, act + us * kActChunkStride, half);
+            bs += (int)dpp<kDppXor1>((uint32_t)bs);       // the partner lane's half
+            if (half == 0)
+                prow[us] = __fmul_rn(__fmul_rn(h2f(Fm1 >> 16), reinterpret_cast<const float*>(act + AL.off_d)[us]),
+                                     (float)bs);
+        } else {
+            unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, prow);
+        }
     }
 }
 
 // Issue the first pass's loads.  tile_ptr(t) is the first row of tile t, for
 // a per-lane t.  The caller issues its own prologue loads before this and
 // waits for them after it (loads complete in order), then calls tiles_finish.
-template <int QT, typename TilePtr>
-__device__ inline void tiles_begin(TileRun<QT>& S, TilePtr tile_ptr) {
+template <int QT, int NT, typename TilePtr>
+__device__ inline void tiles_begin(TileRun<QT, NT>& S, TilePtr tile_ptr) {
     const int g = (int)threadIdx.x;
-    S.lpt = div_small_u(kThreads, S.T.n_mat);
+    S.lpt = div_small_u(NT, S.T.n_mat);
     const int lt = div_small(g, __builtin_amdgcn_rcpf((float)S.lpt));
     const bool idle = lt >= S.T.n_mat;
     S.lt = idle ? S.T.n_mat - 1 : lt;
@@ -361,13 +383,13 @@ __device__ inline void tiles_begin(TileRun<QT>& S, TilePtr tile_ptr) {
 // Stage and decode every pass.  The workgroup barrier after the stores also
 // publishes what the caller's prologue wrote to LDS (activations, tables);
 // the one after each decode frees the stage and publishes the partials.
-template <int QT>
-__device__ inline void tiles_finish(TileRun<QT>& S, const uint8_t* tabs, uint8_t* stage, int* leads, int k,
+template <int QT, int NT>
+__device__ inline void tiles_finish(TileRun<QT, NT>& S, const uint8_t* tabs, uint8_t* stage, int* leads, int k,
                                     const uint8_t* act0, int act_stride, int part_rows, float* part) {
     for (;;) {
         pass_store(S, stage, leads);
         __syncthreads();
-        const TileRun<QT> C = S;                 // this pass (the registers of the next one are reused)
+        const TileRun<QT, NT> C = S;             // this pass (the registers of the next one are reused)
         const int next = C.v0 + C.nv;
         if (next < S.T.total) {
             set_pass(S, next);
@@ -633,8 +655,9 @@ struct DownArgs {
     unsigned int* err;
 };
 
-template <int QT>
-__global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
+template <int QT, int NT = kThreads>
+__global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
+    constexpr int RH = NT == kThreads ? kRoundsH : 1;      // activation rounds prefetched
     SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.d_ff);
@@ -653,18 +676,18 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const ActBatch hb{a.h + (size_t)t * a.n_slots * a.d_ff, (size_t)a.d_ff, a.n_slots, a.d_ff, act_type(QT), act,
                       P.act_bytes};
-    ActRegs<kRoundsH> ha;
-    act_prefetch<kRoundsH>(hb, ha);
-    GridRegs<kThreads> gr;
-    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    ActRegs<RH> ha;
+    act_prefetch<RH>(hb, ha);
+    GridRegs<NT> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
     const uint8_t* e = resolve_slot_word(a.D, a.rt, sw);
     const bool bad = __any(e == nullptr);
     const uint8_t* mine = (e ? e : a.D.base) + (size_t)row0 * rb;
     auto tile_ptr = [&](int m) { return lane_ptr(mine, m); };
-    TileRun<QT> S{TileWalk<QT>(a.n_slots, nrows, rb, a.d_ff)};
+    TileRun<QT, NT> S{TileWalk<QT, NT>(a.n_slots, nrows, rb, a.d_ff)};
     tiles_begin(S, tile_ptr);
-    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
-    act_quantize<kRoundsH>(hb, ha);
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
+    act_quantize<RH>(hb, ha);
     tiles_finish(S, tabs, stage, leads, a.d_ff, act, P.act_bytes, a.R, part);
     float* o = a.out + (size_t)t * a.d_model + row0;
     if (bad) {

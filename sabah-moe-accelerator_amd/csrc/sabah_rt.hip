@@ -76,7 +76,7 @@ unsigned long long g_kind_launches[KK_COUNT] = {0};
 // start and a stop event (hipExtLaunchKernelGGL), so the pair brackets that
 // kernel's execution on its stream and nothing else.
 template <typename K, typename A>
-void launch_kernel(int kind, K kernel, dim3 grid, int lds, hipStream_t st, const A& args) {
+void launch_kernel(int kind, K kernel, dim3 grid, int lds, hipStream_t st, const A& args, int threads = kThreads) {
     if (g_timing) {
         if (g_ev_free.empty()) {
             EvPair p{};
@@ -86,12 +86,12 @@ void launch_kernel(int kind, K kernel, dim3 grid, int lds, hipStream_t st, const
             EvPair ev = g_ev_free.back();
             g_ev_free.pop_back();
             ev.kind = kind;
-            hipExtLaunchKernelGGL(kernel, grid, dim3(kThreads), (uint32_t)lds, st, ev.a, ev.b, 0u, args);
+            hipExtLaunchKernelGGL(kernel, grid, dim3(threads), (uint32_t)lds, st, ev.a, ev.b, 0u, args);
             g_ev_pending.push_back(ev);
             return;
         }
     }
-    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, st, args);
+    hipLaunchKernelGGL(kernel, grid, dim3(threads), lds, st, args);
 }
 
 int fail(const char* fmt, ...) {
@@ -246,10 +246,12 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
 
 template <int QT>
 hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
+    // IQ3_S runs 512 threads, two lanes per unit (twice the waves to hide the decode's LDS latency)
+    constexpr int NT = QT == QT_IQ3_S ? 2 * kThreads : kThreads;
     const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * contribs_per_row(QT, a.d_ff));
-    if (const hipError_t e = fit_lds(k_down_combine<QT>, P.bytes, launch_lds(QT, P))) return e;
+    if (const hipError_t e = fit_lds(k_down_combine<QT, NT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
-    launch_kernel(KK_DOWN, k_down_combine<QT>, grid, P.bytes, st, a);
+    launch_kernel(KK_DOWN, k_down_combine<QT, NT>, grid, P.bytes, st, a, NT);
     return hipGetLastError();
 }
 

@@ -223,6 +223,33 @@ __device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* 
     return 2 * (int)((F[26] >> (4 * ib)) & 15u) + 1;
 }
 
+// The exact integer sum over items 4h .. 4h + 3 (h = 0 or 1, per lane) of an
+// IQ3_S unit: sum ls(ib) * (weights . activations).  The half's fields are
+// moved to items 0..3's places with selects, so every register index stays
+// static.  chunk is the unit's 256-element activation chunk.
+__device__ inline int iq3s_half_bsum(const uint32_t (&F)[27], const uint8_t* smem, const uint8_t* chunk, int h) {
+    uint32_t G[27];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) G[i] = h ? F[8 + i] : F[i];          // qs of items 4h ..
+    G[16] = h ? F[17] : F[16];                                      // their qh bytes
+#pragma unroll
+    for (int i = 0; i < 4; ++i) G[18 + i] = h ? F[22 + i] : F[18 + i];   // their sign bytes
+    G[26] = h ? F[26] >> 16 : F[26];                                // their scale nibbles
+    const uint8_t* ch = chunk + 128 * h;
+    int bsum = 0;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+        uint32_t v[8], A[8];
+        const int ls = iq3s_item(G, ib, smem, v);
+        act8(ch, ib, A);
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
+        bsum += __mul24(ls, s);
+    }
+    return bsum;
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K: element 32j + l = d*sc_j*nib - dmin*m_j, nibble low (j even) / high (j
 // odd) of qs[32*(j/2) + l].  F[0] = d | dmin << 16, F[1..3] packed 6-bit
