@@ -539,30 +539,41 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
 // ---------------------------------------------------------------------------
 // Gate/up + SwiGLU in two rounds per wave, for packed IQ3_S rows whose units
 // per row divide 128.  R = 2 RR rows, RR = 128 / units per row: a round is RR
-// gate and RR up rows, 256 units, one per lane.  Wave w loads, stages and
-// decodes by itself the 64 contiguous units (tile w >> 1, half w & 1) of each
-// round, so a wave decodes as soon as its own bytes are in.  Both rounds'
-// loads are issued up front: round 0 is decoded while round 1 is in flight.
+// gate and RR up rows, 256 units.  With NT = 512 two lanes share a unit (each
+// sums half its items; DPP adds the pair's exact integer sums), so a wave
+// owns 32 units of a round; with NT = 256 a wave owns 64.  A wave loads,
+// stages and decodes its own contiguous units of each round, so it decodes as
+// soon as its own bytes are in; both rounds' loads are issued up front, so
+// round 0 is decoded while round 1 is in flight.
 // grid = (ceil(d_ff / R), n_slots, n_tokens)
 // ---------------------------------------------------------------------------
-constexpr int kRoundUnits = 64;
-// 16-byte chunks of one wave's round at any lead
-template <int QT>
+// units of a round per wave
+template <int NT>
+struct RoundUnits {
+    static constexpr int PER = NT / kThreads;              // lanes per unit
+    static constexpr int V = 64 / PER;
+};
+// 16-byte chunks of one wave's round at any lead, and the loads per lane that cover them
+template <int QT, int NT>
 struct WaveRoundChunks {
-    static constexpr int V = (kRoundUnits * UnitFmt<QT>::BYTES + 30) / 16;
+    static constexpr int V = (RoundUnits<NT>::V * UnitFmt<QT>::BYTES + 30) / 16;
+    static constexpr int LOADS = (V + 63) / 64;
 };
 __host__ __device__ inline bool gate_up_rounds_ok(int qt, int d_model) {
     const int nus = units_per_row(qt, d_model);
     return qt == QT_IQ3_S && d_model % 256 == 0 && nus <= 128 && 128 % nus == 0;
 }
 __host__ __device__ inline int rows_gate_up_rounds(int qt, int d_model) { return 256 / units_per_row(qt, d_model); }
+constexpr int kGateUpRoundThreads = 2 * kThreads;
 
-template <int QT>
-__global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
+template <int QT, int NT>
+__global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
     constexpr int UB = UnitFmt<QT>::BYTES;
-    constexpr int N = StageIters<QT>::V;
-    constexpr int WCH = WaveRoundChunks<QT>::V;
-    static_assert(WCH <= 64 * N && 4 * 16 * WCH <= kStageBytes, "a wave's round must fit its loads and the stage");
+    constexpr int PER = RoundUnits<NT>::PER, UPW = RoundUnits<NT>::V;
+    constexpr int WPT = 128 / UPW;                          // waves per tile and round
+    constexpr int WCH = WaveRoundChunks<QT, NT>::V, N = WaveRoundChunks<QT, NT>::LOADS;
+    static_assert((NT / 64) * 16 * WCH <= kStageBytes, "the waves' rounds must fit the stage");
+    static_assert(PER == 1 || QT == QT_IQ3_S, "split units are IQ3_S only");
     SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NUS = units_per_row(QT, a.d_model), NCB = contribs_per_row(QT, a.d_model);
@@ -576,8 +587,8 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
     act_prefetch<kRoundsX>(xb, xa);
-    GridRegs<kThreads> gr;
-    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    GridRegs<NT> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
     const uint8_t *wg, *wu;
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
@@ -586,7 +597,7 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
         return;
     }
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63u);
-    const int m = wave >> 1;
+    const int m = wave / WPT;
     const uint8_t* tile = (m ? wu : wg) + (size_t)row0 * rb;
     const int nvalid = nrows * NUS;                         // the tile's units in this workgroup
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
@@ -594,8 +605,8 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
     int q[2][N], lead[2], v0[2];
 #pragma unroll
     for (int rd = 0; rd < 2; ++rd) {
-        v0[rd] = 128 * rd + 64 * (wave & 1);
-        const int nu = min(kRoundUnits, nvalid - v0[rd]);
+        v0[rd] = 128 * rd + UPW * (wave % WPT);
+        const int nu = min(UPW, nvalid - v0[rd]);
         const uint8_t* p = tile + (nu > 0 ? (size_t)v0[rd] * UB : 0);
         lead[rd] = (int)(reinterpret_cast<uintptr_t>(p) & 15);
         const uint8_t* g = p - lead[rd];
@@ -606,11 +617,12 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
             d[rd][it] = *(g_u32x4*)(g + 16 * q[rd][it]);
         }
     }
-    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsX>(xb, xa);
     __syncthreads();                                        // activations and tables ready
     uint8_t* region = stage + 16 * WCH * wave;
     const float rcp_nus = __builtin_amdgcn_rcpf((float)NUS);
+    const int j = lane / PER, half = lane & (PER - 1);      // the lane's unit in the round and its half
 #pragma unroll
     for (int rd = 0; rd < 2; ++rd) {
         // the wave's own chunks: LDS operations of one wave complete in order,
@@ -618,12 +630,25 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_rounds(GateUpArgs a) {
         // round 0's reads
 #pragma unroll
         for (int it = 0; it < N; ++it) *reinterpret_cast<u32x4*>(region + 16 * q[rd][it]) = d[rd][it];
-        if (lane < nvalid - v0[rd]) {
-            const int v = v0[rd] + lane;
+        if (j < nvalid - v0[rd]) {                          // both lanes of a pair alike
+            const int v = v0[rd] + j;
             const int r = div_small(v, rcp_nus), us = v - r * NUS;
             LdsWindow<QT> Wn;
-            Wn.load(region + lead[rd] + lane * UB);
-            unit_into_part<QT>(Wn, tabs, act, a.d_model, us, part + (m * a.R + r) * NCB);
+            Wn.load(region + lead[rd] + j * UB);
+            float* prow = part + (m * a.R + r) * NCB;
+            if constexpr (PER == 2) {
+                const ActLayout AL(a.d_model, QT_Q8_K);
+                uint32_t F[UnitFmt<QT>::NF];
+                uint32_t Fm1;
+                Wn.fields(F, Fm1);
+                int bs = iq3s_half_bsum(F, tabs, act + us * kActChunkStride, half);
+                bs += (int)dpp<kDppXor1>((uint32_t)bs);
+                if (half == 0)
+                    prow[us] = __fmul_rn(__fmul_rn(h2f(Fm1 >> 16), reinterpret_cast<const float*>(act + AL.off_d)[us]),
+                                         (float)bs);
+            } else {
+                unit_into_part<QT>(Wn, tabs, act, a.d_model, us, prow);
+            }
         }
     }
     __syncthreads();                                        // partials complete

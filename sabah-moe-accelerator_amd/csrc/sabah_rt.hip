@@ -224,8 +224,9 @@ hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
     dim3 grid((unsigned)((a.d_ff + a.R - 1) / a.R), (unsigned)a.n_slots, (unsigned)n_tokens);
     if constexpr (QT == QT_IQ3_S) {
         if (gate_up_rounds_ok(QT, a.d_model) && a.R == rows_gate_up_rounds(QT, a.d_model)) {
-            if (const hipError_t e = fit_lds(k_gate_up_rounds<QT>, P.bytes, launch_lds(QT, P))) return e;
-            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT>, grid, P.bytes, st, a);
+            constexpr int NT = kGateUpRoundThreads;
+            if (const hipError_t e = fit_lds(k_gate_up_rounds<QT, NT>, P.bytes, launch_lds(QT, P))) return e;
+            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT, NT>, grid, P.bytes, st, a, NT);
             return hipGetLastError();
         }
     }
