@@ -186,8 +186,9 @@ def main() -> int:
     return 0
 
 
-KERNEL_SYMBOL = {"gate_up": "k_gate_up", "down": "k_down_combine", "mmid": "k_mmid",
-                 "grouped_gate_up": "k_grouped_gate_up", "grouped_down": "k_grouped_down"}
+# kernel symbols of each timing kind, as the traffic summaries name them
+KERNEL_SYMBOL = {"gate_up": ("k_gate_up_rounds", "k_gate_up"), "down": ("k_down_combine",), "mmid": ("k_mmid",),
+                 "grouped_gate_up": ("k_grouped_gate_up",), "grouped_down": ("k_grouped_down",)}
 INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
 
 
@@ -351,9 +352,13 @@ def measured_traffic(workload, kind):
     path = os.path.join(ROOT, "profiles", "decode_kernels_%s_traffic.json" % workload)
     try:
         with open(path) as f:
-            return json.load(f)["kernels"][KERNEL_SYMBOL[kind]]["traffic_bytes"]
+            kernels = json.load(f)["kernels"]
     except (OSError, KeyError, ValueError):
         return None
+    for sym in KERNEL_SYMBOL[kind]:
+        if sym in kernels:
+            return kernels[sym]["traffic_bytes"]
+    return None
 
 
 def cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np, dev):
