@@ -721,10 +721,16 @@ __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
         return;
     }
     const float* wt = a.w + (size_t)t * a.n_slots;
+    // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
+    const float rcp_r = __builtin_amdgcn_rcpf((float)a.R);
+    for (int i = threadIdx.x; i < a.n_slots * a.R; i += blockDim.x) {
+        const int sl = div_small(i, rcp_r);
+        if (i - sl * a.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), wt[sl]);
+    }
+    __syncthreads();
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
-        float acc = __fmul_rn(row_sum(part + r * NCB, NCB), wt[0]);
-        for (int s = 1; s < a.n_slots; ++s)
-            acc = __fadd_rn(acc, __fmul_rn(row_sum(part + (s * a.R + r) * NCB, NCB), wt[s]));
+        float acc = part[r * NCB];
+        for (int s = 1; s < a.n_slots; ++s) acc = __fadd_rn(acc, part[(s * a.R + r) * NCB]);
         if (a.shared) acc = __fadd_rn(acc, a.shared[(size_t)t * a.d_model + row0 + r]);
         if (a.resid) acc = __fadd_rn(a.resid[(size_t)t * a.d_model + row0 + r], acc);
         if (a.accumulate) acc = __fadd_rn(o[r], acc);
