@@ -703,6 +703,17 @@ __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
                       P.act_bytes};
     ActRegs<RH> ha;
     act_prefetch<RH>(hb, ha);
+    // the epilogue's own inputs (router weight of this thread's first
+    // (slot, row) and this thread's row of shared / resid / out) are read now,
+    // so their latency hides behind the expert loads
+    const float* wt = a.w + (size_t)t * a.n_slots;
+    const float rcp_r = __builtin_amdgcn_rcpf((float)a.R);
+    const int i0 = (int)threadIdx.x, r0 = (int)threadIdx.x;
+    const float w0 = i0 < a.n_slots * a.R ? wt[div_small(i0, rcp_r)] : 0.0f;
+    const size_t orow = (size_t)t * a.d_model + row0 + r0;
+    const float sh0 = a.shared && r0 < nrows ? a.shared[orow] : 0.0f;
+    const float rs0 = a.resid && r0 < nrows ? a.resid[orow] : 0.0f;
+    const float ac0 = a.accumulate && r0 < nrows ? a.out[orow] : 0.0f;
     GridRegs<NT> gr;
     if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
     const uint8_t* e = resolve_slot_word(a.D, a.rt, sw);
@@ -720,20 +731,19 @@ __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
         for (int r = threadIdx.x; r < nrows; r += blockDim.x) o[r] = __builtin_nanf("");
         return;
     }
-    const float* wt = a.w + (size_t)t * a.n_slots;
     // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
-    const float rcp_r = __builtin_amdgcn_rcpf((float)a.R);
-    for (int i = threadIdx.x; i < a.n_slots * a.R; i += blockDim.x) {
+    for (int i = i0; i < a.n_slots * a.R; i += blockDim.x) {
         const int sl = div_small(i, rcp_r);
-        if (i - sl * a.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), wt[sl]);
+        if (i - sl * a.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : wt[sl]);
     }
     __syncthreads();
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+    for (int r = r0; r < nrows; r += blockDim.x) {
+        const size_t q = (size_t)t * a.d_model + row0 + r;
         float acc = part[r * NCB];
         for (int s = 1; s < a.n_slots; ++s) acc = __fadd_rn(acc, part[(s * a.R + r) * NCB]);
-        if (a.shared) acc = __fadd_rn(acc, a.shared[(size_t)t * a.d_model + row0 + r]);
-        if (a.resid) acc = __fadd_rn(a.resid[(size_t)t * a.d_model + row0 + r], acc);
-        if (a.accumulate) acc = __fadd_rn(o[r], acc);
+        if (a.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : a.shared[q]);
+        if (a.resid) acc = __fadd_rn(r == r0 ? rs0 : a.resid[q], acc);
+        if (a.accumulate) acc = __fadd_rn(r == r0 ? ac0 : o[r], acc);
         o[r] = acc;
     }
 }
