@@ -537,27 +537,41 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up + SwiGLU in two rounds per wave, for packed IQ3_S rows whose units
-// per row divide 128.  R = 2 RR rows, RR = 128 / units per row: a round is RR
-// gate and RR up rows, 256 units.  With NT = 512 two lanes share a unit (each
-// sums half its items; DPP adds the pair's exact integer sums), so a wave
-// owns 32 units of a round; with NT = 256 a wave owns 64.  A wave loads,
-// stages and decodes its own contiguous units of each round, so it decodes as
-// soon as its own bytes are in; both rounds' loads are issued up front, so
-// round 0 is decoded while round 1 is in flight.
+// Gate/up + SwiGLU in rounds, for packed IQ3_S rows whose units per row
+// divide 128.  R = 2 RR rows, RR = 128 / units per row: a workgroup owns R
+// gate and R up rows, 256 units of each.  With PER = 2 two lanes share a unit
+// (each sums half its items; DPP adds the pair's exact integer sums), so a
+// wave owns 32 units of a round; with PER = 1 it owns 64.  Half the waves take
+// the gate rows, half the up rows; a wave loads, stages and decodes its own
+// contiguous units of each of its rounds, so it decodes as soon as its own
+// bytes are in.  Every round's loads are issued up front: with 512 threads a
+// wave has two rounds and decodes round 0 while round 1 is in flight (1024
+// threads, one round per wave, needs 93 KB of LDS, so the next kernel's
+// workgroups cannot start on a CU beside it, and a chain of layers runs
+// slower).  The staging regions (one per wave, reused by its rounds) are in
+// dynamic LDS after the plan: 67 KB per workgroup with the tables.
 // grid = (ceil(d_ff / R), n_slots, n_tokens)
 // ---------------------------------------------------------------------------
 // units of a round per wave
-template <int NT>
+template <int PER>
 struct RoundUnits {
-    static constexpr int PER = NT / kThreads;              // lanes per unit
     static constexpr int V = 64 / PER;
 };
 // 16-byte chunks of one wave's round at any lead, and the loads per lane that cover them
-template <int QT, int NT>
+template <int QT, int PER>
 struct WaveRoundChunks {
-    static constexpr int V = (RoundUnits<NT>::V * UnitFmt<QT>::BYTES + 30) / 16;
+    static constexpr int V = (RoundUnits<PER>::V * UnitFmt<QT>::BYTES + 30) / 16;
     static constexpr int LOADS = (V + 63) / 64;
+};
+template <int QT, int NT, int PER>
+struct GateUpRounds {
+    static constexpr int NW = NT / 64;                      // waves
+    static constexpr int WPM = NW / 2;                      // waves per matrix
+    static constexpr int UPW = RoundUnits<PER>::V;          // units per wave and round
+    static constexpr int RD = 256 / (WPM * UPW);            // rounds per wave
+    static constexpr int WCH = WaveRoundChunks<QT, PER>::V;
+    static constexpr int STAGE = NW * 16 * WCH;             // staging bytes
+    static_assert(RD >= 1 && RD * WPM * UPW == 256, "a workgroup's 256 units per matrix split evenly");
 };
 __host__ __device__ inline bool gate_up_rounds_ok(int qt, int d_model) {
     const int nus = units_per_row(qt, d_model);
@@ -565,19 +579,21 @@ __host__ __device__ inline bool gate_up_rounds_ok(int qt, int d_model) {
 }
 __host__ __device__ inline int rows_gate_up_rounds(int qt, int d_model) { return 256 / units_per_row(qt, d_model); }
 constexpr int kGateUpRoundThreads = 2 * kThreads;
+// dynamic LDS of a launch: the plan, then the staging regions
+__host__ __device__ inline int gate_up_rounds_lds(const Plan& P, int stage) { return align16i(P.bytes) + stage; }
 
-template <int QT, int NT>
+template <int QT, int NT, int PER = 2>
 __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
+    using GR = GateUpRounds<QT, NT, PER>;
     constexpr int UB = UnitFmt<QT>::BYTES;
-    constexpr int PER = RoundUnits<NT>::PER, UPW = RoundUnits<NT>::V;
-    constexpr int WPT = 128 / UPW;                          // waves per tile and round
-    constexpr int WCH = WaveRoundChunks<QT, NT>::V, N = WaveRoundChunks<QT, NT>::LOADS;
-    static_assert((NT / 64) * 16 * WCH <= kStageBytes, "the waves' rounds must fit the stage");
+    constexpr int UPW = GR::UPW, WPM = GR::WPM, RD = GR::RD;
+    constexpr int WCH = GR::WCH, N = WaveRoundChunks<QT, PER>::LOADS;
     static_assert(PER == 1 || QT == QT_IQ3_S, "split units are IQ3_S only");
-    SABAH_STATIC_LDS(QT)
+    __shared__ __align__(16) uint8_t tabs[QT == QT_IQ3_S ? kLdsTables : 16];
     extern __shared__ __align__(16) uint8_t smem[];
     const int NUS = units_per_row(QT, a.d_model), NCB = contribs_per_row(QT, a.d_model);
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * NCB);
+    uint8_t* const stage = smem + align16i(P.bytes);
     const int t = blockIdx.z, s = blockIdx.y, row0 = blockIdx.x * a.R;
     const int nrows = min(a.R, a.d_ff - row0);
     const size_t rb = row_bytes(QT, a.d_model);
@@ -597,15 +613,15 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
         return;
     }
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63u);
-    const int m = wave / WPT;
+    const int m = wave / WPM;
     const uint8_t* tile = (m ? wu : wg) + (size_t)row0 * rb;
     const int nvalid = nrows * NUS;                         // the tile's units in this workgroup
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
-    u32x4 d[2][N];
-    int q[2][N], lead[2], v0[2];
+    u32x4 d[RD][N];
+    int q[RD][N], lead[RD], v0[RD];
 #pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-        v0[rd] = 128 * rd + UPW * (wave % WPT);
+    for (int rd = 0; rd < RD; ++rd) {
+        v0[rd] = WPM * UPW * rd + UPW * (wave % WPM);
         const int nu = min(UPW, nvalid - v0[rd]);
         const uint8_t* p = tile + (nu > 0 ? (size_t)v0[rd] * UB : 0);
         lead[rd] = (int)(reinterpret_cast<uintptr_t>(p) & 15);
@@ -624,7 +640,7 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
     const float rcp_nus = __builtin_amdgcn_rcpf((float)NUS);
     const int j = lane / PER, half = lane & (PER - 1);      // the lane's unit in the round and its half
 #pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
+    for (int rd = 0; rd < RD; ++rd) {
         // the wave's own chunks: LDS operations of one wave complete in order,
         // so its reads below see these writes, and round 1's writes come after
         // round 0's reads

@@ -225,8 +225,9 @@ hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
     if constexpr (QT == QT_IQ3_S) {
         if (gate_up_rounds_ok(QT, a.d_model) && a.R == rows_gate_up_rounds(QT, a.d_model)) {
             constexpr int NT = kGateUpRoundThreads;
-            if (const hipError_t e = fit_lds(k_gate_up_rounds<QT, NT>, P.bytes, launch_lds(QT, P))) return e;
-            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT, NT>, grid, P.bytes, st, a, NT);
+            const int dyn = gate_up_rounds_lds(P, GateUpRounds<QT, NT, 2>::STAGE);
+            if (const hipError_t e = fit_lds(k_gate_up_rounds<QT, NT>, dyn, kLdsTables + dyn)) return e;
+            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT, NT>, grid, dyn, st, a, NT);
             return hipGetLastError();
         }
     }

@@ -154,20 +154,22 @@ __host__ __device__ constexpr uint32_t sign_sel(uint32_t n) { return ((n * 0x008
 // from codebook registers loaded early.
 template <int NT>
 struct GridRegs {
-    uint32_t e[512 / NT];
+    static constexpr int N = NT >= 512 ? 1 : 512 / NT;   // entries per thread (threads 512.. hold none)
+    uint32_t e[N];
 };
 template <int NT>
 __device__ inline GridRegs<NT> load_grid_regs(int w) {
     GridRegs<NT> g;
 #pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) g.e[i] = kIq3sGridDev.e[w + NT * i];
+    for (int i = 0; i < GridRegs<NT>::N; ++i) g.e[i] = kIq3sGridDev.e[min(w + NT * i, 511)];
     return g;
 }
 template <int NT>
 __device__ inline void store_iq3s_tables(uint8_t* smem, const GridRegs<NT>& g, int w) {
     uint32_t* tab = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
+    if (NT > 512 && w >= 512) return;
 #pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) {
+    for (int i = 0; i < GridRegs<NT>::N; ++i) {
         const int idx = w + NT * i;                       // codebook index qs + 256 * b
         uint32_t* row = tab + (idx & 255) + 4096 * (idx >> 8);
         const uint32_t neg = g.e[i] ^ 0xFEFEFEFEu;
