@@ -344,21 +344,21 @@ __device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs
         const int t = div_small(u, rcp_nv);
         const int v = S.v0 + (u - t * S.nv);             // tile-relative unit (row-major over the rows)
         const int r = div_small(v, S.T.rcp_nus), us = v - r * S.T.NUS;
-        LdsWindow<QT> Wn;
-        Wn.load(stage + 16 * S.cpt * t + leads[t] + (int)((size_t)r * S.T.rb) + us * TileWalk<QT>::UB - S.b0);
+        const uint8_t* unit = stage + 16 * S.cpt * t + leads[t] + (int)((size_t)r * S.T.rb) + us * TileWalk<QT>::UB - S.b0;
         float* prow = part + (t * part_rows + r) * S.T.NCB;
         if constexpr (SPLIT) {
             const uint8_t* act = act0 + t * act_stride;
             const ActLayout AL(k, QT_Q8_K);
-            uint32_t F[UnitFmt<QT>::NF];
-            uint32_t Fm1;
-            Wn.fields(F, Fm1);
-            int bs = iq3s_half_bsum(F, tabs, act + us * kActChunkStride, half);
+            uint32_t G[UnitFmt<QT>::NF], A[4][8], dbits;
+            iq3s_half_fields(unit, half, G, dbits);
+            act_half(act + us * kActChunkStride, half, A);
+            int bs = iq3s_half_bsum(G, tabs, A);
             bs += (int)dpp<kDppXor1>((uint32_t)bs);       // the partner lane's half
             if (half == 0)
-                prow[us] = __fmul_rn(__fmul_rn(h2f(Fm1 >> 16), reinterpret_cast<const float*>(act + AL.off_d)[us]),
-                                     (float)bs);
+                prow[us] = __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(act + AL.off_d)[us]), (float)bs);
         } else {
+            LdsWindow<QT> Wn;
+            Wn.load(unit);
             unit_into_part<QT>(Wn, tabs, act0 + t * act_stride, k, us, prow);
         }
     }
@@ -639,6 +639,13 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
     uint8_t* region = stage + 16 * WCH * wave;
     const float rcp_nus = __builtin_amdgcn_rcpf((float)NUS);
     const int j = lane / PER, half = lane & (PER - 1);      // the lane's unit in the round and its half
+    // a lane's unit column is the same in every round (a wave's rounds are
+    // 128 units apart and NUS divides 128), so its activation half is read once
+    uint32_t A[4][8];
+    if constexpr (PER == 2) {
+        const int vj = v0[0] + j;
+        act_half(act + (vj - div_small(vj, rcp_nus) * NUS) * kActChunkStride, half, A);
+    }
 #pragma unroll
     for (int rd = 0; rd < RD; ++rd) {
         // the wave's own chunks: LDS operations of one wave complete in order,
@@ -649,20 +656,20 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
         if (j < nvalid - v0[rd]) {                          // both lanes of a pair alike
             const int v = v0[rd] + j;
             const int r = div_small(v, rcp_nus), us = v - r * NUS;
-            LdsWindow<QT> Wn;
-            Wn.load(region + lead[rd] + j * UB);
+            const uint8_t* unit = region + lead[rd] + j * UB;
             float* prow = part + (m * a.R + r) * NCB;
             if constexpr (PER == 2) {
                 const ActLayout AL(a.d_model, QT_Q8_K);
-                uint32_t F[UnitFmt<QT>::NF];
-                uint32_t Fm1;
-                Wn.fields(F, Fm1);
-                int bs = iq3s_half_bsum(F, tabs, act + us * kActChunkStride, half);
+                uint32_t G[UnitFmt<QT>::NF], dbits;
+                iq3s_half_fields(unit, half, G, dbits);
+                int bs = iq3s_half_bsum(G, tabs, A);
                 bs += (int)dpp<kDppXor1>((uint32_t)bs);
                 if (half == 0)
-                    prow[us] = __fmul_rn(__fmul_rn(h2f(Fm1 >> 16), reinterpret_cast<const float*>(act + AL.off_d)[us]),
+                    prow[us] = __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(act + AL.off_d)[us]),
                                          (float)bs);
             } else {
+                LdsWindow<QT> Wn;
+                Wn.load(unit);
                 unit_into_part<QT>(Wn, tabs, act, a.d_model, us, prow);
             }
         }

@@ -225,28 +225,53 @@ __device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* 
     return 2 * (int)((F[26] >> (4 * ib)) & 15u) + 1;
 }
 
-// The exact integer sum over items 4h .. 4h + 3 (h = 0 or 1, per lane) of an
-// IQ3_S unit: sum ls(ib) * (weights . activations).  The half's fields are
-// moved to items 0..3's places with selects, so every register index stays
-// static.  chunk is the unit's 256-element activation chunk.
-__device__ inline int iq3s_half_bsum(const uint32_t (&F)[27], const uint8_t* smem, const uint8_t* chunk, int h) {
-    uint32_t G[27];
+// Half h (items 4h .. 4h + 3, h = 0 or 1 per lane) of an IQ3_S unit staged in
+// LDS at byte address unit_lds, read straight into the places iq3s_item
+// reads for items 0..3: G[0..7] the half's 32 qs bytes, G[16] its qh bytes,
+// G[18..21] its sign bytes, G[26] (low 16 bits) its scale nibbles.  The
+// unit's fp16 d is returned in the low 16 bits of dbits.  A unit starts at an
+// even byte, so every field is one byte shift (0 or 2) away from the dword
+// grid: 20 dword reads instead of the unit's 29.  Bytes outside the unit
+// (the two before it) are read but never used.
+__device__ inline void iq3s_half_fields(const uint8_t* unit_lds, int h, uint32_t (&G)[27], uint32_t& dbits) {
+    const uint8_t* o = unit_lds + 2;                                 // qs; qh at +64, signs +72, scales +104
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(o) & 3);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(o - sh);
+    const uint32_t* qq = q + 8 * h;                                   // the half's qs
+    uint32_t W[9];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) G[i] = h ? F[8 + i] : F[i];          // qs of items 4h ..
-    G[16] = h ? F[17] : F[16];                                      // their qh bytes
+    for (int i = 0; i < 9; ++i) W[i] = qq[i];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) G[18 + i] = h ? F[22 + i] : F[18 + i];   // their sign bytes
-    G[26] = h ? F[26] >> 16 : F[26];                                // their scale nibbles
-    const uint8_t* ch = chunk + 128 * h;
+    for (int i = 0; i < 8; ++i) G[i] = __builtin_amdgcn_alignbyte(W[i + 1], W[i], sh);
+    const uint32_t* qh = q + 16 + h;
+    G[16] = __builtin_amdgcn_alignbyte(qh[1], qh[0], sh);
+    const uint32_t* sg = q + 18 + 4 * h;
+    uint32_t S[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) S[i] = sg[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) G[18 + i] = __builtin_amdgcn_alignbyte(S[i + 1], S[i], sh);
+    G[26] = __builtin_amdgcn_alignbyte(q[27], q[26], sh) >> (16 * h);
+    dbits = __builtin_amdgcn_alignbyte(q[0], q[-1], sh) >> 16;
+}
+
+// the 128 activation bytes of half h of a 256-element chunk, per item
+__device__ inline void act_half(const uint8_t* chunk, int h, uint32_t (&A)[4][8]) {
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) act8(chunk + 128 * h, ib, A[ib]);
+}
+
+// The exact integer sum over the four items of a half (iq3s_half_fields):
+// sum ls(ib) * (weights . activations).
+__device__ inline int iq3s_half_bsum(const uint32_t (&G)[27], const uint8_t* smem, const uint32_t (&A)[4][8]) {
     int bsum = 0;
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
-        uint32_t v[8], A[8];
+        uint32_t v[8];
         const int ls = iq3s_item(G, ib, smem, v);
-        act8(ch, ib, A);
         int s = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
+        for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[ib][i], s);
         bsum += __mul24(ls, s);
     }
     return bsum;
