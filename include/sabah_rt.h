@@ -144,10 +144,11 @@ int sabah_moe_block(const float *d_x, float *d_out, float *d_h, const void *cons
                     int qt_gate, int qt_up, int qt_down, int accumulate);
 
 /* A MoE layer over n_tokens tokens with ids read on the device from the bank
- * bases (no pointer table), plus an optional dense shared expert and an
- * optional residual.  Generalises sabah_moe_block (sabah_rt.cu:3362-3378) to
- * the ggml graph's batched form (qwen4exp.cpp:848-892):
- *   out[t] = [resid[t] +] sum_k w[t][k] * y[t][k] [+ shared(x[t])]
+ * bases (no pointer table), plus an optional dense shared expert (optionally
+ * sigmoid-gated) and an optional residual.  Generalises sabah_moe_block
+ * (sabah_rt.cu:3362-3378) to the ggml graph's batched form (qwen4exp.cpp:848-892):
+ *   out[t] = [resid[t] +] sum_k w[t][k] * y[t][k] [+ g[t] * shared(x[t])]
+ * with g[t] = sigmoid(shared_gate_inp . x[t]), or 1 without a gate row.
  * Bank bases are device memory in GGUF layout [n_experts][rows][row_bytes]. */
 typedef struct sabah_moe_layer_desc {
     const void *gate, *up, *down;
@@ -156,6 +157,10 @@ typedef struct sabah_moe_layer_desc {
     const void *shared_gate, *shared_up, *shared_down;   /* NULL: no shared expert */
     int qt_shared_gate, qt_shared_up, qt_shared_down;
     int d_ff_shared;
+    /* Optional f32 [d_model] row (ffn_gate_inp_shexp): the shared expert's
+     * output for token t is multiplied by sigmoid(shared_gate_inp . x[t])
+     * before it is added (qwen4exp.cpp:877-885).  NULL adds it unscaled. */
+    const float *shared_gate_inp;
 } sabah_moe_layer_desc;
 
 int sabah_moe_layer(const sabah_moe_layer_desc *layer, const float *d_x, const int32_t *d_ids,

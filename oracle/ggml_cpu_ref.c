@@ -637,6 +637,13 @@ int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *id
             dense_matvec((const uint8_t *)L->shared_up, L->qt_shared_up, Fs, D, xt, us, nt);
             for (int j = 0; j < Fs; ++j) gs[j] = silu_f32(gs[j]) * us[j];
             dense_matvec((const uint8_t *)L->shared_down, L->qt_shared_down, D, Fs, gs, ys, nt);
+            if (L->shared_gate_inp) {
+                double dot = 0.0;
+                for (int i = 0; i < D; ++i) dot += (double)L->shared_gate_inp[i] * (double)xt[i];
+                const float gl = (float)dot;
+                const float g = 1.0f / (1.0f + expf(-gl));       /* ggml_vec_sigmoid_f32 */
+                for (int i = 0; i < D; ++i) ys[i] = ys[i] * g;
+            }
             for (int i = 0; i < D; ++i) ot[i] = ot[i] + ys[i];
             free(gs); free(us); free(ys);
         }

@@ -102,7 +102,10 @@ int orc_mul_mat_id(const void *source, size_t expert_stride, size_t row_stride,
  *   g = MUL_MAT_ID(gate), u = MUL_MAT_ID(up), h = silu(g) * u,
  *   y = MUL_MAT_ID(down, h), out = sum_k (y_k * w_k)   (serial over k)
  * plus, when shared_gate != NULL, a dense shared expert added last:
- *   out += down_s(silu(gate_s x) * up_s x).
+ *   out += g * down_s(silu(gate_s x) * up_s x)
+ * with g = sigmoid(shared_gate_inp . x) when shared_gate_inp != NULL
+ * (qwen4exp.cpp:877-885: ggml_mul_mat, ggml_sigmoid, ggml_mul, ggml_add),
+ * else 1 (no multiply).  The gate's dot product is summed in double. 
  * Expert tensors are [n_experts][rows][row_bytes] (GGUF layout).
  * x [n_tokens][d_model], ids/w [n_tokens][n_used], out [n_tokens][d_model]. */
 typedef struct {
@@ -112,6 +115,7 @@ typedef struct {
     const void *shared_gate, *shared_up, *shared_down;   /* optional */
     int qt_shared_gate, qt_shared_up, qt_shared_down;
     int d_ff_shared;
+    const float *shared_gate_inp;                         /* optional [d_model] */
 } orc_moe_layer_desc;
 
 int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *ids,

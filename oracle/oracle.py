@@ -60,7 +60,8 @@ class MoeLayerDesc(ctypes.Structure):
                 ("shared_gate", ctypes.c_void_p), ("shared_up", ctypes.c_void_p),
                 ("shared_down", ctypes.c_void_p),
                 ("qt_shared_gate", ctypes.c_int), ("qt_shared_up", ctypes.c_int),
-                ("qt_shared_down", ctypes.c_int), ("d_ff_shared", ctypes.c_int)]
+                ("qt_shared_down", ctypes.c_int), ("d_ff_shared", ctypes.c_int),
+                ("shared_gate_inp", ctypes.c_void_p)]
 
 
 def _p(a: np.ndarray):
@@ -166,7 +167,8 @@ def moe_layer(gate, up, down, qts, x, ids, w, shared=None, n_threads: int = 0,
     """Gated expert FFN + combine for T tokens.
 
     gate/up: [E, d_ff, rb] u8, down: [E, d_model, rb] u8, qts = (qt_gate, qt_up, qt_down),
-    x [T, d_model] f32, ids/w [T, n_used]; shared = (gate_s, up_s, down_s, qts_s) or None.
+    x [T, d_model] f32, ids/w [T, n_used]; shared = (gate_s, up_s, down_s, qts_s) or
+    (gate_s, up_s, down_s, qts_s, gate_inp) with gate_inp the [d_model] f32 gate row, or None.
     """
     gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
     x = np.ascontiguousarray(x, np.float32)
@@ -181,12 +183,18 @@ def moe_layer(gate, up, down, qts, x, ids, w, shared=None, n_threads: int = 0,
     desc.d_model, desc.d_ff, desc.n_experts = D, F, gate.shape[0]
     keep = []
     if shared is not None:
-        sg, su, sd, sq = shared
+        sg, su, sd, sq = shared[:4]
         sg, su, sd = (np.ascontiguousarray(a, np.uint8) for a in (sg, su, sd))
         keep = [sg, su, sd]
         desc.shared_gate, desc.shared_up, desc.shared_down = sg.ctypes.data, su.ctypes.data, sd.ctypes.data
         desc.qt_shared_gate, desc.qt_shared_up, desc.qt_shared_down = sq
         desc.d_ff_shared = sg.shape[0]
+        if len(shared) > 4 and shared[4] is not None:
+            gi = np.ascontiguousarray(shared[4], np.float32).reshape(-1)
+            if gi.size != D:
+                raise ValueError("shared gate row has %d values, d_model is %d" % (gi.size, D))
+            keep.append(gi)
+            desc.shared_gate_inp = gi.ctypes.data
     out = np.zeros((T, D), np.float32)
     h = np.zeros((T, n_used, F), np.float32)
     rc = lib().orc_moe_layer(ctypes.byref(desc), _p(x), _p(ids), _p(w), n_used, T, _p(out), _p(h),

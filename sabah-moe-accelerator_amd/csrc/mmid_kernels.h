@@ -419,6 +419,28 @@ constexpr int kRoundsH = 2;   // slot rows: 32 chunk-rows (n_slots * ceil(d_ff /
 // grid = (ceil(rows / R), n_ids, n_tokens).  Rows packed at row_stride form
 // one tile; rows row_stride > row bytes apart are one tile each (R <= kMaxTiles).
 // ---------------------------------------------------------------------------
+// ggml_vec_sigmoid_f32: 1 / (1 + exp(-v))
+__device__ inline float sigmoid_f32(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-v))); }
+
+// Shared-expert gate logit w . x (qwen4exp.cpp:877-885, ffn_gate_inp_shexp
+// times the layer input) in one fixed order:
+// 256 strided partial sums (lane v sums elements v, v + 256, ... in turn),
+// each wave of them summed by a butterfly (every lane ends with the same
+// value), then the four wave sums in order.  The 256 threads of a workgroup
+// call gate_dot_part, which stores each wave's sum in sums[wave]; after a
+// barrier gate_dot_total gives every thread the logit.
+__device__ inline void gate_dot_part(const float* w, const float* x, int n, float* sums) {
+    const int v = (int)threadIdx.x;
+    float p = 0.0f;
+    for (int i = v; i < n; i += 256) p = __fadd_rn(p, __fmul_rn(w[i], x[i]));
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) p = __fadd_rn(p, __shfl_xor(p, m));
+    if ((v & 63) == 0) sums[v >> 6] = p;
+}
+__device__ inline float gate_dot_total(const float* sums) {
+    return __fadd_rn(__fadd_rn(__fadd_rn(sums[0], sums[1]), sums[2]), sums[3]);
+}
+
 struct MmidArgs {
     ExpertSrc W;
     Routing rt;
@@ -431,6 +453,9 @@ struct MmidArgs {
     size_t dst_id_stride, dst_token_stride;
     int rows, k, R;
     unsigned int* err;            // sticky error word, host-mapped; every writer stores 1
+    const float* sg_w;            // optional [sg_n] gate row: every output row of token t is scaled by
+    const float* sg_x;            //   sigmoid(sg_w . sg_x[t]) (the shared expert's gate); sg_x [n_tokens][sg_n]
+    int sg_n;
 };
 
 // The kernels' static LDS: IQ3_S tables (when QT is IQ3_S), the staged
@@ -476,8 +501,16 @@ __global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
     tiles_begin(S, tile_ptr);
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsX>(xb, xa);
+    // the gate's loads come after the weights', so it waits for what the
+    // staging waits for anyway; the staging's barrier publishes the sums
+    __shared__ float sg_sums[4];
+    if (a.sg_w) gate_dot_part(a.sg_w, a.sg_x + (size_t)t * a.sg_n, a.sg_n, sg_sums);
     tiles_finish(S, tabs, stage, leads, a.k, act, 0, packed ? a.R : 1, part);
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) out[r] = row_sum(part + r * NCB, NCB);
+    const float sg = a.sg_w ? sigmoid_f32(gate_dot_total(sg_sums)) : 1.0f;
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        const float y = row_sum(part + r * NCB, NCB);
+        out[r] = a.sg_w ? __fmul_rn(y, sg) : y;
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -656,6 +656,9 @@ static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_
     a.k = Fs;
     a.R = rows_mmid(L->qt_shared_down, Fs, true);
     a.err = g_err_dev;
+    a.sg_w = L->shared_gate_inp;                 // ggml_mul(ffn_shexp, sigmoid(gate_inp_shexp . x))
+    a.sg_x = d_x;
+    a.sg_n = D;
     if (!ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch")) return -1;
     *ys_out = ys;
     return 0;
@@ -693,6 +696,8 @@ static int check_layer_desc(const sabah_moe_layer_desc* L) {
         if (!L->shared_up || !L->shared_down || L->d_ff_shared <= 0 ||
             !layer_types_ok(L->qt_shared_gate, L->qt_shared_up, L->qt_shared_down, L->d_model, L->d_ff_shared))
             return fail("MoE layer: invalid shared expert");
+    } else if (L->shared_gate_inp) {
+        return fail("MoE layer: shared_gate_inp given without a shared expert");
     }
     return 0;
 }

@@ -122,11 +122,15 @@ class ExpertBank:
             d.shared_gate, d.shared_up, d.shared_down = shared.ptrs()
             d.qt_shared_gate = d.qt_shared_up = d.qt_shared_down = shared.qt
             d.d_ff_shared = shared.d_ff
+            if shared.gate_inp is not None:
+                d.shared_gate_inp = shared.gate_inp.data_ptr()
         return d
 
 
 class DenseExpert:
-    """An always-on shared expert: three dense matrices of one quant type."""
+    """An always-on shared expert: three dense matrices of one quant type, and
+    optionally its f32 gate row (ffn_gate_inp_shexp, qwen4exp.cpp:877-885): the
+    expert's output is then scaled by sigmoid(gate_inp . x) before it is added."""
 
     def __init__(self, d_model: int, d_ff: int, qt: int, device: str = "cuda:0"):
         self.d_model, self.d_ff, self.qt = d_model, d_ff, qt
@@ -134,6 +138,17 @@ class DenseExpert:
         self.cols = {"gate": d_model, "up": d_model, "down": d_ff}
         self.mats = {r: torch.empty(self.rows[r], rt.row_bytes(qt, self.cols[r]), dtype=torch.uint8,
                                     device=device) for r in ROLES}
+        self.gate_inp = None
+
+    def set_gate(self, row: np.ndarray | None) -> None:
+        """The shared expert's gate row ([d_model] f32), or None for an ungated add."""
+        if row is None:
+            self.gate_inp = None
+            return
+        row = np.ascontiguousarray(row, np.float32).reshape(-1)
+        if row.size != self.d_model:
+            raise ValueError("gate row has %d values, d_model is %d" % (row.size, self.d_model))
+        self.gate_inp = torch.from_numpy(row).to(self.mats["gate"].device)
 
     def ptrs(self):
         return tuple(self.mats[r].data_ptr() for r in ROLES)

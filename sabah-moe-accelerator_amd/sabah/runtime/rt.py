@@ -55,7 +55,7 @@ class MoeLayerDesc(ctypes.Structure):
                 ("d_model", c_i), ("d_ff", c_i), ("n_experts", c_i),
                 ("shared_gate", c_vp), ("shared_up", c_vp), ("shared_down", c_vp),
                 ("qt_shared_gate", c_i), ("qt_shared_up", c_i), ("qt_shared_down", c_i),
-                ("d_ff_shared", c_i)]
+                ("d_ff_shared", c_i), ("shared_gate_inp", c_vp)]
 
 
 # every symbol include/sabah_rt.h declares, with its ctypes signature

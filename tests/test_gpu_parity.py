@@ -286,6 +286,41 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     assert_parity(out.cpu().numpy(), want, name)
 
 
+def test_moe_layer_with_a_sigmoid_gated_shared_expert(hip_rt, orc):
+    """The shared expert's output times sigmoid(gate_inp . x) (qwen4exp.cpp:877-885),
+    applied in the shared down launch.  A random gate row: within tolerance of the
+    oracle; rows giving g = 1 and g = 0 exactly: bit-identical to the ungated layer
+    and to the layer without the shared expert."""
+    from sabah.runtime import routing
+    from sabah.runtime.bank import DenseExpert
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(71)
+    E, D, F, K, Tn, Fs, qts = 48, 2048, 768, 8, 5, 512, (Q4_K, Q4_K, Q6_K)
+    bank, raws = make_bank(orc, rng, qts, E, D, F)
+    shared = DenseExpert(D, Fs, Q8_0, device="cuda:0")
+    sh_raw = {}
+    for role, (rows, cols) in {"gate": (Fs, D), "up": (Fs, D), "down": (D, Fs)}.items():
+        sh_raw[role] = orc.quantize_weights(Q8_0, (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+        shared.load(role, sh_raw[role])
+    ids, w = routing.uniform_routing(rng, Tn, E, K)
+    x = rng.standard_normal((Tn, D)).astype(np.float32)
+    row = (rng.standard_normal(D) * 0.03).astype(np.float32)
+    shared.set_gate(row)
+    ex = MoEExecutor(bank, max_used=K, shared=shared)
+    got = ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()
+    want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], qts, x, ids, w,
+                         shared=(sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3, row))
+    assert_parity(got, want, "gated shared expert")
+    shared.set_gate(None)
+    ungated = ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()
+    routed = MoEExecutor(bank, max_used=K).run_layer(0, T(x), T(ids), T(w)).cpu().numpy()
+    for t in range(Tn):
+        shared.set_gate(1e4 * x[t])
+        assert np.array_equal(ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()[t], ungated[t])
+        shared.set_gate(-1e4 * x[t])
+        assert np.array_equal(ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()[t], routed[t])
+
+
 @pytest.mark.parametrize("D,F", [(512, 544), (1024, 800)])
 def test_iq3s_gate_up_with_a_partial_last_row_tile(hip_rt, orc, D, F):
     """IQ3_S gate/up runs in two rounds of 256 units per workgroup (R = 256 /

@@ -65,7 +65,8 @@ def test_prefill_layer_is_the_token_major_layer(hip_rt, orc, case, E, D, F, Tn, 
     assert_parity(got.cpu().numpy(), want, "prefill %s" % case)
 
 
-def test_prefill_layer_with_shared_expert_and_residual(hip_rt, orc):
+@pytest.mark.parametrize("gated", [False, True])
+def test_prefill_layer_with_shared_expert_and_residual(hip_rt, orc, gated):
     from sabah.runtime import routing
     from sabah.runtime.bank import DenseExpert
     from sabah.runtime.executor import MoEExecutor
@@ -79,6 +80,8 @@ def test_prefill_layer_with_shared_expert_and_residual(hip_rt, orc):
         shared.load(role, sh_raw[role])
     ids, w = routing.zipf_routing(rng, Tn, E, K)
     x = rng.standard_normal((Tn, D)).astype(np.float32)
+    row = (rng.standard_normal(D) * 0.03).astype(np.float32) if gated else None
+    shared.set_gate(row)
     ex = MoEExecutor(bank, max_used=K, shared=shared)
     xd = T(x)
     got = ex.run_prefill_layer(0, xd, T(ids), T(w), resid=xd)
@@ -86,8 +89,8 @@ def test_prefill_layer_with_shared_expert_and_residual(hip_rt, orc):
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
     y = orc.moe_layer(raws["gate"], raws["up"], raws["down"], (IQ3_S,) * 3, x, ids, w,
-                      shared=(sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3))
-    assert_parity(got.cpu().numpy(), x + y, "prefill + shared + residual")
+                      shared=(sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3, row))
+    assert_parity(got.cpu().numpy(), x + y, "prefill + shared%s + residual" % (" (gated)" if gated else ""))
 
 
 def test_prefill_layer_in_place_on_the_residual_stream(hip_rt, orc):

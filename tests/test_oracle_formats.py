@@ -328,6 +328,45 @@ def test_moe_layer_shared_expert_is_added_last(orc):
     assert np.array_equal(both, routed + shared_only)
 
 
+def test_moe_layer_gated_shared_expert_closed_forms(orc):
+    """qwen4exp.cpp:877-885: the shared expert's output is multiplied by
+    sigmoid(gate_inp . x) and then added.  Rows that make the logit 0, +big and
+    -big give g = 0.5, 1 and 0 exactly, so the gated layer is pinned bit for bit
+    against the routed part and the ungated shared output; a random row is
+    checked against a float64 sigmoid."""
+    rng = np.random.default_rng(23)
+    D, F, Fs, E, T = 256, 256, 256, 4, 3
+    g, u = _bank(orc, rng, Q4_K, E, F, D), _bank(orc, rng, Q4_K, E, F, D)
+    dn = _bank(orc, rng, Q6_K, E, D, F)
+    sg, su = _bank(orc, rng, Q8_0, 1, Fs, D)[0], _bank(orc, rng, Q8_0, 1, Fs, D)[0]
+    sd = _bank(orc, rng, Q8_0, 1, D, Fs)[0]
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ids = np.array([[2, 0], [1, 3], [3, 3]], np.int32)
+    w = np.array([[0.7, 0.3], [0.5, 0.5], [0.9, 0.1]], np.float32)
+    qts, sq = (Q4_K, Q4_K, Q6_K), (Q8_0, Q8_0, Q8_0)
+    routed = orc.moe_layer(g, u, dn, qts, x, ids, w)
+    ys = np.stack([orc.moe_layer(sg[None], su[None], sd[None], sq, x[t:t + 1], np.array([[0]], np.int32),
+                                 np.array([[1.0]], np.float32))[0] for t in range(T)])
+    ungated = orc.moe_layer(g, u, dn, qts, x, ids, w, shared=(sg, su, sd, sq))
+    assert np.array_equal(ungated, routed + ys)
+
+    def gated(row):
+        return orc.moe_layer(g, u, dn, qts, x, ids, w, shared=(sg, su, sd, sq, row))
+    assert np.array_equal(gated(np.zeros(D, np.float32)), routed + ys * np.float32(0.5))
+    for t in range(T):       # a row along x[t] makes that token's logit +-|x|^2 * 1e4
+        up = gated(1e4 * x[t])[t]
+        assert np.array_equal(up, ungated[t])
+        down = gated(-1e4 * x[t])[t]
+        assert np.array_equal(down, routed[t])
+    row = (rng.standard_normal(D) * 0.05).astype(np.float32)
+    logit = x.astype(np.float64) @ row.astype(np.float64)
+    gate = 1.0 / (1.0 + np.exp(-logit))
+    want = routed.astype(np.float64) + ys.astype(np.float64) * gate[:, None]
+    assert max_rel(gated(row), want) < 1e-6
+    with pytest.raises(ValueError):
+        gated(np.zeros(D + 1, np.float32))
+
+
 def test_encoders_round_trip(orc):
     rng = np.random.default_rng(4)
     for qt, k, tol in [(Q8_0, 512, 0.01), (Q4_K, 512, 0.12), (Q6_K, 512, 0.03), (IQ3_S, 512, 0.25)]:
