@@ -190,6 +190,20 @@ int sabah_moe_prefill_layer(const sabah_moe_layer_desc *layer, const float *d_x,
                             const float *d_w, int n_used, int n_tokens, float *d_out, const float *d_resid,
                             void *stream);
 
+/* Router gating for n_tokens rows of n_experts router logits (device f32),
+ * as ggml's graph runs it before MUL_MAT_ID (qwen4exp.cpp:848-862 ->
+ * build_moe_ffn with softmax gating; upstream's fused topk-moe,
+ * ggml-cuda.cu:3390-3405):
+ *   p = softmax(logits[t])                       (ggml_soft_max; exp sums in double)
+ *   d_ids[t] = the n_used largest p, descending  (ggml_argsort_top_k; ties: lower index first)
+ *   d_w[t] = p[d_ids[t]], divided by their sum when norm_w (ggml_sum_rows, ggml_div),
+ *            times w_scale when w_scale != 1 (ggml_scale)
+ * so the fused layer's ids and weights never leave the device.  No reference
+ * counterpart: the reference's runtime receives ids from ggml.  n_experts <=
+ * 4096, n_used <= min(n_experts, 64), w_scale > 0; enqueued on `stream`. */
+int sabah_moe_route(const float *d_logits, int n_tokens, int n_experts, int n_used, int norm_w,
+                    float w_scale, int32_t *d_ids, float *d_w, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

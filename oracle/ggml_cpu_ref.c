@@ -651,3 +651,44 @@ int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *id
     free(g); free(u); free(h); free(y);
     return 0;
 }
+
+int orc_moe_route(const float *logits, int n_tokens, int n_experts, int n_used, int norm_w, float w_scale,
+                  int32_t *ids, float *w) {
+    if (n_experts <= 0 || n_used <= 0 || n_used > n_experts || n_tokens < 0) return -1;
+    float *p = (float *)malloc(sizeof(float) * (size_t)n_experts);
+    char *taken = (char *)malloc((size_t)n_experts);
+    for (int t = 0; t < n_tokens; ++t) {
+        const float *l = logits + (size_t)t * n_experts;
+        float m = -INFINITY;
+        for (int i = 0; i < n_experts; ++i) m = l[i] > m ? l[i] : m;           /* ggml_vec_max_f32 */
+        double sum = 0.0;
+        for (int i = 0; i < n_experts; ++i) {                                  /* ggml_vec_soft_max_f32 */
+            p[i] = expf(l[i] - m);
+            sum += (double)p[i];
+        }
+        const float inv = (float)(1.0 / sum);                                  /* ggml_vec_scale_f32 */
+        for (int i = 0; i < n_experts; ++i) p[i] = p[i] * inv;
+        memset(taken, 0, (size_t)n_experts);
+        int32_t *it = ids + (size_t)t * n_used;
+        float *wt = w + (size_t)t * n_used;
+        for (int k = 0; k < n_used; ++k) {
+            int best = -1;
+            for (int i = 0; i < n_experts; ++i)
+                if (!taken[i] && (best < 0 || p[i] > p[best])) best = i;
+            taken[best] = 1;
+            it[k] = best;
+            wt[k] = p[best];
+        }
+        if (norm_w) {
+            double d = 0.0;
+            for (int k = 0; k < n_used; ++k) d += (double)wt[k];                /* ggml_vec_sum_f32 */
+            const float s = (float)d;
+            for (int k = 0; k < n_used; ++k) wt[k] = wt[k] / s;
+        }
+        if (w_scale != 1.0f)
+            for (int k = 0; k < n_used; ++k) wt[k] = wt[k] * w_scale;
+    }
+    free(p);
+    free(taken);
+    return 0;
+}

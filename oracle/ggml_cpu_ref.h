@@ -122,6 +122,17 @@ int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *id
                   const float *w, int n_used, int n_tokens, float *out,
                   float *h_out /* optional [n_tokens][n_used][d_ff] */, int n_threads);
 
+/* Router gating as ggml's CPU ops run it (qwen4exp.cpp:848-862 ->
+ * build_moe_ffn, softmax gating):
+ *   soft_max: m = max_i l_i (in order), e_i = expf(l_i - m), S = sum_i e_i in
+ *             double (in order), p_i = e_i * (float)(1.0 / S)
+ *   argsort_top_k: the n_used largest p, descending; ties to the lower index
+ *   get_rows, then with norm_w sum_rows (double, in order) and div; then
+ *   times w_scale when w_scale != 1 (ggml_scale).
+ * logits [n_tokens][n_experts], ids / w [n_tokens][n_used]. */
+int orc_moe_route(const float *logits, int n_tokens, int n_experts, int n_used, int norm_w, float w_scale,
+                  int32_t *ids, float *w);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,8 @@ def lib():
     L.orc_mul_mat_id.restype = ci
     L.orc_moe_layer.argtypes = [ctypes.POINTER(MoeLayerDesc), vp, vp, vp, ci, ci, vp, vp, ci]
     L.orc_moe_layer.restype = ci
+    L.orc_moe_route.argtypes = [vp, ci, ci, ci, ci, cf, vp, vp]
+    L.orc_moe_route.restype = ci
     _lib = L
     return L
 
@@ -203,3 +205,14 @@ def moe_layer(gate, up, down, qts, x, ids, w, shared=None, n_threads: int = 0,
     if rc != 0:
         raise ValueError("oracle moe_layer rejected its arguments")
     return (out, h) if return_h else out
+
+
+def moe_route(logits: np.ndarray, n_used: int, norm_w: bool = True, w_scale: float = 1.0):
+    """(ids [T, n_used] int32, w [T, n_used] f32) of ggml's softmax -> top-k -> renormalise."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    ids = np.zeros((T, n_used), np.int32)
+    w = np.zeros((T, n_used), np.float32)
+    if lib().orc_moe_route(_p(logits), T, E, n_used, int(norm_w), w_scale, _p(ids), _p(w)) != 0:
+        raise ValueError("oracle moe_route rejected its arguments")
+    return ids, w

@@ -20,6 +20,7 @@
 
 #include "mmid_kernels.h"
 #include "prefill_kernels.h"
+#include "route_kernels.h"
 #include "synth_kernels.h"
 #include "sabah_rt.h"
 
@@ -817,6 +818,28 @@ SABAH_API int sabah_moe_prefill_layer(const sabah_moe_layer_desc* layer, const f
     ++g_layer_calls;
     g_lookups += (unsigned long long)n_tokens * n_used;
     return moe_prefill_on(layer, d_x, d_ids, d_w, n_used, n_tokens, d_out, d_resid, pick_stream(stream));
+}
+
+SABAH_API int sabah_moe_route(const float* d_logits, int n_tokens, int n_experts, int n_used, int norm_w,
+                              float w_scale, int32_t* d_ids, float* d_w, void* stream) {
+    if (!d_logits || !d_ids || !d_w || n_tokens < 0) return fail("invalid route arguments");
+    if (n_experts <= 0 || n_experts > kRouteThreads * kRouteMaxPerThread)
+        return fail("route: n_experts %d outside [1, %d]", n_experts, kRouteThreads * kRouteMaxPerThread);
+    if (n_used <= 0 || n_used > n_experts || n_used > kRouteMaxUsed)
+        return fail("route: n_used %d outside [1, min(n_experts, %d)]", n_used, kRouteMaxUsed);
+    if (!(w_scale > 0.0f) || w_scale == __builtin_inff()) return fail("route: w_scale must be positive and finite");
+    if (g_device < 0) return fail("sabah_rt_init has not been called");
+    if (n_tokens == 0) return 0;
+    const RouteArgs a{d_logits, d_ids, d_w, n_experts, n_used, norm_w ? 1 : 0, w_scale};
+    const dim3 grid((unsigned)n_tokens), block(kRouteThreads);
+    hipStream_t st = pick_stream(stream);
+    const int per = (n_experts + kRouteThreads - 1) / kRouteThreads;
+    if (per <= 1) hipLaunchKernelGGL(k_route<1>, grid, block, 0, st, a);
+    else if (per <= 2) hipLaunchKernelGGL(k_route<2>, grid, block, 0, st, a);
+    else if (per <= 4) hipLaunchKernelGGL(k_route<4>, grid, block, 0, st, a);
+    else if (per <= 8) hipLaunchKernelGGL(k_route<8>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(k_route<kRouteMaxPerThread>, grid, block, 0, st, a);
+    return ck(hipGetLastError(), "route launch") ? 0 : -1;
 }
 
 // ===========================================================================

@@ -128,6 +128,18 @@ class MoEExecutor:
                  "moe_layer")
         return out
 
+    def route(self, logits: torch.Tensor, n_used: int | None = None, norm_w: bool = True,
+              w_scale: float = 1.0) -> tuple[torch.Tensor, torch.Tensor]:
+        """Router gating on the device (sabah_moe_route): ids [T, n_used] int32 and
+        weights [T, n_used] f32 from router logits [T, n_experts] f32."""
+        k = self.max_used if n_used is None else n_used
+        T, E = logits.shape
+        ids = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+        w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+        rt.check(rt.lib().sabah_moe_route(_vp(logits), T, E, k, int(norm_w), ctypes.c_float(w_scale), _vp(ids),
+                                          _vp(w), _stream(self.device)), "moe_route")
+        return ids, w
+
     def run_prefill_layer(self, layer: int, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor,
                           out: torch.Tensor | None = None, resid: torch.Tensor | None = None) -> torch.Tensor:
         """run_layer computed group-major (sabah_moe_prefill_layer): the (token, slot)

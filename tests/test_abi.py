@@ -116,3 +116,18 @@ def test_prefill_layer_rejects_shapes_it_does_not_group_without_a_device(kw):
     rc = L.sabah_moe_prefill_layer(ctypes.byref(d), vp(1), vp(1), vp(1), 10, 4, vp(1), None, None)
     assert rc == -1
     assert "grouped MoE layer" in rt.last_error() or "unsupported type mix" in rt.last_error()
+
+
+@pytest.mark.parametrize("args,msg", [((0, 10), "n_experts"), ((5000, 10), "n_experts"), ((512, 0), "n_used"),
+                                      ((8, 9), "n_used"), ((512, 65), "n_used")])
+def test_route_rejects_invalid_shapes_without_a_device(args, msg):
+    """sabah_moe_route takes 1 <= n_experts <= 4096 and 1 <= n_used <= min(n_experts, 64);
+    anything else is refused before the device is touched."""
+    from sabah.runtime import rt
+    L = rt.lib()
+    vp = ctypes.c_void_p
+    E, k = args
+    assert L.sabah_moe_route(vp(1), 3, E, k, 1, 1.0, vp(1), vp(1), None) == -1
+    assert msg in rt.last_error()
+    assert L.sabah_moe_route(vp(1), 3, 512, 10, 1, 0.0, vp(1), vp(1), None) == -1
+    assert "w_scale" in rt.last_error()
