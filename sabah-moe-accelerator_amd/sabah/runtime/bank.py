@@ -32,32 +32,51 @@ _ALIGN = 256
 
 
 class ExpertBank:
+    """qtypes: role -> ggml type code for every layer, or (layer, role) -> code
+    (a GGUF may quantise each layer's tensors differently).  `qtypes`,
+    `row_bytes` and `expert_stride` stay keyed by role when every layer agrees;
+    the per-layer forms are `layer_qtype`, `layer_row_bytes`, `layer_stride`."""
+
     def __init__(self, n_layers: int, n_experts: int, d_model: int, d_ff: int,
                  qtypes: dict, device: str = "cuda:0"):
         self.n_layers, self.n_experts = n_layers, n_experts
         self.d_model, self.d_ff = d_model, d_ff
-        self.qtypes = dict(qtypes)              # role -> ggml type code
+        self.lq = {}
+        for l in range(n_layers):
+            for r in ROLES:
+                self.lq[(l, r)] = int(qtypes[(l, r)] if (l, r) in qtypes else qtypes[r])
         self.device = torch.device(device)
         self.rows = {"gate": d_ff, "up": d_ff, "down": d_model}
         self.cols = {"gate": d_model, "up": d_model, "down": d_ff}
-        self.row_bytes = {r: rt.row_bytes(self.qtypes[r], self.cols[r]) for r in ROLES}
-        self.expert_stride = {r: self.rows[r] * self.row_bytes[r] for r in ROLES}
+        uniform = all(len({self.lq[(l, r)] for l in range(n_layers)}) == 1 for r in ROLES)
+        self.qtypes = {r: self.lq[(0, r)] for r in ROLES} if uniform else None
+        self.row_bytes = {r: rt.row_bytes(self.qtypes[r], self.cols[r]) for r in ROLES} if uniform else None
+        self.expert_stride = {r: self.rows[r] * self.row_bytes[r] for r in ROLES} if uniform else None
         self.offsets = {}
         off = 0
         for l in range(n_layers):
             for r in ROLES:
                 self.offsets[(l, r)] = off
-                off += (self.expert_stride[r] * n_experts + _ALIGN - 1) // _ALIGN * _ALIGN
+                off += (self.layer_stride(l, r) * n_experts + _ALIGN - 1) // _ALIGN * _ALIGN
         self.total_bytes = off
         self.storage = torch.empty(self.total_bytes, dtype=torch.uint8, device=self.device)
         self._registered = []
+
+    def layer_qtype(self, layer: int, role: str) -> int:
+        return self.lq[(layer, role)]
+
+    def layer_row_bytes(self, layer: int, role: str) -> int:
+        return rt.row_bytes(self.lq[(layer, role)], self.cols[role])
+
+    def layer_stride(self, layer: int, role: str) -> int:
+        return self.rows[role] * self.layer_row_bytes(layer, role)
 
     # ---- addressing ----------------------------------------------------------
     def tensor(self, layer: int, role: str) -> torch.Tensor:
         """[n_experts, rows, row_bytes] uint8 view of one (layer, role) tensor."""
         o = self.offsets[(layer, role)]
-        n = self.expert_stride[role] * self.n_experts
-        return self.storage[o:o + n].view(self.n_experts, self.rows[role], self.row_bytes[role])
+        n = self.layer_stride(layer, role) * self.n_experts
+        return self.storage[o:o + n].view(self.n_experts, self.rows[role], self.layer_row_bytes(layer, role))
 
     def base_ptr(self, layer: int, role: str) -> int:
         return self.storage.data_ptr() + self.offsets[(layer, role)]
@@ -65,10 +84,10 @@ class ExpertBank:
     def expert_ptr(self, layer: int, role: str, expert: int) -> int:
         if not 0 <= expert < self.n_experts:
             raise IndexError("expert %d outside [0, %d)" % (expert, self.n_experts))
-        return self.base_ptr(layer, role) + expert * self.expert_stride[role]
+        return self.base_ptr(layer, role) + expert * self.layer_stride(layer, role)
 
     def expert_bytes(self, layer: int, expert: int) -> int:
-        return sum(self.expert_stride[r] for r in ROLES)
+        return sum(self.layer_stride(layer, r) for r in ROLES)
 
     # ---- filling -------------------------------------------------------------
     def fill_synthetic(self, seed: int, sigma: float = 0.02, layers=None) -> None:
@@ -78,7 +97,7 @@ class ExpertBank:
         for l in (range(self.n_layers) if layers is None else layers):
             for i, r in enumerate(ROLES):
                 s = (int(seed) * 1000003 + l * 8 + i) & 0xFFFFFFFFFFFFFFFF
-                rt.check(L.sabah_synth_weights(ctypes.c_void_p(self.base_ptr(l, r)), self.qtypes[r],
+                rt.check(L.sabah_synth_weights(ctypes.c_void_p(self.base_ptr(l, r)), self.lq[(l, r)],
                                                self.n_experts * self.rows[r], self.cols[r],
                                                ctypes.c_ulonglong(s), ctypes.c_float(sigma),
                                                ctypes.c_void_p(stream)), "synth weights")
@@ -101,10 +120,15 @@ class ExpertBank:
         L = rt.lib()
         for (l, r), o in self.offsets.items():
             key = (key_base + o) if key_base is not None else self.base_ptr(l, r)
-            n = self.expert_stride[r] * self.n_experts
-            rt.check(L.sabah_rt_register_bank(ctypes.c_void_p(key), ctypes.c_void_p(self.base_ptr(l, r)), n,
-                                              self.expert_stride[r], self.n_experts), "register bank")
-            self._registered.append(key)
+            self.register_tensor(l, r, key)
+
+    def register_tensor(self, layer: int, role: str, key: int) -> None:
+        """Register one (layer, role) tensor under a caller-side key address."""
+        L = rt.lib()
+        stride = self.layer_stride(layer, role)
+        rt.check(L.sabah_rt_register_bank(ctypes.c_void_p(key), ctypes.c_void_p(self.base_ptr(layer, role)),
+                                          stride * self.n_experts, stride, self.n_experts), "register bank")
+        self._registered.append(key)
 
     def unregister(self) -> None:
         L = rt.lib()
@@ -116,7 +140,7 @@ class ExpertBank:
         """sabah_moe_layer_desc of one layer; shared = DenseExpert or None."""
         d = rt.MoeLayerDesc()
         d.gate, d.up, d.down = (self.base_ptr(layer, r) for r in ROLES)
-        d.qt_gate, d.qt_up, d.qt_down = (self.qtypes[r] for r in ROLES)
+        d.qt_gate, d.qt_up, d.qt_down = (self.lq[(layer, r)] for r in ROLES)
         d.d_model, d.d_ff, d.n_experts = self.d_model, self.d_ff, self.n_experts
         if shared is not None:
             d.shared_gate, d.shared_up, d.shared_down = shared.ptrs()

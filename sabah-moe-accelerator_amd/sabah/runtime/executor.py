@@ -82,7 +82,7 @@ class MoEExecutor:
         self.d_ptr[:3 * n].copy_(torch.from_numpy(flat))
         self.d_w[:n].copy_(torch.from_numpy(w))
         torch.cuda.current_stream(self.device).synchronize()     # the block runs on the library stream
-        q = self.bank.qtypes
+        q = {r: self.bank.layer_qtype(block, r) for r in ROLES}
         rt.check(rt.lib().sabah_moe_block(_vp(self.d_x), _vp(self.d_out), _vp(self.d_h), _vp(self.d_ptr),
                                           _vp(self.d_w), self.d_model, self.ff, n,
                                           q["gate"], q["up"], q["down"], 1 if accumulate else 0), "moe_block")
@@ -101,12 +101,12 @@ class MoEExecutor:
         (e.g. a registered caller-side key)."""
         b = self.bank
         T, n_ids = ids.shape
-        rows, k, qt = b.rows[role], b.cols[role], b.qtypes[role]
+        rows, k, qt = b.rows[role], b.cols[role], b.layer_qtype(layer, role)
         if out is None:
             out = torch.empty(T, n_ids, rows, dtype=torch.float32, device=self.device)
         src = b.base_ptr(layer, role) if source is None else source
         rc = rt.lib().sabah_rt_mul_mat_id_v2(
-            ctypes.c_void_p(src), b.expert_stride[role], b.row_bytes[role],
+            ctypes.c_void_p(src), b.layer_stride(layer, role), b.layer_row_bytes(layer, role),
             _vp(x), x.stride(1) * 4, x.shape[1], x.stride(0) * 4,
             _vp(ids), ids.stride(1) * 4, ids.stride(0) * 4, n_ids, T,
             _vp(out), out.stride(1) * 4, out.stride(0) * 4,
