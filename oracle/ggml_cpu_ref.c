@@ -18,6 +18,7 @@
  */
 #include "ggml_cpu_ref.h"
 #include "iq3s_grid_u32.h"
+#include "iq_tables_u32.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -28,8 +29,8 @@
 
 int orc_block_elems(int qt) {
     switch (qt) {
-    case ORC_Q8_0: return 32;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: return 256;
+    case ORC_Q8_0: case ORC_IQ4_NL: return 32;
+    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: return 256;
     }
     return 0;
 }
@@ -41,6 +42,9 @@ int orc_block_bytes(int qt) {
     case ORC_Q6_K: return 210;   /* ql[128], qh[64], int8 sc[16], fp16 d      */
     case ORC_Q8_K: return 292;   /* float d, int8 qs[256], int16 bsums[16]    */
     case ORC_IQ3_S: return 110;  /* d, qs[64], qh[8], signs[32], scales[4]    */
+    case ORC_IQ3_XXS: return 98; /* d, qs[64] grid indices, 8 x u32 scale/signs */
+    case ORC_IQ4_NL: return 18;  /* d, 16 B nibbles                          */
+    case ORC_IQ4_XS: return 136; /* d, scales_h u16, scales_l[4], qs[128]     */
     }
     return 0;
 }
@@ -53,8 +57,8 @@ size_t orc_row_bytes(int qt, int n) {
 
 int orc_vec_dot_type(int qt) {
     switch (qt) {
-    case ORC_Q8_0: return ORC_Q8_0;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: return ORC_Q8_K;
+    case ORC_Q8_0: case ORC_IQ4_NL: return ORC_Q8_0;
+    case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: return ORC_Q8_K;
     }
     return -1;
 }
@@ -256,6 +260,53 @@ int orc_dequantize_row(int qt, const uint8_t *x, float *y, int k) {
             }
         }
         return 0;
+    case ORC_IQ3_XXS:   /* sabah_rt.cu:2320-2344; quants.py:1039-1075 */
+        for (int b = 0; b < k / 256; ++b, x += 98) {
+            const float d = ld_f16(x);
+            const uint8_t *qs = x + 2, *ss = x + 66;
+            for (int ib = 0; ib < 8; ++ib) {
+                uint32_t aux;
+                memcpy(&aux, ss + 4 * ib, 4);
+                const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+                for (int l = 0; l < 4; ++l) {
+                    const uint8_t sg = orc_ksigns_iq2xs[(aux >> (7 * l)) & 127];
+                    const uint32_t g1 = orc_iq3xxs_grid[qs[8 * ib + 2 * l]], g2 = orc_iq3xxs_grid[qs[8 * ib + 2 * l + 1]];
+                    for (int j = 0; j < 4; ++j) {
+                        y[j] = db * (float)((g1 >> (8 * j)) & 0xFF) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                        y[j + 4] = db * (float)((g2 >> (8 * j)) & 0xFF) * ((sg >> (j + 4)) & 1 ? -1.0f : 1.0f);
+                    }
+                    y += 8;
+                }
+            }
+        }
+        return 0;
+    case ORC_IQ4_NL:    /* sabah_rt.cu:2380-2389; quants.py:1364-1382 */
+        for (int b = 0; b < k / 32; ++b, x += 18) {
+            const float d = ld_f16(x);
+            for (int j = 0; j < 16; ++j) {
+                y[j] = d * (float)orc_kvalues_iq4nl[x[2 + j] & 0xF];
+                y[j + 16] = d * (float)orc_kvalues_iq4nl[x[2 + j] >> 4];
+            }
+            y += 32;
+        }
+        return 0;
+    case ORC_IQ4_XS:    /* sabah_rt.cu:2391-2409; quants.py:1385-1411 */
+        for (int b = 0; b < k / 256; ++b, x += 136) {
+            const float d = ld_f16(x);
+            const int sh = x[2] | (x[3] << 8);
+            const uint8_t *sl = x + 4, *qs = x + 8;
+            for (int ib = 0; ib < 8; ++ib) {
+                const int ls = ((sl[ib / 2] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
+                const float dl = d * (float)(ls - 32);
+                for (int j = 0; j < 16; ++j) {
+                    y[j] = dl * (float)orc_kvalues_iq4nl[qs[j] & 0xF];
+                    y[j + 16] = dl * (float)orc_kvalues_iq4nl[qs[j] >> 4];
+                }
+                y += 32;
+                qs += 16;
+            }
+        }
+        return 0;
     }
     return -1;
 }
@@ -371,12 +422,84 @@ static float dot_iq3_s(const uint8_t *w, const uint8_t *a, int k) {
     return sumf;
 }
 
+/* ggml_vec_dot_iq3_xxs_q8_K (generic): bsum = sum_ib32 (2*(aux>>28)+1) *
+ * sum(grid*sign*q8) per super-block (sign byte = ksigns[7-bit index]);
+ * sumf += (dw*d8) * bsum; the result is 0.25f * sumf. */
+static float dot_iq3_xxs(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 256; ++b, w += 98, a += 292) {
+        const uint8_t *q3 = w + 2, *gas = w + 66;
+        const int8_t *q8 = q8K_qs(a);
+        int bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t aux;
+            memcpy(&aux, gas + 4 * ib, 4);
+            const int ls = 2 * (int)(aux >> 28) + 1;
+            int sumi = 0;
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t g1 = orc_iq3xxs_grid[q3[8 * ib + 2 * l]], g2 = orc_iq3xxs_grid[q3[8 * ib + 2 * l + 1]];
+                const uint8_t sg = orc_ksigns_iq2xs[(aux >> (7 * l)) & 127];
+                for (int j = 0; j < 4; ++j) {
+                    sumi += (int)((g1 >> (8 * j)) & 0xFF) * (int)q8[32 * ib + 8 * l + j] * ((sg >> j) & 1 ? -1 : 1);
+                    sumi += (int)((g2 >> (8 * j)) & 0xFF) * (int)q8[32 * ib + 8 * l + 4 + j] * ((sg >> (j + 4)) & 1 ? -1 : 1);
+                }
+            }
+            bsum += sumi * ls;
+        }
+        const float d = ld_f16(w) * q8K_d(a);
+        sumf += d * (float)bsum;
+    }
+    return 0.25f * sumf;
+}
+
+/* ggml_vec_dot_iq4_nl_q8_0 (generic): per 32-block sumf += (d8*dw) * sum(kv[q]*q8). */
+static float dot_iq4_nl(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 32; ++b, w += 18, a += 34) {
+        const float d = ld_f16(a) * ld_f16(w);
+        const int8_t *q8 = (const int8_t *)(a + 2);
+        int s1 = 0, s2 = 0;
+        for (int j = 0; j < 16; ++j) {
+            s1 += (int)q8[j] * (int)orc_kvalues_iq4nl[w[2 + j] & 0xF];
+            s2 += (int)q8[j + 16] * (int)orc_kvalues_iq4nl[w[2 + j] >> 4];
+        }
+        sumf += d * (float)(s1 + s2);
+    }
+    return sumf;
+}
+
+/* ggml_vec_dot_iq4_xs_q8_K (generic): per 32-element sub-block
+ * sumf += ((dw*d8) * (ls - 32)) * sum(kv[q]*q8), sub-blocks in order. */
+static float dot_iq4_xs(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 256; ++b, w += 136, a += 292) {
+        const float d4d8 = ld_f16(w) * q8K_d(a);
+        const int sh = w[2] | (w[3] << 8);
+        const uint8_t *sl = w + 4, *qs = w + 8;
+        const int8_t *q8 = q8K_qs(a);
+        for (int ib = 0; ib < 8; ++ib) {
+            const int ls = ((sl[ib / 2] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
+            const float dl = d4d8 * (float)(ls - 32);
+            int s1 = 0, s2 = 0;
+            for (int j = 0; j < 16; ++j) {
+                s1 += (int)q8[32 * ib + j] * (int)orc_kvalues_iq4nl[qs[16 * ib + j] & 0xF];
+                s2 += (int)q8[32 * ib + 16 + j] * (int)orc_kvalues_iq4nl[qs[16 * ib + j] >> 4];
+            }
+            sumf += dl * (float)(s1 + s2);
+        }
+    }
+    return sumf;
+}
+
 float orc_vec_dot(int qt, const uint8_t *w, const uint8_t *a, int k) {
     switch (qt) {
     case ORC_Q8_0: return dot_q8_0(w, a, k);
     case ORC_Q4_K: return dot_q4_K(w, a, k);
     case ORC_Q6_K: return dot_q6_K(w, a, k);
     case ORC_IQ3_S: return dot_iq3_s(w, a, k);
+    case ORC_IQ3_XXS: return dot_iq3_xxs(w, a, k);
+    case ORC_IQ4_NL: return dot_iq4_nl(w, a, k);
+    case ORC_IQ4_XS: return dot_iq4_xs(w, a, k);
     }
     return NAN;
 }
@@ -516,6 +639,59 @@ static void enc_q6_K(const float *x, uint8_t *y, int k) {
     }
 }
 
+/* IQ4 levels: the index of the level nearest v (lowest on ties) */
+static int iq4_nearest(float v) {
+    int best = 0;
+    float be = fabsf(v - (float)orc_kvalues_iq4nl[0]);
+    for (int i = 1; i < 16; ++i) {
+        const float e = fabsf(v - (float)orc_kvalues_iq4nl[i]);
+        if (e < be) { be = e; best = i; }
+    }
+    return best;
+}
+
+/* simple IQ4_NL encoder (synthetic data): d = amax / 127 per 32-block, nearest level */
+static void enc_iq4_nl(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 32; ++b, x += 32, y += 18) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+        const uint16_t dh = orc_fp32_to_fp16(amax / 127.0f);
+        const float d = orc_fp16_to_fp32(dh), id = d > 0.0f ? 1.0f / d : 0.0f;
+        y[0] = (uint8_t)dh; y[1] = (uint8_t)(dh >> 8);
+        for (int j = 0; j < 16; ++j)
+            y[2 + j] = (uint8_t)(iq4_nearest(x[j] * id) | (iq4_nearest(x[j + 16] * id) << 4));
+    }
+}
+
+/* simple IQ4_XS encoder (synthetic data): one fp16 d per super-block, 6-bit
+ * sub-block scales ls in [33, 63] (ls - 32 in [1, 31]), nearest level */
+static void enc_iq4_xs(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 256; ++b, x += 256, y += 136) {
+        float am[8], amax = 0.0f;
+        for (int ib = 0; ib < 8; ++ib) {
+            am[ib] = 0.0f;
+            for (int j = 0; j < 32; ++j) am[ib] = fmaxf(am[ib], fabsf(x[32 * ib + j]));
+            amax = fmaxf(amax, am[ib]);
+        }
+        const uint16_t dh = orc_fp32_to_fp16(amax / (127.0f * 31.0f));
+        const float d = orc_fp16_to_fp32(dh);
+        y[0] = (uint8_t)dh; y[1] = (uint8_t)(dh >> 8);
+        memset(y + 2, 0, 6);
+        int sh = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int s = d > 0.0f ? clampi((int)lrintf(am[ib] / (127.0f * d)), 1, 31) : 1;
+            const int ls = s + 32;
+            y[4 + ib / 2] |= (uint8_t)((ls & 0xF) << (4 * (ib & 1)));
+            sh |= ((ls >> 4) & 3) << (2 * ib);
+            const float id = d > 0.0f ? 1.0f / (d * (float)s) : 0.0f;
+            for (int j = 0; j < 16; ++j)
+                y[8 + 16 * ib + j] = (uint8_t)(iq4_nearest(x[32 * ib + j] * id) |
+                                               (iq4_nearest(x[32 * ib + 16 + j] * id) << 4));
+        }
+        y[2] = (uint8_t)sh; y[3] = (uint8_t)(sh >> 8);
+    }
+}
+
 int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k) {
     if (orc_row_bytes(qt, k) == 0) return -1;
     switch (qt) {
@@ -523,6 +699,8 @@ int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k) {
     case ORC_Q4_K: enc_q4_K(x, y, k); return 0;
     case ORC_Q6_K: enc_q6_K(x, y, k); return 0;
     case ORC_IQ3_S: enc_iq3_s(x, y, k); return 0;
+    case ORC_IQ4_NL: enc_iq4_nl(x, y, k); return 0;
+    case ORC_IQ4_XS: enc_iq4_xs(x, y, k); return 0;
     }
     return -1;
 }

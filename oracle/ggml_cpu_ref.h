@@ -53,7 +53,10 @@ enum {
     ORC_Q4_K = 12,
     ORC_Q6_K = 14,
     ORC_Q8_K = 15,
+    ORC_IQ3_XXS = 18,
+    ORC_IQ4_NL = 20,
     ORC_IQ3_S = 21,
+    ORC_IQ4_XS = 23,
 };
 
 /* Block geometry: elements and bytes per block (sabah_rt.cu:2155-2184;

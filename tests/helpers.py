@@ -42,7 +42,7 @@ def f16(x: float) -> bytes:
 def dequant_act(O, qt: int, act: np.ndarray, k: int) -> np.ndarray:
     """float64 values of a quantised activation row (as its vec_dot partner sees them)."""
     act = np.ascontiguousarray(act, np.uint8).reshape(-1)
-    if qt == O.Q8_0:
+    if qt in (O.Q8_0, O.IQ4_NL):                     # q8_0 activations
         blk = act.reshape(-1, 34)
         d = blk[:, :2].copy().view(np.float16).astype(np.float64)
         return (blk[:, 2:].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
@@ -85,7 +85,7 @@ def random_blocks(rng, qt: int, n_rows: int, k: int) -> np.ndarray:
     def scales(n):
         return (rng.uniform(0.25, 2.0, size=n) * rng.choice([-1, 1], size=n) * 1e-2).astype(np.float16)
 
-    if qt in (8, 21):                       # Q8_0, IQ3_S: fp16 d at 0
+    if qt in (8, 18, 20, 21, 23):           # Q8_0, IQ3_XXS, IQ4_NL, IQ3_S, IQ4_XS: fp16 d at 0
         raw[:, :, 0:2] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
     elif qt == 12:                          # Q4_K: d, dmin at 0, 2 (non-negative in real data)
         raw[:, :, 0:2] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)
@@ -118,3 +118,25 @@ def unfused_rounding_row(k: int, amax: float = 3.0) -> np.ndarray:
         row[256 * b] = amax
         row[256 * b + 1:256 * (b + 1)] = [hits[(b * per + i) % len(hits)] for i in range(per)]
     return row
+
+
+def reference_table(name: str, n: int, width: int) -> list[int] | None:
+    """A table of the reference's sabah_iq_tables.h (text parse), or None if it is not mounted."""
+    p = os.path.join(REF, "sabah/runtime/cuda/sabah_iq_tables.h")
+    if not os.path.exists(p):
+        return None
+    t = open(p).read()
+    i = t.index(name + "[%d]" % n)
+    body = t[t.index("{", i):t.index("};", i)]
+    if width == 0:
+        return [int(x) for x in re.findall(r"-?\d+", body)]
+    return [int(x, 16) for x in re.findall(r"0x([0-9a-fA-F]{%d})" % width, body)]
+
+
+def oracle_table(name: str) -> list[int]:
+    """A table of oracle/iq_tables_u32.h."""
+    t = open(os.path.join(ROOT, "oracle", "iq_tables_u32.h")).read()
+    i = t.index(name + "[")
+    body = t[t.index("{", i):t.index("};", i)]
+    return [int(x, 0) for x in re.findall(r"-?0x[0-9a-fA-F]+|-?\d+", body)]
+

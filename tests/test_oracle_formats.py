@@ -7,6 +7,8 @@ float64 recomputation from independently decoded operands.
 """
 from __future__ import annotations
 
+import struct
+
 import numpy as np
 import pytest
 
@@ -374,3 +376,103 @@ def test_encoders_round_trip(orc):
         back = orc.dequantize(qt, orc.quantize_weights(qt, w), k)
         err = np.linalg.norm(back - w) / np.linalg.norm(w)
         assert err < tol, (qt, err)
+
+
+# ---------------------------------------------------------------------------
+# IQ3_XXS, IQ4_NL, IQ4_XS (sabah_rt.cu:2320-2344, 2380-2409; quants.py:1039-1075, 1364-1411)
+# ---------------------------------------------------------------------------
+IQ3_XXS, IQ4_NL, IQ4_XS = 18, 20, 23
+KV = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def test_iq4_nl_known_answer(orc):
+    qs = bytes((j | ((15 - j) << 4)) for j in range(16))
+    blk = np.frombuffer(f16(1.0) + qs, np.uint8)
+    y = orc.dequantize(IQ4_NL, blk, 32)
+    assert y[:16].tolist() == KV and y[16:].tolist() == KV[::-1]
+    blk = np.frombuffer(f16(0.5) + qs, np.uint8)
+    assert np.array_equal(orc.dequantize(IQ4_NL, blk, 32), y * np.float32(0.5))
+
+
+def test_iq4_xs_known_answer_scales(orc):
+    """ls of sub-block ib = scales_l nibble ib | 2 bits ib of scales_h << 4; value d*(ls-32)*kv[q]."""
+    ls = [33, 32, 63, 0, 40, 17, 48, 31]
+    sh = sum(((v >> 4) & 3) << (2 * i) for i, v in enumerate(ls))
+    sl = bytes((ls[2 * i] & 15) | ((ls[2 * i + 1] & 15) << 4) for i in range(4))
+    qs = bytes((j % 16) | (((j + 5) % 16) << 4) for j in range(128))
+    blk = np.frombuffer(f16(1.0) + struct.pack("<H", sh) + sl + qs, np.uint8)
+    y = orc.dequantize(IQ4_XS, blk, 256).reshape(8, 32)
+    for ib in range(8):
+        q = [j % 16 for j in range(16 * ib, 16 * ib + 16)]
+        want = [KV[v] * (ls[ib] - 32) for v in q] + [KV[(v + 5) % 16] * (ls[ib] - 32) for v in q]
+        assert y[ib].tolist() == want, ib
+
+
+def test_iq3_xxs_known_answer_grid_signs_and_scale(orc):
+    from helpers import oracle_table
+    grid = oracle_table("orc_iq3xxs_grid")
+    qs = np.arange(64, dtype=np.uint8) * 3            # grid entries 0, 3, ..., 189
+    aux = []
+    for ib in range(8):           # sign indices (7 bits each) and the scale nibble
+        s7 = [(5 * ib + l) & 127 for l in range(4)]
+        aux.append(s7[0] | (s7[1] << 7) | (s7[2] << 14) | (s7[3] << 21) | (ib << 28))
+    blk = np.frombuffer(f16(1.0) + qs.tobytes() + struct.pack("<8I", *aux), np.uint8)
+    y = orc.dequantize(IQ3_XXS, blk, 256)
+    for ib in range(8):
+        db = (0.5 + ib) * 0.5
+        for l in range(4):
+            s7 = (5 * ib + l) & 127
+            sg = s7 | ((bin(s7).count("1") & 1) << 7)
+            for h in range(2):
+                g = grid[int(qs[8 * ib + 2 * l + h])]
+                for j in range(4):
+                    e = 32 * ib + 8 * l + 4 * h + j
+                    sign = -1.0 if (sg >> (4 * h + j)) & 1 else 1.0
+                    assert y[e] == np.float32(db * ((g >> (8 * j)) & 0xFF) * sign), (ib, l, h, j)
+
+
+@pytest.mark.parametrize("qt,k", [(IQ3_XXS, 512), (IQ4_NL, 256), (IQ4_XS, 512)])
+def test_new_iq_dots_match_float64_of_decoded_operands(orc, qt, k):
+    rng = np.random.default_rng(qt + 100)
+    raw = random_blocks(rng, qt, 8, k)
+    w = orc.dequantize(qt, raw, k).astype(np.float64)
+    for r in range(8):
+        x = rng.standard_normal(k).astype(np.float32)
+        a = orc.quantize_act(qt, x[None])[0]
+        ref = float(w[r] @ dequant_act(orc, qt, a, k))
+        got = orc.vec_dot(qt, raw[r], a, k)
+        scale = float(np.abs(w[r]).max() * np.abs(dequant_act(orc, qt, a, k)).sum())
+        assert abs(got - ref) <= 1e-6 * scale, (qt, r, got, ref)
+
+
+def test_iq3_xxs_dot_is_a_quarter_of_the_exact_integer_sum(orc):
+    from helpers import oracle_table
+    grid = oracle_table("orc_iq3xxs_grid")
+    rng = np.random.default_rng(12)
+    qs = rng.integers(0, 256, 64).astype(np.uint8)
+    aux = rng.integers(0, 2 ** 32, 8, dtype=np.uint64).astype(np.uint32)
+    blk = np.frombuffer(f16(1.0) + qs.tobytes() + aux.tobytes(), np.uint8)
+    xi = rng.integers(-126, 127, 256).astype(np.float32)
+    xi[3] = -127.0                                     # activation scale d = 1 exactly
+    a = orc.quantize_q8_K(xi)
+    total = 0
+    for ib in range(8):
+        v = int(aux[ib])
+        ls = 2 * (v >> 28) + 1
+        for l in range(4):
+            s7 = (v >> (7 * l)) & 127
+            sg = s7 | ((bin(s7).count("1") & 1) << 7)
+            for h in range(2):
+                g = grid[int(qs[8 * ib + 2 * l + h])]
+                for j in range(4):
+                    e = 32 * ib + 8 * l + 4 * h + j
+                    total += ls * ((g >> (8 * j)) & 0xFF) * (-1 if (sg >> (4 * h + j)) & 1 else 1) * int(xi[e])
+    assert orc.vec_dot(IQ3_XXS, blk, a, 256) == np.float32(0.25) * np.float32(total)
+
+
+@pytest.mark.parametrize("qt", [IQ4_NL, IQ4_XS])
+def test_iq4_encoders_round_trip(orc, qt):
+    rng = np.random.default_rng(qt)
+    w = (rng.standard_normal((8, 512)) * 0.02).astype(np.float32)
+    back = orc.dequantize(qt, orc.quantize_weights(qt, w), 512)
+    assert np.sqrt(np.mean((back - w) ** 2)) < 0.15 * np.sqrt(np.mean(w ** 2))
