@@ -133,7 +133,7 @@ constexpr int kMaxTiles = 64;
 
 // 16-byte loads per lane per pass
 __host__ __device__ constexpr int stage_iters(int qt) {
-    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : 9;
+    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7 : qt == QT_IQ4_NL ? 5 : 9;
 }
 // the same load count spread over nt threads
 __host__ __device__ constexpr int stage_iters_nt(int qt, int nt) { return (stage_iters(qt) * kThreads + nt - 1) / nt; }
@@ -169,10 +169,13 @@ __host__ __device__ inline int pass_units(int qt, int n_mat, int unit_bytes) {
     return max(1, (16 * tile_chunk_cap(qt, n_mat) - 30) / unit_bytes);
 }
 
-// Q8_0 rows need only be whole 32-element blocks: their last unit may hold 1..3 blocks
-__host__ __device__ inline int units_per_row(int qt, int k) { return qt == QT_Q8_0 ? (k + 127) / 128 : k / 256; }
-__host__ __device__ inline int contribs_per_row(int qt, int k) { return k / block_elems(qt); }   // ggml blocks
-__host__ __device__ inline int unit_bytes(int qt) { return qt == QT_Q8_0 ? 136 : (int)block_bytes(qt); }
+// Q8_0 and IQ4_NL rows need only be whole 32-element blocks: their last unit
+// may hold 1..3 blocks
+__host__ __device__ inline bool four_block_units(int qt) { return qt == QT_Q8_0 || qt == QT_IQ4_NL; }
+__host__ __device__ inline int units_per_row(int qt, int k) { return four_block_units(qt) ? (k + 127) / 128 : k / 256; }
+// fp32 terms of ggml's row sum: one per block, one per 32-element sub-block for IQ4_XS
+__host__ __device__ inline int contribs_per_row(int qt, int k) { return qt == QT_IQ4_XS ? k / 32 : k / block_elems(qt); }
+__host__ __device__ inline int unit_bytes(int qt) { return four_block_units(qt) ? 4 * (int)block_bytes(qt) : (int)block_bytes(qt); }
 
 // Rows per workgroup: about one unit per lane, with the n_mat tiles staged in
 // one pass where a row fits.
@@ -209,21 +212,21 @@ __host__ __device__ inline Plan make_plan(int qt, int k, int n_act, int n_part) 
 // leads, then the staging area with a guard on each side
 template <int QT>
 struct StaticLds {
-    static constexpr int TABLES = (QT == QT_IQ3_S) ? kLdsTables : 0;
+    static constexpr int TABLES = table_bytes(QT);
     static constexpr int LEADS = TABLES;
     static constexpr int STAGE = LEADS + 4 * kMaxTiles + kStageGuard;
     static constexpr int BYTES = STAGE + kStageBytes + kStageGuard;
 };
 // total LDS of a launch (static + dynamic), for the host's limit check
 __host__ inline int launch_lds(int qt, const Plan& P) {
-    const int tables = (qt == QT_IQ3_S) ? kLdsTables : 0;
+    const int tables = table_bytes(qt);
     return tables + 4 * kMaxTiles + 2 * kStageGuard + kStageBytes + P.bytes;
 }
 
 // bytes of unit us of a row of k elements
 template <int QT>
 __device__ inline int unit_len(int k, int us) {
-    if constexpr (QT == QT_Q8_0) return 34 * min(4, k / 32 - 4 * us);
+    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL) return block_bytes(QT) * min(4, k / 32 - 4 * us);
     return UnitFmt<QT>::BYTES;
 }
 
@@ -235,13 +238,17 @@ __device__ inline void unit_into_part(const LdsWindow<QT>& Wn, const uint8_t* ta
     const ActLayout AL(k, act_type(QT));
     const float* dxa = reinterpret_cast<const float*>(act + AL.off_d);
     const int16_t* bsa = reinterpret_cast<const int16_t*>(act + AL.off_bsum);
-    if constexpr (QT == QT_Q8_0) {
+    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL) {
         const uint8_t* chunk = act + (us >> 1) * kActChunkStride + (us & 1) * 128;
         const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + 4 * us, bsa);
         const int nb = min(4, k / 32 - 4 * us);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (j < nb) part_row[4 * us + j] = r.c[j];
+    } else if constexpr (QT == QT_IQ4_XS) {
+        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, act + us * kActChunkStride, dxa + us, bsa + 16 * us);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part_row[8 * us + j] = r.c[j];
     } else {
         const uint8_t* chunk = act + us * kActChunkStride;
         const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + us, bsa + 16 * us);
@@ -486,8 +493,7 @@ __global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
     const ActBatch xb{xr, 0, 1, a.k, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
     act_prefetch<kRoundsX>(xb, xa);
-    GridRegs<kThreads> gr;
-    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    const TableRegs<QT, kThreads> gr = load_tables<QT, kThreads>((int)threadIdx.x);
     const uint8_t* w = expert_ptr(a.W, a.rt, t, i, a.n_ids);
     if (w == nullptr) {   // uniform across the workgroup
         flag_error(a.err);
@@ -499,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
     auto tile_ptr = [&](int r) { return packed ? w : w + (size_t)r * a.row_stride; };
     TileRun<QT> S{TileWalk<QT>(packed ? 1 : nrows, packed ? nrows : 1, rb, a.k)};
     tiles_begin(S, tile_ptr);
-    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    store_tables<QT, kThreads>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsX>(xb, xa);
     // the gate's loads come after the weights', so it waits for what the
     // staging waits for anyway; the staging's barrier publishes the sums
@@ -545,8 +551,7 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
     act_prefetch<kRoundsX>(xb, xa);
-    GridRegs<kThreads> gr;
-    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    const TableRegs<QT, kThreads> gr = load_tables<QT, kThreads>((int)threadIdx.x);
     const uint8_t *wg, *wu;
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
@@ -559,7 +564,7 @@ __global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
     auto tile_ptr = [&](int m) { return m ? wu : wg; };
     TileRun<QT> S{TileWalk<QT>(2, nrows, rb, a.d_model)};
     tiles_begin(S, tile_ptr);
-    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    store_tables<QT, kThreads>(tabs, gr, (int)threadIdx.x);
     act_quantize<kRoundsX>(xb, xa);
     tiles_finish(S, tabs, stage, leads, a.d_model, act, 0, a.R, part);
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
@@ -777,15 +782,14 @@ __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
     const float sh0 = a.shared && r0 < nrows ? a.shared[orow] : 0.0f;
     const float rs0 = a.resid && r0 < nrows ? a.resid[orow] : 0.0f;
     const float ac0 = a.accumulate && r0 < nrows ? a.out[orow] : 0.0f;
-    GridRegs<NT> gr;
-    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
+    const TableRegs<QT, NT> gr = load_tables<QT, NT>((int)threadIdx.x);
     const uint8_t* e = resolve_slot_word(a.D, a.rt, sw);
     const bool bad = __any(e == nullptr);
     const uint8_t* mine = (e ? e : a.D.base) + (size_t)row0 * rb;
     auto tile_ptr = [&](int m) { return lane_ptr(mine, m); };
     TileRun<QT, NT> S{TileWalk<QT, NT>(a.n_slots, nrows, rb, a.d_ff)};
     tiles_begin(S, tile_ptr);
-    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
+    store_tables<QT, NT>(tabs, gr, (int)threadIdx.x);
     act_quantize<RH>(hb, ha);
     tiles_finish(S, tabs, stage, leads, a.d_ff, act, P.act_bytes, a.R, part);
     float* o = a.out + (size_t)t * a.d_model + row0;
@@ -819,7 +823,7 @@ template <int QT>
 __global__ __launch_bounds__(kThreads) void k_dequant(const uint8_t* __restrict__ src, float* __restrict__ dst,
                                                       int n_rows, int k) {
     extern __shared__ __align__(16) uint8_t smem[];
-    if constexpr (QT == QT_IQ3_S) stage_iq3s_tables(smem);
+    store_tables<QT, kThreads>(smem, load_tables<QT, kThreads>((int)threadIdx.x), (int)threadIdx.x);
     __syncthreads();
     const int NUS = units_per_row(QT, k);
     const long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x;

@@ -215,6 +215,9 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
     case QT_Q4_K: return launch_mmid<QT_Q4_K>(a, st);
     case QT_Q6_K: return launch_mmid<QT_Q6_K>(a, st);
     case QT_IQ3_S: return launch_mmid<QT_IQ3_S>(a, st);
+    case QT_IQ3_XXS: return launch_mmid<QT_IQ3_XXS>(a, st);
+    case QT_IQ4_NL: return launch_mmid<QT_IQ4_NL>(a, st);
+    case QT_IQ4_XS: return launch_mmid<QT_IQ4_XS>(a, st);
     }
     return hipErrorInvalidValue;
 }
@@ -243,6 +246,9 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
     case QT_Q4_K: return launch_gate_up<QT_Q4_K>(a, n_tokens, st);
     case QT_Q6_K: return launch_gate_up<QT_Q6_K>(a, n_tokens, st);
     case QT_IQ3_S: return launch_gate_up<QT_IQ3_S>(a, n_tokens, st);
+    case QT_IQ3_XXS: return launch_gate_up<QT_IQ3_XXS>(a, n_tokens, st);
+    case QT_IQ4_NL: return launch_gate_up<QT_IQ4_NL>(a, n_tokens, st);
+    case QT_IQ4_XS: return launch_gate_up<QT_IQ4_XS>(a, n_tokens, st);
     }
     return hipErrorInvalidValue;
 }
@@ -264,6 +270,9 @@ hipError_t dispatch_down(int qt, const DownArgs& a, int n_tokens, hipStream_t st
     case QT_Q4_K: return launch_down<QT_Q4_K>(a, n_tokens, st);
     case QT_Q6_K: return launch_down<QT_Q6_K>(a, n_tokens, st);
     case QT_IQ3_S: return launch_down<QT_IQ3_S>(a, n_tokens, st);
+    case QT_IQ3_XXS: return launch_down<QT_IQ3_XXS>(a, n_tokens, st);
+    case QT_IQ4_NL: return launch_down<QT_IQ4_NL>(a, n_tokens, st);
+    case QT_IQ4_XS: return launch_down<QT_IQ4_XS>(a, n_tokens, st);
     }
     return hipErrorInvalidValue;
 }
@@ -540,13 +549,16 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
     if (n_rows == 0) return 0;
     const long long nunits = (long long)n_rows * units_per_row(qt, row_elems);
     dim3 grid((unsigned)((nunits + kThreads - 1) / kThreads));
-    const size_t lds = qt == QT_IQ3_S ? kLdsTables : 0;
+    const size_t lds = table_bytes(qt);
     const uint8_t* s = reinterpret_cast<const uint8_t*>(d_src);
     switch (qt) {
     case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_IQ3_XXS: hipLaunchKernelGGL(k_dequant<QT_IQ3_XXS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_IQ4_NL: hipLaunchKernelGGL(k_dequant<QT_IQ4_NL>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_IQ4_XS: hipLaunchKernelGGL(k_dequant<QT_IQ4_XS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     }
     if (!ck(hipGetLastError(), "dequant launch")) return -1;
     return ck(hipStreamSynchronize(g_stream), "dequant sync") ? 0 : -1;
@@ -879,6 +891,8 @@ SABAH_API int sabah_synth_weights(void* d_dst, int qt, long long n_rows, int k, 
         return fail("synth: invalid arguments (type %d, k %d)", qt, k);
     if (g_device < 0) return fail("sabah_rt_init has not been called");
     if (n_rows == 0) return 0;
+    if (qt != QT_Q8_0 && qt != QT_Q4_K && qt != QT_Q6_K && qt != QT_IQ3_S)
+        return fail("synth: no device encoder for type %d (load the bank's bytes instead)", qt);
     if (qt == QT_IQ3_S && ensure_nearest_table()) return -1;
     const long long nb = n_rows * (long long)(k / block_elems(qt));
     const dim3 grid((unsigned)((nb + 255) / 256));

@@ -1,7 +1,8 @@
 // Register-resident decoding of quantised weights, one "unit" per lane.
 //
-// A unit is one 256-element super-block (Q4_K 144 B, Q6_K 210 B, IQ3_S 110 B)
-// or four 32-element Q8_0 blocks (136 B).  Each lane loads its unit straight
+// A unit is one 256-element super-block (Q4_K 144 B, Q6_K 210 B, IQ3_S 110 B,
+// IQ3_XXS 98 B, IQ4_XS 136 B) or four 32-element blocks (Q8_0 136 B, IQ4_NL
+// 72 B).  Each lane loads its unit straight
 // from HBM into VGPRs with 8-byte loads that cover exactly the unit's 8-byte
 // granules (so a load never touches a page the unit does not), then
 // re-aligns the bytes so that every field of the format sits at a static
@@ -9,12 +10,13 @@
 // q8 activations held in LDS.
 //
 // Field origin: all fields used in the inner loops start at the same residue
-// mod 4 inside the block (IQ3_S: byte 2; Q8_0 even blocks: byte 2; Q4_K and
-// Q6_K: byte 0).  F[i] is the dword at (unit start + ORG + 4 i); Fm1 is the
+// mod 4 inside the block (IQ3_S, IQ3_XXS: byte 2; Q8_0 and IQ4_NL even
+// blocks: byte 2; Q4_K, Q6_K and IQ4_XS: byte 0).  F[i] is the dword at (unit start + ORG + 4 i); Fm1 is the
 // dword before it (IQ3_S reads its fp16 d there).
 //
 // Block layouts: sabah_rt.cu:2462-2485 (Q4_K), 2537-2545 (Q8_0), 2618-2647
-// (IQ3_S); gguf-py quants.py:586-606 (Q6_K: ql[128] qh[64] int8 sc[16] d).
+// (IQ3_S), 2320-2344 (IQ3_XXS), 2380-2409 (IQ4_NL, IQ4_XS); gguf-py
+// quants.py:586-606 (Q6_K: ql[128] qh[64] int8 sc[16] d).
 #pragma once
 #include "quant_formats.h"
 
@@ -42,6 +44,9 @@ template <> struct UnitFmt<QT_IQ3_S> { static constexpr int BYTES = 110, ELEMS =
 template <> struct UnitFmt<QT_Q4_K> { static constexpr int BYTES = 144, ELEMS = 256, ORG = 0, NF = 36, CONTRIB = 1; };
 template <> struct UnitFmt<QT_Q6_K> { static constexpr int BYTES = 210, ELEMS = 256, ORG = 0, NF = 53, CONTRIB = 1; };
 template <> struct UnitFmt<QT_Q8_0> { static constexpr int BYTES = 136, ELEMS = 128, ORG = 2, NF = 34, CONTRIB = 4; };
+template <> struct UnitFmt<QT_IQ3_XXS> { static constexpr int BYTES = 98, ELEMS = 256, ORG = 2, NF = 24, CONTRIB = 1; };
+template <> struct UnitFmt<QT_IQ4_XS> { static constexpr int BYTES = 136, ELEMS = 256, ORG = 0, NF = 34, CONTRIB = 8; };
+template <> struct UnitFmt<QT_IQ4_NL> { static constexpr int BYTES = 72, ELEMS = 128, ORG = 2, NF = 18, CONTRIB = 4; };
 
 // Window: the unit's granules, loaded from base = (origin - 4) rounded down to
 // 8 bytes; the origin then sits at byte p in [4, 11] of the window.
@@ -180,6 +185,70 @@ __device__ inline void store_iq3s_tables(uint8_t* smem, const GridRegs<NT>& g, i
 // all 256 threads of the workgroup
 __device__ inline void stage_iq3s_tables(uint8_t* smem) {
     store_iq3s_tables<256>(smem, load_grid_regs<256>((int)threadIdx.x), (int)threadIdx.x);
+}
+
+// IQ3_XXS: the 256-entry codebook with every sign pattern applied, 4096 u32
+// at LDS byte 0: entry q + 256 * n holds grid[q] with byte j negated where bit
+// j of the sign nibble n is set.  The magnitudes are even (4 .. 62), so a
+// byte's negation is ~g + 1 (no carry leaves a byte).
+constexpr int kLdsTablesXxs = 4096 * 4;
+
+__device__ inline uint32_t neg_bytes(uint32_t g) { return ~g + 0x01010101u; }
+
+// LDS table bytes of a weight type's decoder
+__host__ __device__ constexpr int table_bytes(int qt) {
+    return qt == QT_IQ3_S ? kLdsTables : qt == QT_IQ3_XXS ? kLdsTablesXxs : 0;
+}
+
+// Codebook words a thread loads early (the first NT threads of 512 / 256
+// entries) and later expands into the LDS table; nothing for types without
+// a table.
+template <int QT, int NT>
+struct TableRegs {
+    static constexpr int ENTRIES = QT == QT_IQ3_S ? 512 : QT == QT_IQ3_XXS ? 256 : 0;
+    static constexpr int N = ENTRIES == 0 ? 0 : (NT >= ENTRIES ? 1 : ENTRIES / NT);
+    uint32_t e[N > 0 ? N : 1];
+};
+template <int QT, int NT>
+__device__ inline TableRegs<QT, NT> load_tables(int w) {
+    TableRegs<QT, NT> g;
+    constexpr int E = TableRegs<QT, NT>::ENTRIES;
+#pragma unroll
+    for (int i = 0; i < TableRegs<QT, NT>::N; ++i) {
+        const int idx = min(w + NT * i, E - 1);
+        g.e[i] = QT == QT_IQ3_S ? kIq3sGridDev.e[idx] : kIq3xxsGridDev.e[idx];
+    }
+    return g;
+}
+template <int QT, int NT>
+__device__ inline void store_tables(uint8_t* smem, const TableRegs<QT, NT>& g, int w) {
+    if constexpr (QT == QT_IQ3_S) {
+        GridRegs<NT> gr;
+#pragma unroll
+        for (int i = 0; i < GridRegs<NT>::N; ++i) gr.e[i] = g.e[i];
+        store_iq3s_tables<NT>(smem, gr, w);
+    } else if constexpr (QT == QT_IQ3_XXS) {
+        uint32_t* tab = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
+        if (NT > 256 && w >= 256) return;
+#pragma unroll
+        for (int i = 0; i < TableRegs<QT, NT>::N; ++i) {
+            const int idx = w + NT * i;
+            const uint32_t neg = neg_bytes(g.e[i]);
+#pragma unroll
+            for (int n = 0; n < 16; ++n) tab[idx + 256 * n] = __builtin_amdgcn_perm(neg, g.e[i], sign_sel((uint32_t)n));
+        }
+    }
+}
+
+// IQ4_NL / IQ4_XS: the int8 levels of four 4-bit indices (one per byte):
+// two v_perm over the 16 levels (low eight, high eight) and a per-byte
+// select on bit 3 of the index.
+__device__ inline uint32_t iq4_levels(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4nlLevelWords[1], kIq4nlLevelWords[0], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4nlLevelWords[3], kIq4nlLevelWords[2], sel);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, 0x0C0C0C0Cu | ((n >> 3) & 0x01010101u));   // 0xFF where bit 3 set
+    return (hi & m) | (lo & ~m);
 }
 
 __device__ inline uint32_t lds_u32(const uint8_t* smem, uint32_t byte_off) {
@@ -340,6 +409,59 @@ __device__ inline void q8_0_block(const uint32_t (&F)[34], uint32_t Fm1, uint32_
 }
 
 // ---------------------------------------------------------------------------
+// IQ3_XXS: element 32 ib + 8 l + 4 h + j = ls(ib) * grid[qs[8 ib + 2 l + h]][j]
+//        * (-1 if bit 4 h + j of ksigns[(aux >> 7 l) & 127]), aux = the u32
+// of sub-block ib, ls = 2 * (aux >> 28) + 1 (the 0.5 + nibble of ggml, times
+// two: the result carries a final factor 0.25).  ksigns[i] is i with an
+// even-parity bit 7.  F[0..15] qs, F[16..23] aux, Fm1 >> 16 = d.
+// ---------------------------------------------------------------------------
+__device__ inline int iq3xxs_item(const uint32_t (&F)[24], int ib, const uint8_t* smem, uint32_t (&v)[8]) {
+    const uint32_t aux = F[16 + ib];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t s7 = (aux >> (7 * l)) & 127u;
+        const uint32_t sg = s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
+        const uint32_t q2 = (F[2 * ib + (l >> 1)] >> (16 * (l & 1))) & 0xFFFFu;   // grid indices of 8 l, 8 l + 4
+        v[2 * l] = lds_u32(smem, kLdsGrid + 4u * ((q2 & 0xFFu) | ((sg & 15u) << 8)));
+        v[2 * l + 1] = lds_u32(smem, kLdsGrid + 4u * ((q2 >> 8) | ((sg >> 4) << 8)));
+    }
+    return 2 * (int)(aux >> 28) + 1;
+}
+
+// ---------------------------------------------------------------------------
+// IQ4_NL unit = 4 blocks of 18 B: d at 18 j, qs[16] at 18 j + 2; element
+// 32 j + i = d * kvalues[qs[i] & 15], element 32 j + 16 + i = d *
+// kvalues[qs[i] >> 4].  With the origin at unit byte 2, block j's qs sit at
+// F-byte 18 j (dword aligned for even j) and its d at F-byte 18 j - 2.
+// ---------------------------------------------------------------------------
+template <int J>
+__device__ inline void iq4nl_block(const uint32_t (&F)[18], uint32_t Fm1, uint32_t (&qd)[4], uint32_t& dbits) {
+    constexpr int qo = 18 * J;
+    if constexpr ((qo & 3) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qd[i] = F[qo / 4 + i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qd[i] = __builtin_amdgcn_alignbyte(F[qo / 4 + i + 1], F[qo / 4 + i], 2);
+    }
+    constexpr int dob = qo - 2;
+    if constexpr (dob < 0) dbits = Fm1 >> 16;
+    else if constexpr ((dob & 3) == 0) dbits = F[dob / 4] & 0xFFFFu;
+    else dbits = F[dob / 4] >> 16;
+}
+
+// the integer dot of 16 level bytes (four dwords of nibble pairs) with 32
+// activations: low nibbles against A[0..3], high nibbles against A[4..7]
+__device__ inline int iq4_dot32(const uint32_t* qd, const uint32_t* A) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = sdot4(iq4_levels(qd[i] & 0x0F0F0F0Fu), A[i], s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = sdot4(iq4_levels((qd[i] >> 4) & 0x0F0F0F0Fu), A[4 + i], s);
+    return s;
+}
+
+// ---------------------------------------------------------------------------
 // unit dot: contribution(s) of one unit to its row, ggml's float order per
 // block: (d_w * d_x) * isum  [Q4_K: minus (dmin_w * d_x) * msum]
 //   chunk: LDS activation bytes of the unit's 256-element chunk
@@ -405,6 +527,43 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
             isum += __mul24(q6k_scale(F, 2 * j), sa) + __mul24(q6k_scale(F, 2 * j + 1), sb);   // |sa|, |sb| < 2^18
         }
         r.c[0] = __fmul_rn(__fmul_rn(h2f(F[52]), dx[0]), (float)isum);
+    } else if constexpr (QT == QT_IQ3_XXS) {
+        // ggml: sumf += (d_w * d_x) * bsum per super-block, result 0.25 * sumf;
+        // the power-of-two factor is applied per contribution (exact)
+        int bsum = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t v[8], A[8];
+            const int ls = iq3xxs_item(F, ib, smem, v);
+            act8(chunk, ib, A);
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
+            bsum += __mul24(ls, s);              // |s| <= 32 * 62 * 127 < 2^18
+        }
+        r.c[0] = __fmul_rn(__fmul_rn(__fmul_rn(h2f(Fm1 >> 16), dx[0]), (float)bsum), 0.25f);
+    } else if constexpr (QT == QT_IQ4_XS) {
+        // ggml: per 32-element sub-block sumf += ((d_w * d_x) * (ls - 32)) * sumi
+        const float d4d8 = __fmul_rn(h2f(F[0]), dx[0]);
+        const uint32_t sh = F[0] >> 16;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t A[8];
+            act8(chunk, ib, A);
+            const int s = iq4_dot32(F + 2 + 4 * ib, A);
+            const int ls = (int)((F[1] >> (4 * ib)) & 15u) | (int)(((sh >> (2 * ib)) & 3u) << 4);
+            r.c[ib] = __fmul_rn(__fmul_rn(d4d8, (float)(ls - 32)), (float)s);
+        }
+    } else if constexpr (QT == QT_IQ4_NL) {   // four independent q8_0-paired blocks
+        uint32_t qd[4], A[8], db;
+#define SB_IQ4NL_BLOCK(J)                                                                  \
+        {                                                                                  \
+            iq4nl_block<J>(F, Fm1, qd, db);                                                \
+            act8(chunk, J, A);                                                             \
+            r.c[J] = __fmul_rn(__fmul_rn(dx[J], h2f(db)), (float)iq4_dot32(qd, A));       \
+        }
+        SB_IQ4NL_BLOCK(0) SB_IQ4NL_BLOCK(1) SB_IQ4NL_BLOCK(2) SB_IQ4NL_BLOCK(3)
+#undef SB_IQ4NL_BLOCK
     } else {   // Q8_0: four independent blocks
         uint32_t v[8], A[8], db;
 #define SB_Q8_BLOCK(J)                                                              \
@@ -461,6 +620,48 @@ __device__ inline void unit_dequant(const UnitWindow<QT>& Wn, const uint8_t* sme
                 out[32 * j + e] = __fmul_rn(__fmul_rn(d, (float)q6k_scale(F, 2 * j + (e >> 4))), (float)q);
             }
         }
+    } else if constexpr (QT == QT_IQ3_XXS) {
+        const float d = h2f(Fm1 >> 16);
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t v[8];
+            iq3xxs_item(F, ib, smem, v);
+            const float db = __fmul_rn(__fmul_rn(d, __fadd_rn(0.5f, (float)(F[16 + ib] >> 28))), 0.5f);
+            for (int e = 0; e < 32; ++e)
+                out[32 * ib + e] = __fmul_rn(db, (float)(int8_t)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu));
+        }
+    } else if constexpr (QT == QT_IQ4_XS) {
+        const float d = h2f(F[0]);
+        const uint32_t sh = F[0] >> 16;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int ls = (int)((F[1] >> (4 * ib)) & 15u) | (int)(((sh >> (2 * ib)) & 3u) << 4);
+            const float dl = __fmul_rn(d, (float)(ls - 32));
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = F[2 + 4 * ib + i];
+                const uint32_t lo = iq4_levels(q & 0x0F0F0F0Fu), hi = iq4_levels((q >> 4) & 0x0F0F0F0Fu);
+                for (int b = 0; b < 4; ++b) {
+                    out[32 * ib + 4 * i + b] = __fmul_rn(dl, (float)(int8_t)((lo >> (8 * b)) & 0xFFu));
+                    out[32 * ib + 16 + 4 * i + b] = __fmul_rn(dl, (float)(int8_t)((hi >> (8 * b)) & 0xFFu));
+                }
+            }
+        }
+    } else if constexpr (QT == QT_IQ4_NL) {
+        uint32_t qd[4], db;
+#define SB_IQ4NL_DEQ(J)                                                                              \
+        {                                                                                            \
+            iq4nl_block<J>(F, Fm1, qd, db);                                                          \
+            const float d = h2f(db);                                                                 \
+            if (32 * J < n)                                                                          \
+                for (int i = 0; i < 4; ++i) {                                                        \
+                    const uint32_t lo = iq4_levels(qd[i] & 0x0F0F0F0Fu);                             \
+                    const uint32_t hi = iq4_levels((qd[i] >> 4) & 0x0F0F0F0Fu);                      \
+                    for (int b = 0; b < 4; ++b) {                                                    \
+                        out[32 * J + 4 * i + b] = __fmul_rn(d, (float)(int8_t)((lo >> (8 * b)) & 0xFFu));      \
+                        out[32 * J + 16 + 4 * i + b] = __fmul_rn(d, (float)(int8_t)((hi >> (8 * b)) & 0xFFu)); \
+                    }                                                                                \
+                }                                                                                    \
+        }
+        SB_IQ4NL_DEQ(0) SB_IQ4NL_DEQ(1) SB_IQ4NL_DEQ(2) SB_IQ4NL_DEQ(3)
+#undef SB_IQ4NL_DEQ
     } else {
         uint32_t v[8], db;
 #define SB_Q8_DEQ(J)                                                                                       \

@@ -10,8 +10,12 @@ ARCH = "qwen4exp"
 
 
 def expert_tensors(orc, rng, layer, role, qt, E, rows, cols):
-    w = (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32)
-    raw = orc.quantize_weights(qt, w)
+    if qt == 18:          # IQ3_XXS: no encoder here; random valid blocks
+        from helpers import random_blocks
+        raw = random_blocks(rng, qt, E * rows, cols).reshape(E, rows, -1)
+    else:
+        w = (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32)
+        raw = orc.quantize_weights(qt, w)
     t = gguf.WriterTensor("blk.%d.ffn_%s_exps.weight" % (layer, role), (cols, rows, E), qt, raw)
     return t, raw
 

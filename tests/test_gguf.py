@@ -54,6 +54,20 @@ def test_rejects_what_is_not_a_gguf(tmp_path):
         gguf.GgufFile(q)
 
 
+def test_inspector_accepts_the_shipped_iq_mix(tmp_path, orc):
+    """IQ3_XXS gate/up with IQ4_NL down (the reference's shipped blocks) and
+    IQ4_XS layers are decodable; the per-expert sizes follow their blocks
+    (98 B per 256, 18 B per 32, 136 B per 256)."""
+    p = str(tmp_path / "iq.gguf")
+    rng = np.random.default_rng(3)
+    write_model(p, orc, rng, n_layers=2, E=4, D=512, F=256, layer_types=[(18, 18, 20), (23, 23, 23)])
+    prof = model.inspect_model(p)
+    assert prof.supported, prof.notes
+    assert prof.experts[(0, "gate")].per_expert_bytes == 256 * 2 * 98
+    assert prof.experts[(0, "down")].per_expert_bytes == 512 * 8 * 18
+    assert prof.experts[(1, "up")].per_expert_bytes == 256 * 2 * 136
+
+
 def test_inspector_profiles_a_supported_model(tmp_path, orc):
     p = str(tmp_path / "m.gguf")
     rng = np.random.default_rng(1)

@@ -17,7 +17,9 @@ from helpers import assert_parity, random_blocks, unfused_rounding_row
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_K, Q6_K, IQ3_S = 8, 12, 14, 21
+Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ4_XS = 8, 12, 14, 18, 20, 21, 23
+# formats whose fp32 steps follow ggml's vec_dot order exactly: results bit-identical to the oracle's
+BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS)
 DEV = torch.device("cuda:0")
 
 
@@ -33,13 +35,21 @@ def stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def expert_weights(orc, rng, qt, E, rows, cols):
+    """[E, rows, row bytes] of type qt: N(0, 0.02) quantised by the oracle's
+    encoder, or (IQ3_XXS, which has none) random valid blocks with modest scales."""
+    if qt == IQ3_XXS:
+        return random_blocks(rng, qt, E * rows, cols).reshape(E, rows, -1)
+    return orc.quantize_weights(qt, (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32))
+
+
 def make_bank(orc, rng, qts, E, D, F, n_layers=1):
     from sabah.runtime.bank import ExpertBank
     bank = ExpertBank(n_layers, E, D, F, {"gate": qts[0], "up": qts[1], "down": qts[2]}, device="cuda:0")
     raws = {}
     for l in range(n_layers):
         for role, (rows, cols), qt in (("gate", (F, D), qts[0]), ("up", (F, D), qts[1]), ("down", (D, F), qts[2])):
-            raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32))
+            raw = expert_weights(orc, rng, qt, E, rows, cols)
             bank.load(l, role, raw)
             raws[(l, role)] = raw
     return bank, raws
@@ -71,7 +81,9 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
     assert np.array_equal(y.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768)])
+@pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768),
+                                  (IQ3_XXS, 2048), (IQ3_XXS, 768), (IQ4_NL, 640), (IQ4_NL, 96), (IQ4_XS, 2048),
+                                  (IQ4_XS, 768)])
 def test_dequant_is_bit_exact(hip_rt, orc, qt, k):
     rng = np.random.default_rng(qt * 7 + k)
     raw = random_blocks(rng, qt, 37, k)
@@ -97,8 +109,11 @@ def v2(hip_rt, src, expert_stride, row_bytes, x, ids, out, rows, k, E, qt):
 
 # (Q8_0, 32768): a row (34816 bytes) larger than a workgroup's 32 KB staging
 # area, so each row is staged in two passes, with over 64 KB of LDS
+# (IQ4_NL, 96): a row of three blocks, one partial four-block unit
 CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), (Q4_K, 768, 64),
-         (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104), (Q8_0, 32768, 6)]
+         (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104), (Q8_0, 32768, 6),
+         (IQ3_XXS, 2048, 48), (IQ3_XXS, 2560, 40), (IQ4_NL, 640, 64), (IQ4_NL, 96, 24), (IQ4_XS, 2048, 48),
+         (IQ4_XS, 768, 72)]
 
 
 @pytest.mark.parametrize("qt,k,rows", CASES)
@@ -106,7 +121,7 @@ CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), 
 def test_mul_mat_id_matches_oracle(hip_rt, orc, qt, k, rows, x_rows_is_n_ids):
     rng = np.random.default_rng(qt * 1000 + k + rows + x_rows_is_n_ids)
     E, Tn, K = 7, 3, 4
-    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    raw = expert_weights(orc, rng, qt, E, rows, k)
     ids = np.stack([rng.choice(E, K, replace=False) for _ in range(Tn)]).astype(np.int32)
     ids[2, 3] = ids[2, 1]                                    # duplicate id
     x_rows = K if x_rows_is_n_ids else 1
@@ -119,7 +134,7 @@ def test_mul_mat_id_matches_oracle(hip_rt, orc, qt, k, rows, x_rows_is_n_ids):
     got = out.cpu().numpy()
     want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
     assert_parity(got, want, "qt=%d k=%d" % (qt, k))
-    if qt in (Q8_0, IQ3_S):
+    if qt in BIT_EXACT:
         # same int sums, same fp32 scale-and-accumulate order as ggml's vec_dot
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     if x_rows == 1:
@@ -252,7 +267,11 @@ def test_moe_block_single_token_q8_0(hip_rt, orc):
     assert_parity(ex.download_out(), 2 * want, "moe_block accumulate")
 
 
-@pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small"])
+# iq3xxs_iq4nl_artifact_shape: the quant mix of the reference's shipped block
+# (IQ3_XXS gate/up, IQ4_NL down; results/bench_moe_blk0_iq3s.json) at its
+# inferred shape, d_model 2560 and expert d_ff 640 (REPORT.md:345-347)
+@pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small",
+                                  "iq3xxs_iq4nl_artifact_shape", "iq4xs_small"])
 def test_moe_layer_matches_oracle(hip_rt, orc, name):
     from sabah.runtime import routing
     from sabah.runtime.bank import DenseExpert
@@ -264,6 +283,12 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
         ids, w = routing.uniform_routing(rng, Tn, E, K)
     elif name == "mixed_t32_q4k_q6k_shared":
         E, D, F, K, Tn, qts = 96, 2048, 768, 10, 32, (Q4_K, Q4_K, Q6_K)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
+    elif name == "iq3xxs_iq4nl_artifact_shape":
+        E, D, F, K, Tn, qts = 64, 2560, 640, 10, 3, (IQ3_XXS, IQ3_XXS, IQ4_NL)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "iq4xs_small":
+        E, D, F, K, Tn, qts = 32, 2048, 768, 8, 2, (IQ4_XS, IQ4_XS, IQ4_XS)
         ids, w = routing.uniform_routing(rng, Tn, E, K)
     else:
         E, D, F, K, Tn, qts = 64, 2048, 768, 10, 4, (IQ3_S, IQ3_S, IQ3_S)
