@@ -30,7 +30,8 @@
 int orc_block_elems(int qt) {
     switch (qt) {
     case ORC_Q8_0: case ORC_IQ4_NL: return 32;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: return 256;
+    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS:
+    case ORC_IQ2_S: return 256;
     }
     return 0;
 }
@@ -43,6 +44,7 @@ int orc_block_bytes(int qt) {
     case ORC_Q8_K: return 292;   /* float d, int8 qs[256], int16 bsums[16]    */
     case ORC_IQ3_S: return 110;  /* d, qs[64], qh[8], signs[32], scales[4]    */
     case ORC_IQ3_XXS: return 98; /* d, qs[64] grid indices, 8 x u32 scale/signs */
+    case ORC_IQ2_S: return 82;   /* d, qs[32], signs[32], qh[8], scales[8]       */
     case ORC_IQ4_NL: return 18;  /* d, 16 B nibbles                          */
     case ORC_IQ4_XS: return 136; /* d, scales_h u16, scales_l[4], qs[128]     */
     }
@@ -58,7 +60,8 @@ size_t orc_row_bytes(int qt, int n) {
 int orc_vec_dot_type(int qt) {
     switch (qt) {
     case ORC_Q8_0: case ORC_IQ4_NL: return ORC_Q8_0;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: return ORC_Q8_K;
+    case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: case ORC_IQ2_S:
+        return ORC_Q8_K;
     }
     return -1;
 }
@@ -260,6 +263,26 @@ int orc_dequantize_row(int qt, const uint8_t *x, float *y, int k) {
             }
         }
         return 0;
+    case ORC_IQ2_S:     /* sabah_rt.cu:2293-2318; quants.py:935-1037 */
+        /* element 32 ib + 8 l + j = db(l) * grid[qs[4 ib + l] | qh bits 2l..2l+1 << 8][j]
+         * * (-1 if bit j of signs[4 ib + l]); db = d * (0.5 + nibble) * 0.25, the low
+         * nibble of scales[ib] for l < 2, the high one for l >= 2 */
+        for (int b = 0; b < k / 256; ++b, x += 82) {
+            const float d = ld_f16(x);
+            const uint8_t *qs = x + 2, *signs = x + 34, *qh = x + 66, *sc = x + 74;
+            for (int ib = 0; ib < 8; ++ib) {
+                const float db0 = d * (0.5f + (float)(sc[ib] & 0xF)) * 0.25f;
+                const float db1 = d * (0.5f + (float)(sc[ib] >> 4)) * 0.25f;
+                for (int l = 0; l < 4; ++l) {
+                    const float dl = l < 2 ? db0 : db1;
+                    const uint64_t g = orc_iq2s_grid[qs[4 * ib + l] | ((qh[ib] << (8 - 2 * l)) & 0x300)];
+                    const uint8_t sg = signs[4 * ib + l];
+                    for (int j = 0; j < 8; ++j)
+                        *y++ = dl * (float)((g >> (8 * j)) & 0xFF) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                }
+            }
+        }
+        return 0;
     case ORC_IQ3_XXS:   /* sabah_rt.cu:2320-2344; quants.py:1039-1075 */
         for (int b = 0; b < k / 256; ++b, x += 98) {
             const float d = ld_f16(x);
@@ -452,6 +475,33 @@ static float dot_iq3_xxs(const uint8_t *w, const uint8_t *a, int k) {
     return 0.25f * sumf;
 }
 
+/* ggml_vec_dot_iq2_s_q8_K (generic): bsum = sum_ib32 (ls1 * sumi1 + ls2 * sumi2),
+ * ls = 2 * nibble + 1 for the sub-block's first / second 16 elements, sumi =
+ * sum(grid * sign * q8); sumf += (dw * d8) * bsum per super-block; the result
+ * is 0.125f * sumf (db = d * (0.5 + nibble) * 0.25 = d * ls / 8). */
+static float dot_iq2_s(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 256; ++b, w += 82, a += 292) {
+        const uint8_t *qs = w + 2, *signs = w + 34, *qh = w + 66, *sc = w + 74;
+        const int8_t *q8 = q8K_qs(a);
+        int bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int ls1 = 1 + 2 * (sc[ib] & 0xF), ls2 = 1 + 2 * (sc[ib] >> 4);
+            int sumi[2] = {0, 0};
+            for (int l = 0; l < 4; ++l) {
+                const uint64_t g = orc_iq2s_grid[qs[4 * ib + l] | ((qh[ib] << (8 - 2 * l)) & 0x300)];
+                for (int j = 0; j < 8; ++j)
+                    sumi[l >> 1] += (int)q8[32 * ib + 8 * l + j] * (int)((g >> (8 * j)) & 0xFF) *
+                                    ((signs[4 * ib + l] >> j) & 1 ? -1 : 1);
+            }
+            bsum += ls1 * sumi[0] + ls2 * sumi[1];
+        }
+        const float d = ld_f16(w) * q8K_d(a);
+        sumf += d * (float)bsum;
+    }
+    return 0.125f * sumf;
+}
+
 /* ggml_vec_dot_iq4_nl_q8_0 (generic): per 32-block sumf += (d8*dw) * sum(kv[q]*q8). */
 static float dot_iq4_nl(const uint8_t *w, const uint8_t *a, int k) {
     float sumf = 0.0f;
@@ -498,6 +548,7 @@ float orc_vec_dot(int qt, const uint8_t *w, const uint8_t *a, int k) {
     case ORC_Q6_K: return dot_q6_K(w, a, k);
     case ORC_IQ3_S: return dot_iq3_s(w, a, k);
     case ORC_IQ3_XXS: return dot_iq3_xxs(w, a, k);
+    case ORC_IQ2_S: return dot_iq2_s(w, a, k);
     case ORC_IQ4_NL: return dot_iq4_nl(w, a, k);
     case ORC_IQ4_XS: return dot_iq4_xs(w, a, k);
     }

@@ -1,9 +1,9 @@
 /*
  * ORACLE - test infrastructure only.
  *
- * A plain-C restatement of ggml's CPU MUL_MAT_ID path for the seven expert
- * formats (Q8_0, Q4_K, Q6_K, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS), used as the
- * checker for the HIP kernels.
+ * A plain-C restatement of ggml's CPU MUL_MAT_ID path for the eight expert
+ * formats (Q8_0, Q4_K, Q6_K, IQ3_S, IQ3_XXS, IQ2_S, IQ4_NL, IQ4_XS), used as
+ * the checker for the HIP kernels.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
  * it.  The product library never links or calls it.
  *
@@ -27,18 +27,19 @@
  *     sabah_rt.cu:2233-2423 and quants.py:412-435, 509-556, 586-606, 1091-1159.
  *   the IQ3_S codebook: equal to both reference copies (sabah_iq_tables.h:
  *     638-704 and quants.py:1094-1127 grid_hex) and to its recorded sha256.
- *   the IQ3_XXS codebook, the IQ2_XXS/IQ3_XXS sign bytes and the IQ4 levels:
+ *   the IQ3_XXS and IQ2_S codebooks, the IQ2_XXS/IQ3_XXS sign bytes and the IQ4 levels:
  *     generated from quants.py text (oracle/gen_iq_tables.py), equal to the
  *     reference's second copy (sabah_iq_tables.h) and to recorded sha256
  *     values; closed forms (ksigns = index with an even-parity bit 7, levels
  *     sorted, grid bytes among the eight magnitudes).
- *   IQ3_XXS / IQ4_NL / IQ4_XS dequantisation: known-answer blocks (grid row,
- *     sign bytes, 4-bit scale; level bytes and d; 6-bit sub-block scales)
- *     from sabah_rt.cu:2320-2344, 2380-2409 and quants.py:1039-1075,
- *     1364-1411.
+ *   IQ3_XXS / IQ2_S / IQ4_NL / IQ4_XS dequantisation: known-answer blocks
+ *     (grid row, sign bytes, 4-bit scale; grid index high bits from qh and
+ *     the two scale nibbles; level bytes and d; 6-bit sub-block scales) from
+ *     sabah_rt.cu:2293-2344, 2380-2409 and quants.py:935-1075, 1364-1411.
  *   orc_vec_dot: the float64 dot of the decoded operands (all formats); the
- *     IQ3_S integer block sums exactly; IQ3_XXS exactly a quarter of its
- *     integer sum; the Q4_K min term through bsums.
+ *     IQ3_S integer block sums exactly; IQ3_XXS exactly a quarter and IQ2_S
+ *     exactly an eighth of their integer sums; the Q4_K min term through
+ *     bsums.
  *   orc_mul_mat_id / orc_moe_layer: brute-force loops; bad ids and geometry
  *     rejected; a layer is the composition of its MUL_MAT_IDs; the shared
  *     expert is added last; duplicate ids of the reference's recorded routing
@@ -68,6 +69,7 @@ enum {
     ORC_Q6_K = 14,
     ORC_Q8_K = 15,
     ORC_IQ3_XXS = 18,
+    ORC_IQ2_S = 22,
     ORC_IQ4_NL = 20,
     ORC_IQ3_S = 21,
     ORC_IQ4_XS = 23,

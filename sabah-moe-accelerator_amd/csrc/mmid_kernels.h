@@ -133,7 +133,8 @@ constexpr int kMaxTiles = 64;
 
 // 16-byte loads per lane per pass
 __host__ __device__ constexpr int stage_iters(int qt) {
-    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7 : qt == QT_IQ4_NL ? 5 : 9;
+    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7 : qt == QT_IQ4_NL ? 5
+         : qt == QT_IQ2_S ? 6 : 9;
 }
 // the same load count spread over nt threads
 __host__ __device__ constexpr int stage_iters_nt(int qt, int nt) { return (stage_iters(qt) * kThreads + nt - 1) / nt; }

@@ -2,8 +2,8 @@
 //
 // Type codes are ggml's enum values so traces stay comparable with llama.cpp
 // (sabah/runtime/rt.py:20-23; Q6_K = 14 and Q8_K = 15 are the same enum).
-// Geometry follows sabah_rt.cu:2155-2191 for Q8_0/Q4_K/IQ3_S/IQ3_XXS/IQ4_NL/
-// IQ4_XS and gguf-py quants.py:586-606 for Q6_K (ql[128] qh[64] int8
+// Geometry follows sabah_rt.cu:2155-2191 for Q8_0/Q4_K/IQ3_S/IQ3_XXS/IQ2_S/
+// IQ4_NL/IQ4_XS and gguf-py quants.py:586-606 for Q6_K (ql[128] qh[64] int8
 // scales[16] fp16 d).
 #pragma once
 #include <hip/hip_fp16.h>
@@ -25,13 +25,14 @@ enum : int {
     QT_IQ3_XXS = 18,
     QT_IQ4_NL = 20,
     QT_IQ3_S = 21,
+    QT_IQ2_S = 22,
     QT_IQ4_XS = 23,
 };
 
 __host__ __device__ constexpr int block_elems(int qt) {
     return (qt == QT_Q8_0 || qt == QT_IQ4_NL) ? 32
          : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_Q8_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS ||
-            qt == QT_IQ4_XS) ? 256 : 0;
+            qt == QT_IQ4_XS || qt == QT_IQ2_S) ? 256 : 0;
 }
 
 __host__ __device__ constexpr int block_bytes(int qt) {
@@ -42,6 +43,7 @@ __host__ __device__ constexpr int block_bytes(int qt) {
          : qt == QT_IQ3_S ? 110
          : qt == QT_IQ3_XXS ? 98      // fp16 d, qs[64] grid indices, 8 x u32 (4 x 7-bit signs, 4-bit scale)
          : qt == QT_IQ4_NL ? 18       // fp16 d, 16 bytes of level nibbles
+         : qt == QT_IQ2_S ? 82        // fp16 d, qs[32], signs[32], qh[8], scales[8]
          : qt == QT_IQ4_XS ? 136 : 0; // fp16 d, u16 scales_h, scales_l[4], qs[128]
 }
 
@@ -53,15 +55,16 @@ __host__ __device__ inline size_t row_bytes(int qt, int n) {
 
 // The activation format ggml's CPU pairs with each weight type (its
 // vec_dot_type): q8_0 for Q8_0 and IQ4_NL; q8_K for the K-quants, IQ3_S,
-// IQ3_XXS and IQ4_XS.
+// IQ3_XXS, IQ2_S and IQ4_XS.
 __host__ __device__ constexpr int act_type(int qt) {
     return (qt == QT_Q8_0 || qt == QT_IQ4_NL) ? QT_Q8_0
-         : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS || qt == QT_IQ4_XS) ? QT_Q8_K : -1;
+         : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS || qt == QT_IQ4_XS ||
+            qt == QT_IQ2_S) ? QT_Q8_K : -1;
 }
 
 __host__ __device__ constexpr bool supported_weight_type(int qt) {
     return qt == QT_Q8_0 || qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS || qt == QT_IQ4_NL ||
-           qt == QT_IQ4_XS;
+           qt == QT_IQ4_XS || qt == QT_IQ2_S;
 }
 
 // Expanded IQ3_S codebook entry: byte j = 2*level_j + 1.
@@ -88,6 +91,17 @@ __host__ __device__ constexpr Iq3xxsGrid make_iq3xxs_grid() {
 }
 // the IQ3_XXS codebook (magnitudes 4 .. 62, one per byte) as device constant memory
 __constant__ Iq3xxsGrid kIq3xxsGridDev = make_iq3xxs_grid();
+
+struct Iq2sGrid {
+    uint32_t w[2048];
+};
+__host__ __device__ constexpr Iq2sGrid make_iq2s_grid() {
+    Iq2sGrid g{};
+    for (int i = 0; i < 2048; ++i) g.w[i] = kIq2sGridWords[i];
+    return g;
+}
+// the IQ2_S codebook (two dwords per entry, magnitudes 8 / 25 / 43) as device constant memory
+__constant__ Iq2sGrid kIq2sGridDev = make_iq2s_grid();
 
 // ---------------------------------------------------------------------------
 // Device-side activation row layout (LDS scratch, never an ABI):

@@ -218,6 +218,7 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
     case QT_IQ3_XXS: return launch_mmid<QT_IQ3_XXS>(a, st);
     case QT_IQ4_NL: return launch_mmid<QT_IQ4_NL>(a, st);
     case QT_IQ4_XS: return launch_mmid<QT_IQ4_XS>(a, st);
+    case QT_IQ2_S: return launch_mmid<QT_IQ2_S>(a, st);
     }
     return hipErrorInvalidValue;
 }
@@ -249,6 +250,7 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
     case QT_IQ3_XXS: return launch_gate_up<QT_IQ3_XXS>(a, n_tokens, st);
     case QT_IQ4_NL: return launch_gate_up<QT_IQ4_NL>(a, n_tokens, st);
     case QT_IQ4_XS: return launch_gate_up<QT_IQ4_XS>(a, n_tokens, st);
+    case QT_IQ2_S: return launch_gate_up<QT_IQ2_S>(a, n_tokens, st);
     }
     return hipErrorInvalidValue;
 }
@@ -273,6 +275,7 @@ hipError_t dispatch_down(int qt, const DownArgs& a, int n_tokens, hipStream_t st
     case QT_IQ3_XXS: return launch_down<QT_IQ3_XXS>(a, n_tokens, st);
     case QT_IQ4_NL: return launch_down<QT_IQ4_NL>(a, n_tokens, st);
     case QT_IQ4_XS: return launch_down<QT_IQ4_XS>(a, n_tokens, st);
+    case QT_IQ2_S: return launch_down<QT_IQ2_S>(a, n_tokens, st);
     }
     return hipErrorInvalidValue;
 }
@@ -559,6 +562,7 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
     case QT_IQ3_XXS: hipLaunchKernelGGL(k_dequant<QT_IQ3_XXS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ4_NL: hipLaunchKernelGGL(k_dequant<QT_IQ4_NL>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ4_XS: hipLaunchKernelGGL(k_dequant<QT_IQ4_XS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_IQ2_S: hipLaunchKernelGGL(k_dequant<QT_IQ2_S>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     }
     if (!ck(hipGetLastError(), "dequant launch")) return -1;
     return ck(hipStreamSynchronize(g_stream), "dequant sync") ? 0 : -1;

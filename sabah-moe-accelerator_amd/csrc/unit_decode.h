@@ -1,7 +1,7 @@
 // Register-resident decoding of quantised weights, one "unit" per lane.
 //
 // A unit is one 256-element super-block (Q4_K 144 B, Q6_K 210 B, IQ3_S 110 B,
-// IQ3_XXS 98 B, IQ4_XS 136 B) or four 32-element blocks (Q8_0 136 B, IQ4_NL
+// IQ3_XXS 98 B, IQ2_S 82 B, IQ4_XS 136 B) or four 32-element blocks (Q8_0 136 B, IQ4_NL
 // 72 B).  Each lane loads its unit straight
 // from HBM into VGPRs with 8-byte loads that cover exactly the unit's 8-byte
 // granules (so a load never touches a page the unit does not), then
@@ -10,12 +10,12 @@
 // q8 activations held in LDS.
 //
 // Field origin: all fields used in the inner loops start at the same residue
-// mod 4 inside the block (IQ3_S, IQ3_XXS: byte 2; Q8_0 and IQ4_NL even
+// mod 4 inside the block (IQ3_S, IQ3_XXS, IQ2_S: byte 2; Q8_0 and IQ4_NL even
 // blocks: byte 2; Q4_K, Q6_K and IQ4_XS: byte 0).  F[i] is the dword at (unit start + ORG + 4 i); Fm1 is the
 // dword before it (IQ3_S reads its fp16 d there).
 //
 // Block layouts: sabah_rt.cu:2462-2485 (Q4_K), 2537-2545 (Q8_0), 2618-2647
-// (IQ3_S), 2320-2344 (IQ3_XXS), 2380-2409 (IQ4_NL, IQ4_XS); gguf-py
+// (IQ3_S), 2293-2318 (IQ2_S), 2320-2344 (IQ3_XXS), 2380-2409 (IQ4_NL, IQ4_XS); gguf-py
 // quants.py:586-606 (Q6_K: ql[128] qh[64] int8 sc[16] d).
 #pragma once
 #include "quant_formats.h"
@@ -47,6 +47,7 @@ template <> struct UnitFmt<QT_Q8_0> { static constexpr int BYTES = 136, ELEMS = 
 template <> struct UnitFmt<QT_IQ3_XXS> { static constexpr int BYTES = 98, ELEMS = 256, ORG = 2, NF = 24, CONTRIB = 1; };
 template <> struct UnitFmt<QT_IQ4_XS> { static constexpr int BYTES = 136, ELEMS = 256, ORG = 0, NF = 34, CONTRIB = 8; };
 template <> struct UnitFmt<QT_IQ4_NL> { static constexpr int BYTES = 72, ELEMS = 128, ORG = 2, NF = 18, CONTRIB = 4; };
+template <> struct UnitFmt<QT_IQ2_S> { static constexpr int BYTES = 82, ELEMS = 256, ORG = 2, NF = 20, CONTRIB = 1; };
 
 // Window: the unit's granules, loaded from base = (origin - 4) rounded down to
 // 8 bytes; the origin then sits at byte p in [4, 11] of the window.
@@ -195,9 +196,13 @@ constexpr int kLdsTablesXxs = 4096 * 4;
 
 __device__ inline uint32_t neg_bytes(uint32_t g) { return ~g + 0x01010101u; }
 
+// IQ2_S: the 1024-entry codebook unsigned, two dwords per entry (8 KB at LDS
+// byte 0): one 8-byte read per eight weights, the signs applied in VALU.
+constexpr int kLdsTablesIq2s = 2048 * 4;
+
 // LDS table bytes of a weight type's decoder
 __host__ __device__ constexpr int table_bytes(int qt) {
-    return qt == QT_IQ3_S ? kLdsTables : qt == QT_IQ3_XXS ? kLdsTablesXxs : 0;
+    return qt == QT_IQ3_S ? kLdsTables : qt == QT_IQ3_XXS ? kLdsTablesXxs : qt == QT_IQ2_S ? kLdsTablesIq2s : 0;
 }
 
 // Codebook words a thread loads early (the first NT threads of 512 / 256
@@ -205,7 +210,7 @@ __host__ __device__ constexpr int table_bytes(int qt) {
 // a table.
 template <int QT, int NT>
 struct TableRegs {
-    static constexpr int ENTRIES = QT == QT_IQ3_S ? 512 : QT == QT_IQ3_XXS ? 256 : 0;
+    static constexpr int ENTRIES = QT == QT_IQ3_S ? 512 : QT == QT_IQ3_XXS ? 256 : QT == QT_IQ2_S ? 2048 : 0;   // words
     static constexpr int N = ENTRIES == 0 ? 0 : (NT >= ENTRIES ? 1 : ENTRIES / NT);
     uint32_t e[N > 0 ? N : 1];
 };
@@ -216,7 +221,7 @@ __device__ inline TableRegs<QT, NT> load_tables(int w) {
 #pragma unroll
     for (int i = 0; i < TableRegs<QT, NT>::N; ++i) {
         const int idx = min(w + NT * i, E - 1);
-        g.e[i] = QT == QT_IQ3_S ? kIq3sGridDev.e[idx] : kIq3xxsGridDev.e[idx];
+        g.e[i] = QT == QT_IQ3_S ? kIq3sGridDev.e[idx] : QT == QT_IQ3_XXS ? kIq3xxsGridDev.e[idx] : kIq2sGridDev.w[idx];
     }
     return g;
 }
@@ -237,6 +242,11 @@ __device__ inline void store_tables(uint8_t* smem, const TableRegs<QT, NT>& g, i
 #pragma unroll
             for (int n = 0; n < 16; ++n) tab[idx + 256 * n] = __builtin_amdgcn_perm(neg, g.e[i], sign_sel((uint32_t)n));
         }
+    } else if constexpr (QT == QT_IQ2_S) {
+        uint32_t* tab = reinterpret_cast<uint32_t*>(smem + kLdsGrid);
+        if (NT > 2048 && w >= 2048) return;
+#pragma unroll
+        for (int i = 0; i < TableRegs<QT, NT>::N; ++i) tab[w + NT * i] = g.e[i];
     }
 }
 
@@ -429,6 +439,24 @@ __device__ inline int iq3xxs_item(const uint32_t (&F)[24], int ib, const uint8_t
 }
 
 // ---------------------------------------------------------------------------
+// IQ2_S: element 32 ib + 8 l + j = db(l) * grid[qs[4 ib + l] | qh bits 2l,
+// 2l+1 << 8][j] * (-1 if bit j of signs[4 ib + l]); ls = 2 * nibble + 1, the
+// low nibble of scales[ib] for l < 2, the high one after (ggml's result
+// carries a final factor 0.125).  F[0..7] qs, F[8..15] signs, F[16..17] qh,
+// F[18..19] scales, Fm1 >> 16 = d.  The magnitudes (8, 25, 43) are negated
+// byte-wise as ~g + 1.
+// ---------------------------------------------------------------------------
+__device__ inline void iq2s_group(const uint32_t (&F)[20], int ib, int l, const uint8_t* smem, uint32_t& lo,
+                                  uint32_t& hi) {
+    const uint32_t qh = byte_of(F + 16, ib);
+    const uint32_t gi = byte_of(F, 4 * ib + l) | (((qh >> (2 * l)) & 3u) << 8);
+    const uint2 g = *reinterpret_cast<const uint2*>(smem + kLdsGrid + 8u * gi);
+    const uint32_t sg = byte_of(F + 8, 4 * ib + l);
+    lo = __builtin_amdgcn_perm(neg_bytes(g.x), g.x, sign_sel(sg & 15u));
+    hi = __builtin_amdgcn_perm(neg_bytes(g.y), g.y, sign_sel(sg >> 4));
+}
+
+// ---------------------------------------------------------------------------
 // IQ4_NL unit = 4 blocks of 18 B: d at 18 j, qs[16] at 18 j + 2; element
 // 32 j + i = d * kvalues[qs[i] & 15], element 32 j + 16 + i = d *
 // kvalues[qs[i] >> 4].  With the origin at unit byte 2, block j's qs sit at
@@ -542,6 +570,25 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
             bsum += __mul24(ls, s);              // |s| <= 32 * 62 * 127 < 2^18
         }
         r.c[0] = __fmul_rn(__fmul_rn(__fmul_rn(h2f(Fm1 >> 16), dx[0]), (float)bsum), 0.25f);
+    } else if constexpr (QT == QT_IQ2_S) {
+        // ggml: sumf += (d_w * d_x) * bsum per super-block, result 0.125 * sumf;
+        // the power-of-two factor is applied per contribution (exact)
+        int bsum = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t A[8];
+            act8(chunk, ib, A);
+            int s[2] = {0, 0};
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                uint32_t lo, hi;
+                iq2s_group(F, ib, l, smem, lo, hi);
+                s[l >> 1] = sdot4(hi, A[2 * l + 1], sdot4(lo, A[2 * l], s[l >> 1]));
+            }
+            const uint32_t sc = byte_of(F + 18, ib);
+            bsum += __mul24(2 * (int)(sc & 15u) + 1, s[0]) + __mul24(2 * (int)(sc >> 4) + 1, s[1]);   // |s| < 2^15
+        }
+        r.c[0] = __fmul_rn(__fmul_rn(__fmul_rn(h2f(Fm1 >> 16), dx[0]), (float)bsum), 0.125f);
     } else if constexpr (QT == QT_IQ4_XS) {
         // ggml: per 32-element sub-block sumf += ((d_w * d_x) * (ls - 32)) * sumi
         const float d4d8 = __fmul_rn(h2f(F[0]), dx[0]);
@@ -628,6 +675,20 @@ __device__ inline void unit_dequant(const UnitWindow<QT>& Wn, const uint8_t* sme
             const float db = __fmul_rn(__fmul_rn(d, __fadd_rn(0.5f, (float)(F[16 + ib] >> 28))), 0.5f);
             for (int e = 0; e < 32; ++e)
                 out[32 * ib + e] = __fmul_rn(db, (float)(int8_t)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu));
+        }
+    } else if constexpr (QT == QT_IQ2_S) {
+        const float d = h2f(Fm1 >> 16);
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t sc = byte_of(F + 18, ib);
+            const float db0 = __fmul_rn(__fmul_rn(d, __fadd_rn(0.5f, (float)(sc & 15u))), 0.25f);
+            const float db1 = __fmul_rn(__fmul_rn(d, __fadd_rn(0.5f, (float)(sc >> 4))), 0.25f);
+            for (int l = 0; l < 4; ++l) {
+                uint32_t v[2];
+                iq2s_group(F, ib, l, smem, v[0], v[1]);
+                const float dl = l < 2 ? db0 : db1;
+                for (int e = 0; e < 8; ++e)
+                    out[32 * ib + 8 * l + e] = __fmul_rn(dl, (float)(int8_t)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu));
+            }
         }
     } else if constexpr (QT == QT_IQ4_XS) {
         const float d = h2f(F[0]);

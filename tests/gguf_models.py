@@ -10,7 +10,7 @@ ARCH = "qwen4exp"
 
 
 def expert_tensors(orc, rng, layer, role, qt, E, rows, cols):
-    if qt == 18:          # IQ3_XXS: no encoder here; random valid blocks
+    if qt in (18, 22):    # IQ3_XXS, IQ2_S: no encoder here; random valid blocks
         from helpers import random_blocks
         raw = random_blocks(rng, qt, E * rows, cols).reshape(E, rows, -1)
     else:

@@ -85,7 +85,7 @@ def random_blocks(rng, qt: int, n_rows: int, k: int) -> np.ndarray:
     def scales(n):
         return (rng.uniform(0.25, 2.0, size=n) * rng.choice([-1, 1], size=n) * 1e-2).astype(np.float16)
 
-    if qt in (8, 18, 20, 21, 23):           # Q8_0, IQ3_XXS, IQ4_NL, IQ3_S, IQ4_XS: fp16 d at 0
+    if qt in (8, 18, 20, 21, 22, 23):       # Q8_0, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS: fp16 d at 0
         raw[:, :, 0:2] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
     elif qt == 12:                          # Q4_K: d, dmin at 0, 2 (non-negative in real data)
         raw[:, :, 0:2] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)

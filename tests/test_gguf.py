@@ -55,14 +55,15 @@ def test_rejects_what_is_not_a_gguf(tmp_path):
 
 
 def test_inspector_accepts_the_shipped_iq_mix(tmp_path, orc):
-    """IQ3_XXS gate/up with IQ4_NL down (the reference's shipped blocks) and
-    IQ4_XS layers are decodable; the per-expert sizes follow their blocks
-    (98 B per 256, 18 B per 32, 136 B per 256)."""
+    """IQ3_XXS gate/up with IQ4_NL down (the reference's shipped blocks), IQ4_XS
+    and IQ2_S layers are decodable; the per-expert sizes follow their blocks
+    (98 B per 256, 18 B per 32, 136 B per 256, 82 B per 256)."""
     p = str(tmp_path / "iq.gguf")
     rng = np.random.default_rng(3)
-    write_model(p, orc, rng, n_layers=2, E=4, D=512, F=256, layer_types=[(18, 18, 20), (23, 23, 23)])
+    write_model(p, orc, rng, n_layers=3, E=4, D=512, F=256, layer_types=[(18, 18, 20), (23, 23, 23), (22, 22, 21)])
     prof = model.inspect_model(p)
     assert prof.supported, prof.notes
+    assert prof.experts[(2, "gate")].per_expert_bytes == 256 * 2 * 82
     assert prof.experts[(0, "gate")].per_expert_bytes == 256 * 2 * 98
     assert prof.experts[(0, "down")].per_expert_bytes == 512 * 8 * 18
     assert prof.experts[(1, "up")].per_expert_bytes == 256 * 2 * 136
@@ -120,13 +121,12 @@ def test_inspector_refuses(tmp_path, orc, case, needle):
         kv = [("general.architecture", gguf.STR, ARCH), ("%s.block_count" % ARCH, gguf.U32, 1),
               ("%s.embedding_length" % ARCH, gguf.U32, D), ("%s.expert_count" % ARCH, gguf.U32, E),
               ("%s.expert_used_count" % ARCH, gguf.U32, 2), ("%s.expert_feed_forward_length" % ARCH, gguf.U32, F)]
-        rb = {21: 110, 22: 82}
         def t(role, qt, shape):
             n = gguf.tensor_bytes(qt, shape)
             return gguf.WriterTensor("blk.0.ffn_%s_exps.weight" % role, shape, qt, np.zeros(n, np.uint8))
         ts = [t("gate", 21, (D, F, E)), t("up", 21, (D, F, E))]
         if case == "type":
-            ts.append(t("down", 22, (F, D, E)))             # IQ2_S: a GGUF type the kernels do not decode
+            ts.append(t("down", 42, (F, D, E)))             # Q2_0: a GGUF type the kernels do not decode
         elif case == "axis":
             ts.append(t("down", 21, (F, E, D)))             # experts not the slowest axis
         gguf.write_gguf(p, kv, ts)

@@ -17,9 +17,9 @@ from helpers import assert_parity, random_blocks, unfused_rounding_row
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ4_XS = 8, 12, 14, 18, 20, 21, 23
+Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS = 8, 12, 14, 18, 20, 21, 22, 23
 # formats whose fp32 steps follow ggml's vec_dot order exactly: results bit-identical to the oracle's
-BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS)
+BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S)
 DEV = torch.device("cuda:0")
 
 
@@ -37,8 +37,8 @@ def stream():
 
 def expert_weights(orc, rng, qt, E, rows, cols):
     """[E, rows, row bytes] of type qt: N(0, 0.02) quantised by the oracle's
-    encoder, or (IQ3_XXS, which has none) random valid blocks with modest scales."""
-    if qt == IQ3_XXS:
+    encoder, or (IQ3_XXS and IQ2_S, which have none) random valid blocks with modest scales."""
+    if qt in (IQ3_XXS, IQ2_S):
         return random_blocks(rng, qt, E * rows, cols).reshape(E, rows, -1)
     return orc.quantize_weights(qt, (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32))
 
@@ -83,7 +83,7 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
 
 @pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768),
                                   (IQ3_XXS, 2048), (IQ3_XXS, 768), (IQ4_NL, 640), (IQ4_NL, 96), (IQ4_XS, 2048),
-                                  (IQ4_XS, 768)])
+                                  (IQ4_XS, 768), (IQ2_S, 2048), (IQ2_S, 768)])
 def test_dequant_is_bit_exact(hip_rt, orc, qt, k):
     rng = np.random.default_rng(qt * 7 + k)
     raw = random_blocks(rng, qt, 37, k)
@@ -113,7 +113,7 @@ def v2(hip_rt, src, expert_stride, row_bytes, x, ids, out, rows, k, E, qt):
 CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), (Q4_K, 768, 64),
          (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104), (Q8_0, 32768, 6),
          (IQ3_XXS, 2048, 48), (IQ3_XXS, 2560, 40), (IQ4_NL, 640, 64), (IQ4_NL, 96, 24), (IQ4_XS, 2048, 48),
-         (IQ4_XS, 768, 72)]
+         (IQ4_XS, 768, 72), (IQ2_S, 2048, 48), (IQ2_S, 768, 80)]
 
 
 @pytest.mark.parametrize("qt,k,rows", CASES)
@@ -271,7 +271,7 @@ def test_moe_block_single_token_q8_0(hip_rt, orc):
 # (IQ3_XXS gate/up, IQ4_NL down; results/bench_moe_blk0_iq3s.json) at its
 # inferred shape, d_model 2560 and expert d_ff 640 (REPORT.md:345-347)
 @pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small",
-                                  "iq3xxs_iq4nl_artifact_shape", "iq4xs_small"])
+                                  "iq3xxs_iq4nl_artifact_shape", "iq4xs_small", "iq2s_iq3s_mix"])
 def test_moe_layer_matches_oracle(hip_rt, orc, name):
     from sabah.runtime import routing
     from sabah.runtime.bank import DenseExpert
@@ -286,6 +286,9 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
         ids, w = routing.uniform_routing(rng, Tn, E, K)
     elif name == "iq3xxs_iq4nl_artifact_shape":
         E, D, F, K, Tn, qts = 64, 2560, 640, 10, 3, (IQ3_XXS, IQ3_XXS, IQ4_NL)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "iq2s_iq3s_mix":
+        E, D, F, K, Tn, qts = 48, 2560, 768, 10, 2, (IQ2_S, IQ2_S, IQ3_S)
         ids, w = routing.zipf_routing(rng, Tn, E, K)
     elif name == "iq4xs_small":
         E, D, F, K, Tn, qts = 32, 2048, 768, 8, 2, (IQ4_XS, IQ4_XS, IQ4_XS)

@@ -431,7 +431,57 @@ def test_iq3_xxs_known_answer_grid_signs_and_scale(orc):
                     assert y[e] == np.float32(db * ((g >> (8 * j)) & 0xFF) * sign), (ib, l, h, j)
 
 
-@pytest.mark.parametrize("qt,k", [(IQ3_XXS, 512), (IQ4_NL, 256), (IQ4_XS, 512)])
+IQ2_S = 22
+
+
+def iq2s_block(qs, signs, qh, scales, d=1.0):
+    return np.frombuffer(f16(d) + bytes(qs) + bytes(signs) + bytes(qh) + bytes(scales), np.uint8)
+
+
+def test_iq2_s_known_answer_grid_qh_signs_and_scales(orc):
+    """element 32 ib + 8 l + j = db * grid[qs[4 ib + l] | qh bits 2l, 2l+1 << 8][j] * sign bit j;
+    db = d * (0.5 + nibble) * 0.25 with the low nibble of scales[ib] for l < 2, the high one after
+    (sabah_rt.cu:2293-2318; quants.py:1007-1037)."""
+    from helpers import oracle_table
+    grid = oracle_table("orc_iq2s_grid")
+    qs = [(37 * i + 5) & 255 for i in range(32)]
+    signs = [(29 * i + 3) & 255 for i in range(32)]
+    qh = [(0x1B * (i + 1)) & 255 for i in range(8)]         # every 2-bit pattern occurs
+    scales = [(i | ((15 - 2 * i) << 4)) & 255 for i in range(8)]
+    y = orc.dequantize(IQ2_S, iq2s_block(qs, signs, qh, scales), 256)
+    for ib in range(8):
+        for l in range(4):
+            gi = qs[4 * ib + l] | (((qh[ib] >> (2 * l)) & 3) << 8)
+            nib = (scales[ib] & 15) if l < 2 else (scales[ib] >> 4)
+            db = (0.5 + nib) * 0.25
+            for j in range(8):
+                sign = -1.0 if (signs[4 * ib + l] >> j) & 1 else 1.0
+                e = 32 * ib + 8 * l + j
+                assert y[e] == np.float32(db * ((grid[gi] >> (8 * j)) & 0xFF) * sign), (ib, l, j)
+
+
+def test_iq2_s_dot_is_an_eighth_of_the_exact_integer_sum(orc):
+    from helpers import oracle_table
+    grid = oracle_table("orc_iq2s_grid")
+    rng = np.random.default_rng(14)
+    qs, signs = rng.integers(0, 256, 32), rng.integers(0, 256, 32)
+    qh, scales = rng.integers(0, 256, 8), rng.integers(0, 256, 8)
+    blk = iq2s_block(qs.astype(np.uint8), signs.astype(np.uint8), qh.astype(np.uint8), scales.astype(np.uint8))
+    xi = rng.integers(-126, 127, 256).astype(np.float32)
+    xi[7] = -127.0                                     # activation scale d = 1 exactly
+    a = orc.quantize_q8_K(xi)
+    total = 0
+    for ib in range(8):
+        for l in range(4):
+            gi = int(qs[4 * ib + l]) | (((int(qh[ib]) >> (2 * l)) & 3) << 8)
+            ls = 2 * ((int(scales[ib]) & 15) if l < 2 else (int(scales[ib]) >> 4)) + 1
+            for j in range(8):
+                s = -1 if (int(signs[4 * ib + l]) >> j) & 1 else 1
+                total += ls * ((grid[gi] >> (8 * j)) & 0xFF) * s * int(xi[32 * ib + 8 * l + j])
+    assert orc.vec_dot(IQ2_S, blk, a, 256) == np.float32(0.125) * np.float32(total)
+
+
+@pytest.mark.parametrize("qt,k", [(IQ3_XXS, 512), (IQ4_NL, 256), (IQ4_XS, 512), (IQ2_S, 512)])
 def test_new_iq_dots_match_float64_of_decoded_operands(orc, qt, k):
     rng = np.random.default_rng(qt + 100)
     raw = random_blocks(rng, qt, 8, k)

@@ -90,3 +90,33 @@ def test_product_tables_are_the_oracle_tables():
     words = [int(x, 16) for x in re.findall(r"0x([0-9a-fA-F]{8})", body)]
     kv = [((words[i // 4] >> (8 * (i % 4))) & 0xFF) for i in range(16)]
     assert [v - 256 if v > 127 else v for v in kv] == oracle_table("orc_kvalues_iq4nl")
+
+
+IQ2S_SHA256 = "e1aa1473412b0552c2174c30ef22ab4073f6a181b85a17056e8249bd2932fd88"
+
+
+def test_iq2s_grid_entries_and_fixture():
+    """1024 distinct entries of eight magnitudes from {8, 25, 43} (quants.py:935-939 grid_map)."""
+    from helpers import oracle_table
+    g = oracle_table("orc_iq2s_grid")
+    assert len(g) == 1024 and len(set(g)) == 1024
+    assert all(((e >> (8 * j)) & 0xFF) in (0x08, 0x19, 0x2B) for e in g for j in range(8))
+    assert hashlib.sha256(struct.pack("<1024Q", *g)).hexdigest() == IQ2S_SHA256
+
+
+def test_iq2s_grid_matches_the_reference_header():
+    from helpers import oracle_table, reference_table
+    ref = reference_table("iq2s_grid", 1024, 16)
+    if ref is None:
+        pytest.skip("reference not mounted; the SHA-256 fixture and closed forms pin the table")
+    assert ref == oracle_table("orc_iq2s_grid")
+
+
+def test_product_iq2s_grid_is_the_oracle_grid():
+    import os
+    import re
+    from helpers import ROOT, oracle_table
+    t = open(os.path.join(ROOT, "sabah-moe-accelerator_amd", "csrc", "iq_tables.h")).read()
+    body = t[t.index("kIq2sGridWords"):t.index("};", t.index("kIq2sGridWords"))]
+    w = [int(x, 16) for x in re.findall(r"0x([0-9a-fA-F]{8})", body)]
+    assert [w[2 * e] | (w[2 * e + 1] << 32) for e in range(1024)] == oracle_table("orc_iq2s_grid")
