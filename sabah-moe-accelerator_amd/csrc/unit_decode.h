@@ -11,11 +11,13 @@
 //
 // Field origin: all fields used in the inner loops start at the same residue
 // mod 4 inside the block (IQ3_S, IQ3_XXS, IQ2_S: byte 2; Q8_0 and IQ4_NL even
-// blocks: byte 2; Q4_K, Q6_K and IQ4_XS: byte 0).  F[i] is the dword at (unit start + ORG + 4 i); Fm1 is the
-// dword before it (IQ3_S reads its fp16 d there).
+// blocks: byte 2; Q4_K, Q6_K and IQ4_XS: byte 0).  F[i] is the dword at
+// (unit start + ORG + 4 i); Fm1 is the dword before it (the IQ formats read
+// their fp16 d there).
 //
 // Block layouts: sabah_rt.cu:2462-2485 (Q4_K), 2537-2545 (Q8_0), 2618-2647
-// (IQ3_S), 2293-2318 (IQ2_S), 2320-2344 (IQ3_XXS), 2380-2409 (IQ4_NL, IQ4_XS); gguf-py
+// (IQ3_S), 2293-2318 (IQ2_S), 2320-2344 (IQ3_XXS), 2380-2409 (IQ4_NL,
+// IQ4_XS); gguf-py
 // quants.py:586-606 (Q6_K: ql[128] qh[64] int8 sc[16] d).
 #pragma once
 #include "quant_formats.h"
