@@ -747,11 +747,24 @@ struct DownArgs {
     float* out;                   // [n_tokens][d_model] (may alias resid)
     int n_slots, d_model, d_ff, R, accumulate;
     unsigned int* err;
+    // optional: h already quantised, one activation row (the kernels' layout,
+    // kDownHqRow(qt, d_ff) bytes) per (token, slot), token-major
+    const uint8_t* hq;
 };
 
-template <int QT, int NT = kThreads>
+// Bytes of one pre-quantised h row, and the most a workgroup copies in: with
+// several tokens per launch, h is quantised once per (token, slot) row by a
+// k_quant_rows launch instead of once per row tile by every workgroup.
+__host__ __device__ inline int down_hq_row_bytes(int qt, int d_ff) { return align16i((int)ActLayout(d_ff, act_type(qt)).bytes); }
+constexpr int kDownHqLoads = 4;                            // 16-byte loads per lane per 256 threads
+__host__ __device__ inline bool down_hq_fits(int qt, int d_ff, int n_slots) {
+    return n_slots * down_hq_row_bytes(qt, d_ff) <= 16 * kDownHqLoads * kThreads;
+}
+
+template <int QT, int NT = kThreads, bool HQ = false>
 __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
     constexpr int RH = NT == kThreads ? kRoundsH : 1;      // activation rounds prefetched
+    constexpr int HQN = kDownHqLoads * kThreads / NT;
     SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.d_ff);
@@ -771,7 +784,15 @@ __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
     const ActBatch hb{a.h + (size_t)t * a.n_slots * a.d_ff, (size_t)a.d_ff, a.n_slots, a.d_ff, act_type(QT), act,
                       P.act_bytes};
     ActRegs<RH> ha;
-    act_prefetch<RH>(hb, ha);
+    u32x4 hqv[HQ ? HQN : 1];
+    const int hq_chunks = HQ ? (a.n_slots * P.act_bytes) >> 4 : 0;
+    if constexpr (HQ) {        // the token's q8 h rows, as 16-byte chunks (every lane loads HQN)
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.hq + (size_t)t * a.n_slots * P.act_bytes);
+#pragma unroll
+        for (int i = 0; i < HQN; ++i) hqv[i] = src[min((int)threadIdx.x + NT * i, hq_chunks - 1)];
+    } else {
+        act_prefetch<RH>(hb, ha);
+    }
     // the epilogue's own inputs (router weight of this thread's first
     // (slot, row) and this thread's row of shared / resid / out) are read now,
     // so their latency hides behind the expert loads
@@ -791,7 +812,13 @@ __global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
     TileRun<QT, NT> S{TileWalk<QT, NT>(a.n_slots, nrows, rb, a.d_ff)};
     tiles_begin(S, tile_ptr);
     store_tables<QT, NT>(tabs, gr, (int)threadIdx.x);
-    act_quantize<RH>(hb, ha);
+    if constexpr (HQ) {
+#pragma unroll
+        for (int i = 0; i < HQN; ++i)
+            if ((int)threadIdx.x + NT * i < hq_chunks) reinterpret_cast<u32x4*>(act)[threadIdx.x + NT * i] = hqv[i];
+    } else {
+        act_quantize<RH>(hb, ha);
+    }
     tiles_finish(S, tabs, stage, leads, a.d_ff, act, P.act_bytes, a.R, part);
     float* o = a.out + (size_t)t * a.d_model + row0;
     if (bad) {

@@ -54,7 +54,7 @@ struct Scratch {
     void* p = nullptr;
     size_t bytes = 0;
 };
-Scratch g_scratch_h, g_scratch_hs, g_scratch_ys;
+Scratch g_scratch_h, g_scratch_hs, g_scratch_ys, g_scratch_hq;
 // grouped (prefill) layer: offsets, pair maps, q8 rows of x and h, h and y in group order
 Scratch g_scratch_goff, g_scratch_gpair, g_scratch_gxq, g_scratch_gh, g_scratch_ghq, g_scratch_gy;
 uint16_t* g_nearest_dev = nullptr;   // IQ3_S encoder table, uploaded on first use
@@ -260,8 +260,13 @@ hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
     // IQ3_S runs 512 threads, two lanes per unit (twice the waves to hide the decode's LDS latency)
     constexpr int NT = QT == QT_IQ3_S ? 2 * kThreads : kThreads;
     const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * contribs_per_row(QT, a.d_ff));
-    if (const hipError_t e = fit_lds(k_down_combine<QT, NT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
+    if (a.hq) {
+        if (const hipError_t e = fit_lds(k_down_combine<QT, NT, true>, P.bytes, launch_lds(QT, P))) return e;
+        launch_kernel(KK_DOWN, k_down_combine<QT, NT, true>, grid, P.bytes, st, a, NT);
+        return hipGetLastError();
+    }
+    if (const hipError_t e = fit_lds(k_down_combine<QT, NT>, P.bytes, launch_lds(QT, P))) return e;
     launch_kernel(KK_DOWN, k_down_combine<QT, NT>, grid, P.bytes, st, a, NT);
     return hipGetLastError();
 }
@@ -332,7 +337,7 @@ SABAH_API int sabah_rt_init(int device) {
 SABAH_API int sabah_rt_shutdown(void) {
     if (g_device < 0) return 0;
     if (g_stream) (void)hipStreamSynchronize(g_stream);
-    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys, &g_scratch_goff, &g_scratch_gpair, &g_scratch_gxq,
+    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys, &g_scratch_hq, &g_scratch_goff, &g_scratch_gpair, &g_scratch_gxq,
                        &g_scratch_gh, &g_scratch_ghq, &g_scratch_gy}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
@@ -599,6 +604,19 @@ static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D,
     a.R = rows_down(qtd, d_ff, n_slots);
     a.accumulate = accumulate;
     a.err = g_err_dev;
+    // several tokens: quantise h once per (token, slot) row rather than in
+    // every down workgroup (one launch; a single token keeps the fused form)
+    if (n_tokens >= 2 && down_hq_fits(qtd, d_ff, n_slots) && d_ff % 256 == 0) {
+        const int hb = down_hq_row_bytes(qtd, d_ff);
+        const int n_rows = n_tokens * n_slots;
+        uint8_t* hq = static_cast<uint8_t*>(scratch(g_scratch_hq, (size_t)hb * n_rows, st));
+        if (!hq) return -1;
+        const int chunk_rows = n_rows * (d_ff / 256);
+        hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((chunk_rows + 15) / 16)), dim3(kThreads), 0, st, gu.h, n_rows,
+                           d_ff, act_type(qtd), hq, hb);
+        if (!ck(hipGetLastError(), "h quantisation launch")) return -1;
+        a.hq = hq;
+    }
     return ck(dispatch_down(qtd, a, n_tokens, st), "down/combine launch") ? 0 : -1;
 }
 
