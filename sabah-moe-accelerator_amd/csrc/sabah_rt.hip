@@ -149,8 +149,36 @@ hipError_t fit_lds(K kernel, int bytes, int total) {
 int rows_mmid(int qt, int k, bool packed) {
     return packed ? rows_per_wg(qt, k, 1) : std::min(kMaxTiles, rows_per_wg(qt, k, 1));
 }
-int rows_gate_up(int qt, int k) { return gate_up_rounds_ok(qt, k) ? rows_gate_up_rounds(qt, k) : rows_per_wg(qt, k, 2); }
-int rows_down(int qt, int k, int n_slots) { return rows_per_wg(qt, k, n_slots); }
+// Rows per workgroup of the tile kernels: the tile one pass stages (r0), or a
+// multiple of it while the launch keeps at least kMinWorkgroups workgroups:
+// with several tokens per launch there are workgroups to spare, and a
+// workgroup that walks its tiles in several passes (the next pass loading
+// while the current one decodes) spreads its fixed costs (expert ids, q8
+// activations, codebook table, epilogue) over more rows.  Measured on the
+// mixed 32-token layer (Q4_K gate/up, Q6_K down): gate/up 75 -> 62 us at 8
+// passes (16 passes: 67 us), down 213 -> 135 us at 13 passes (8: 149 us).
+constexpr int kMinWorkgroups = 1024;
+constexpr int kMaxPassesGateUp = 8, kMaxPassesDown = 16;
+// lds_of(R): the launch's LDS at R rows per workgroup (the partials grow with R)
+template <typename F>
+int grow_rows(int r0, int rows, long long wg_per_row_tile, int max_passes, F lds_of) {
+    int m = 1;
+    while (m < max_passes && r0 * (m + 1) <= rows &&
+           (long long)((rows + r0 * (m + 1) - 1) / (r0 * (m + 1))) * wg_per_row_tile >= kMinWorkgroups &&
+           lds_of(r0 * (m + 1)) <= g_max_lds)
+        ++m;
+    return r0 * m;
+}
+int rows_gate_up(int qt, int k, int d_ff, int n_slots, int n_tokens) {
+    if (gate_up_rounds_ok(qt, k)) return rows_gate_up_rounds(qt, k);
+    return grow_rows(rows_per_wg(qt, k, 2), d_ff, (long long)n_slots * n_tokens, kMaxPassesGateUp,
+                     [&](int r) { return launch_lds(qt, make_plan(qt, k, 1, 2 * r * contribs_per_row(qt, k))); });
+}
+int rows_down(int qt, int k, int n_slots, int d_model, int n_tokens) {
+    return grow_rows(rows_per_wg(qt, k, n_slots), d_model, n_tokens, kMaxPassesDown, [&](int r) {
+        return launch_lds(qt, make_plan(qt, k, n_slots, n_slots * r * contribs_per_row(qt, k)));
+    });
+}
 
 bool check_sticky() {
     if (g_err_host && __atomic_load_n(g_err_host, __ATOMIC_ACQUIRE) != 0) {
@@ -601,7 +629,7 @@ static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D,
     a.n_slots = n_slots;
     a.d_model = d_model;
     a.d_ff = d_ff;
-    a.R = rows_down(qtd, d_ff, n_slots);
+    a.R = rows_down(qtd, d_ff, n_slots, d_model, n_tokens);
     a.accumulate = accumulate;
     a.err = g_err_dev;
     // several tokens: quantise h once per (token, slot) row rather than in
@@ -643,7 +671,7 @@ SABAH_API int sabah_moe_block(const float* d_x, float* d_out, float* d_h, const 
     gu.n_slots = n_used;
     gu.d_model = d_model;
     gu.d_ff = ff;
-    gu.R = rows_gate_up(qt_gate, d_model);
+    gu.R = rows_gate_up(qt_gate, d_model, ff, n_used, 1);
     gu.err = g_err_dev;
     const ExpertSrc D{nullptr, d_ptrs + 2 * n_used, 0};
     ++g_layer_calls;
@@ -671,7 +699,7 @@ static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_
     gs.n_slots = 1;
     gs.d_model = D;
     gs.d_ff = Fs;
-    gs.R = rows_gate_up(L->qt_shared_gate, D);
+    gs.R = rows_gate_up(L->qt_shared_gate, D, Fs, 1, 1);   // single-pass tiles: grown ones ran slower here
     gs.err = g_err_dev;
     if (!ck(dispatch_gate_up(L->qt_shared_gate, gs, n_tokens, st), "shared gate/up launch")) return -1;
     MmidArgs a{};
@@ -716,7 +744,7 @@ static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const i
     gu.n_slots = n_used;
     gu.d_model = D;
     gu.d_ff = F;
-    gu.R = rows_gate_up(L->qt_gate, D);
+    gu.R = rows_gate_up(L->qt_gate, D, F, n_used, n_tokens);
     gu.err = g_err_dev;
     const ExpertSrc DS{reinterpret_cast<const uint8_t*>(L->down), nullptr, row_bytes(L->qt_down, F) * (size_t)D};
     return run_layer(gu, L->qt_gate, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, shared, d_resid, d_out, 0, st);
