@@ -517,7 +517,11 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
     a.dst_token_stride = dst_token_stride;
     a.rows = rows;
     a.k = k;
-    a.R = rows_mmid(qt, k, row_stride == sabah_row_bytes(qt, k));
+    const bool packed = row_stride == sabah_row_bytes(qt, k);
+    a.R = rows_mmid(qt, k, packed);
+    if (packed)   // several tokens: longer row tiles in passes (as for the fused layer's kernels)
+        a.R = grow_rows(a.R, rows, (long long)n_ids * n_tokens, kMaxPassesGateUp,
+                        [&](int r) { return launch_lds(qt, make_plan(qt, k, 1, r * contribs_per_row(qt, k))); });
     a.err = g_err_dev;
     if (!ck(dispatch_mmid(qt, a, st), "MUL_MAT_ID launch")) return -1;
     ++g_calls;
