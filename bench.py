@@ -208,6 +208,7 @@ def bench_batch(args, W):
     from sabah.runtime import rt
     from sabah.runtime.bank import DenseExpert, ExpertBank
     from sabah.runtime.executor import MoEExecutor
+    from sabah.runtime.rt import row_bytes
 
     dev = torch.device("cuda:0")
     rt.init(0)
@@ -278,13 +279,22 @@ def bench_batch(args, W):
     dom = max(kernels, key=lambda q: kernels[q]["total_ms"])
     u_mean = float(np.mean(U))
     pairs = T * k
-    per_launch = {
-        "grouped_gate_up": u_mean * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * pairs * W.d_ff,
-        "grouped_down": u_mean * W.matrix_bytes("down") + 4 * pairs * W.d_ff,
-        "gate_up": k * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * W.d_model + 4 * k * W.d_ff,
-        "down": k * W.matrix_bytes("down") + 4 * k * W.d_ff + 4 * (2 * W.d_model + k),
-        "mmid": 0,
-    }[dom]
+    D, F, Fs = W.d_model, W.d_ff, W.shared_d_ff
+    sh_gu = 2 * Fs * row_bytes(W.qt_shared, D) if Fs else 0
+    sh_down = D * row_bytes(W.qt_shared, Fs) if Fs else 0
+    # algorithmic bytes per step of each kernel kind: every distinct routed expert matrix once,
+    # the activations each launch reads and writes.  Token-major: gate_up covers the routed and
+    # (when present) the shared expert's gate/up launch, mmid the shared down launch.
+    step_kind_bytes = {
+        "grouped_gate_up": u_mean * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * pairs * F,
+        "grouped_down": u_mean * W.matrix_bytes("down") + 4 * pairs * F,
+        "gate_up": (u_mean * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + sh_gu
+                    + 4 * T * D * (2 if Fs else 1) + 4 * pairs * F + 4 * T * Fs),
+        "down": u_mean * W.matrix_bytes("down") + 4 * pairs * F + 4 * T * (2 * D + k),
+        "mmid": sh_down + 4 * T * Fs + 4 * T * D,
+    }
+    launches_per_step = kernels[dom]["launches"] / (args.warmup + steps)
+    per_launch = step_kind_bytes[dom] / launches_per_step
     achieved = per_launch / (kernels[dom]["avg_us"] * 1e3)
     flops = 2.0 * pairs * 3 * W.d_model * W.d_ff
     us_step = 1000.0 * ms / steps

@@ -474,8 +474,13 @@ struct MmidArgs {
     int* const leads = reinterpret_cast<int*>(lds_static + StaticLds<QT>::LEADS);        \
     uint8_t* const stage = lds_static + StaticLds<QT>::STAGE;
 
+// Waves per SIMD the tile kernels are compiled for.  Q6_K's fully unrolled unit
+// decoder takes just over 256 registers (one wave per SIMD); bounded to two
+// waves it fits in 256, which keeps a second workgroup's loads in flight.
+__host__ __device__ constexpr int tile_min_waves(int qt) { return qt == QT_Q6_K ? 2 : 1; }
+
 template <int QT>
-__global__ __launch_bounds__(kThreads) void k_mmid(MmidArgs a) {
+__global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_mmid(MmidArgs a) {
     SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.k);
@@ -538,7 +543,7 @@ struct GateUpArgs {
 __device__ inline float silu_f32(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf(-v))); }
 
 template <int QT>
-__global__ __launch_bounds__(kThreads) void k_gate_up(GateUpArgs a) {
+__global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUpArgs a) {
     SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
     const int NCB = contribs_per_row(QT, a.d_model);
@@ -762,7 +767,7 @@ __host__ __device__ inline bool down_hq_fits(int qt, int d_ff, int n_slots) {
 }
 
 template <int QT, int NT = kThreads, bool HQ = false>
-__global__ __launch_bounds__(NT) void k_down_combine(DownArgs a) {
+__global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_down_combine(DownArgs a) {
     constexpr int RH = NT == kThreads ? kRoundsH : 1;      // activation rounds prefetched
     constexpr int HQN = kDownHqLoads * kThreads / NT;
     SABAH_STATIC_LDS(QT)
