@@ -141,6 +141,31 @@ def test_mul_mat_id_matches_oracle(hip_rt, orc, qt, k, rows, x_rows_is_n_ids):
         assert np.array_equal(got[2, 3], got[2, 1])
 
 
+# Many tokens: 32 tokens x 10 ids over 1000-2048 rows give 10,000+ single-pass
+# row tiles, so the launch grows each workgroup's row tile to several staging
+# passes (up to 8) while keeping 1,024+ workgroups.  IQ3_S at k 2048: 32-row
+# passes, 256-row tiles.  Q6_K at k 768: 51-row passes, 408-row tiles, the last
+# 8 rows long (2048 = 5 x 408 + 8).  Q8_0 at k 1024: 30-row passes, 240-row
+# tiles, the last 40 rows long.
+@pytest.mark.parametrize("qt,k,rows", [(IQ3_S, 2048, 2048), (Q6_K, 768, 2048), (Q8_0, 1024, 1000)])
+def test_mul_mat_id_many_tokens_in_multi_pass_row_tiles(hip_rt, orc, qt, k, rows):
+    rng = np.random.default_rng(qt * 7 + rows)
+    E, Tn, K = 24, 32, 10
+    raw = expert_weights(orc, rng, qt, E, rows, k)
+    ids = np.stack([rng.choice(E, K, replace=False) for _ in range(Tn)]).astype(np.int32)
+    x = rng.standard_normal((Tn, 1, k)).astype(np.float32)
+    bank = T(raw)
+    out = torch.full((Tn, K, rows), float("nan"), dtype=torch.float32, device=DEV)
+    rb = raw.shape[-1]
+    hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * rb, rb, T(x), T(ids), out, rows, k, E, qt), "v2")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    assert_parity(got, want, "qt=%d k=%d rows=%d" % (qt, k, rows))
+    if qt in BIT_EXACT:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("qt,k,rows,pad", [(IQ3_S, 2560, 40, 36), (Q8_0, 1024, 24, 6), (Q4_K, 512, 70, 16)])
 def test_mul_mat_id_padded_rows(hip_rt, orc, qt, k, rows, pad):
     """Rows `pad` bytes apart beyond their length (src0->nb[1] > row bytes):
@@ -270,7 +295,9 @@ def test_moe_block_single_token_q8_0(hip_rt, orc):
 # iq3xxs_iq4nl_artifact_shape: the quant mix of the reference's shipped block
 # (IQ3_XXS gate/up, IQ4_NL down; results/bench_moe_blk0_iq3s.json) at its
 # inferred shape, d_model 2560 and expert d_ff 640 (REPORT.md:345-347)
-@pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small",
+# iq3s_t32: 32 tokens, so gate/up and down run grown multi-pass row tiles and
+# down reads h quantised once per (token, slot) row
+@pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small", "iq3s_t32",
                                   "iq3xxs_iq4nl_artifact_shape", "iq4xs_small", "iq2s_iq3s_mix"])
 def test_moe_layer_matches_oracle(hip_rt, orc, name):
     from sabah.runtime import routing
@@ -289,6 +316,9 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
         ids, w = routing.zipf_routing(rng, Tn, E, K)
     elif name == "iq2s_iq3s_mix":
         E, D, F, K, Tn, qts = 48, 2560, 768, 10, 2, (IQ2_S, IQ2_S, IQ3_S)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "iq3s_t32":
+        E, D, F, K, Tn, qts = 64, 2048, 768, 10, 32, (IQ3_S, IQ3_S, IQ3_S)
         ids, w = routing.zipf_routing(rng, Tn, E, K)
     elif name == "iq4xs_small":
         E, D, F, K, Tn, qts = 32, 2048, 768, 8, 2, (IQ4_XS, IQ4_XS, IQ4_XS)
