@@ -206,6 +206,17 @@ int sabah_moe_prefill_layer(const sabah_moe_layer_desc *layer, const float *d_x,
 int sabah_moe_route(const float *d_logits, int n_tokens, int n_experts, int n_used, int norm_w,
                     float w_scale, int32_t *d_ids, float *d_w, void *stream);
 
+/* How sabah_rt_mul_mat_id_v2 runs IQ3_S calls over many tokens.  No reference
+ * counterpart: the reference's kernel re-reads an expert per (token, slot)
+ * (sabah_rt.cu:2791-2839).  Grouped, the (token, slot) pairs are grouped by
+ * expert on the device and each expert is read once per call (int8 MFMA);
+ * eligible calls have packed rows, dense ids and x, n_experts <= 4096, and
+ * k <= 1024 with rows % 64 == 0, or k % 512 == 0, k <= 2048, rows % 32 == 0.
+ * mode 0 (default): grouped when eligible with at least 2 pairs per expert on
+ * average; 1: never; 2: whenever eligible.  The results are bit-identical
+ * either way.  Returns -1 for another mode. */
+int sabah_rt_set_mmid_grouping(int mode);
+
 #ifdef __cplusplus
 }
 #endif

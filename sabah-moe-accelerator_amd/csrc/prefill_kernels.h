@@ -21,6 +21,13 @@
 //   k_grouped_down    y[pos] = Wd[e] . q8(h[pos])
 //   k_combine         out[t] = [resid +] ((y0 w0 + y1 w1) + ...) [+ shared]
 // Supported: IQ3_S gate, up and down; d_model / 256 even and <= 8; d_ff / 256 <= 4.
+//
+// The same kernels, instantiated with MMID = true, run a grouped MUL_MAT_ID
+// (sabah_rt_mul_mat_id_v2 over many tokens): k_group_pairs, k_quant_rows on
+// x, then k_grouped_down<true> (k <= 1024, 64-row tiles) or
+// k_grouped_gate_up<true> (k <= 2048, two 16-row groups of one matrix in the
+// places of gate and up, no SwiGLU), each reading x through the pair's token
+// (or its own row when x has one row per slot) and writing dst[t][slot].
 #pragma once
 #include "mmid_kernels.h"
 
@@ -49,6 +56,9 @@ struct GroupArgs {
     int* pair_of;                 // [n_tokens * k]
     int* pos_of;                  // [n_tokens * k]
     unsigned int* err;
+    float* poison;                // MUL_MAT_ID: a bad pair's dst row becomes NaN (null: none)
+    size_t poison_nb1, poison_nb2;  // dst slot and token strides, bytes
+    int poison_rows;
 };
 
 // exclusive scan of one int per thread over the workgroup; tmp holds blockDim.x ints
@@ -106,6 +116,11 @@ __global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
         } else {
             a.pos_of[p] = -1;
             bad = true;
+            if (a.poison) {                                 // error path only: one thread per bad pair
+                float* d = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.poison) +
+                                                    (size_t)(p / a.k) * a.poison_nb2 + (size_t)(p % a.k) * a.poison_nb1);
+                for (int r = 0; r < a.poison_rows; ++r) d[r] = __builtin_nanf("");
+            }
         }
     }
     if (bad) *reinterpret_cast<volatile unsigned int*>(a.err) = 1u;
@@ -235,8 +250,20 @@ struct GroupedGateUpArgs {
     int xq_stride;
     float* h;                     // [pairs in group order][d_ff]
     int d_model, d_ff;
+    // MMID: x row of pair p = p / x_div (1: a row per slot, k: a row per token);
+    // rows 32 b .. 32 b + 31 of the one matrix at gate; out = dst[t][s]
+    int x_div;
+    float* dst;
+    size_t dst_nb1, dst_nb2;
 };
 
+// dst row of pair p (t = p / n_ids, slot p % n_ids) for the grouped MUL_MAT_ID
+__device__ inline float* pair_dst(float* dst, size_t nb1, size_t nb2, int n_ids, int p) {
+    return reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(dst) + (size_t)(p / n_ids) * nb2 +
+                                    (size_t)(p % n_ids) * nb1);
+}
+
+template <bool MMID = false>
 __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs a) {
     constexpr int QT = QT_IQ3_S;
     const int e = blockIdx.y;
@@ -247,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
     __shared__ __align__(16) float dw_tab[2 * kGuBlocksPerWave * 2 * kGuRows];
     __shared__ __align__(16) float part[2][kGuBlocksPerWave][kGuRows][kPairTile];
     __shared__ __align__(16) float gu[2][kGuRows][kPairTile];
-    const int row0 = blockIdx.x * kGuRows;
+    const int row0 = blockIdx.x * (MMID ? 2 * kGuRows : kGuRows);
     const int nb = a.d_model / 256, nb0 = nb / 2;
     const size_t rb = row_bytes(QT, a.d_model);
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
@@ -256,13 +283,13 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
     const ActLayout XL(a.d_model, QT_Q8_K);
     GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
     const uint8_t* wg = a.gate + (size_t)e * a.expert_stride + (size_t)row0 * rb;
-    const uint8_t* wu = a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
+    const uint8_t* wu = MMID ? wg + (size_t)kGuRows * rb : a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     auto tile_ptr = [&](int mm) { return mm ? wu : wg; };
     TileRun<QT> S{TileWalk<QT>(2, kGuRows, rb, a.d_model)};
     tiles_begin(S, tile_ptr);
     auto pair_x = [&](int pt, XRegs<kGuBlocksPerWave>& R) {
         const int cnt = min(kPairTile, n_e - pt);
-        const int t = a.pair_of[g0 + pt + min(j, cnt - 1)] / a.k;
+        const int t = a.pair_of[g0 + pt + min(j, cnt - 1)] / (MMID ? a.x_div : a.k);
         const uint8_t* xrow = a.xq + (size_t)t * a.xq_stride;
         load_x(R, xrow, reinterpret_cast<const float*>(xrow + XL.off_d), b0, b1, q);
     };
@@ -301,7 +328,14 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
             }
         }
         __syncthreads();
-        {
+        if constexpr (MMID) {
+            const int rr = (int)threadIdx.x >> 4, jj = (int)threadIdx.x & 15;
+            if (jj < cnt) {
+                float* d = pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.k, a.pair_of[g0 + pt + jj]);
+                d[row0 + rr] = gu[0][rr][jj];
+                d[row0 + kGuRows + rr] = gu[1][rr][jj];
+            }
+        } else {
             const int rr = (int)threadIdx.x >> 4, jj = (int)threadIdx.x & 15;
             if (jj < cnt)
                 a.h[(size_t)(g0 + pt + jj) * a.d_ff + row0 + rr] = __fmul_rn(silu_f32(gu[0][rr][jj]), gu[1][rr][jj]);
@@ -322,8 +356,14 @@ struct GroupedDownArgs {
     int hq_stride;
     float* y;                     // [pairs in group order][d_model]
     int d_model, d_ff;
+    // MMID: input row of pair p = hq + (p / x_div) * hq_stride; out = dst[t][s]
+    const int* pair_of;
+    int n_ids, x_div;
+    float* dst;
+    size_t dst_nb1, dst_nb2;
 };
 
+template <bool MMID = false>
 __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
     constexpr int QT = QT_IQ3_S;
     const int e = blockIdx.y;
@@ -345,7 +385,8 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
     tiles_begin(S, tile_ptr);
     auto pair_x = [&](int pt, XRegs<kDownBlocks>& R) {
         const int cnt = min(kPairTile, n_e - pt);
-        const uint8_t* hrow = a.hq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.hq_stride;
+        const int pos = g0 + pt + min(j, cnt - 1);
+        const uint8_t* hrow = a.hq + (size_t)(MMID ? a.pair_of[pos] / a.x_div : pos) * a.hq_stride;
         load_x(R, hrow, reinterpret_cast<const float*>(hrow + HL.off_d), 0, nb, q);
     };
     store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
@@ -363,13 +404,15 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
         float c[kDownBlocks][4];
         mfma_blocks<kDownBlocks>(rowp, tabs, 0, nb, XR, valid, ls_tab, dw_tab, kDownRows, rbase, q, c);
         if (valid) {
+            float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, a.pair_of[pos])
+                              : a.y + (size_t)pos * a.d_model;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float acc = 0.0f;
 #pragma unroll
                 for (int jj = 0; jj < kDownBlocks; ++jj)
                     if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
-                a.y[(size_t)pos * a.d_model + row0 + rbase + 4 * q + i] = acc;
+                out[row0 + rbase + 4 * q + i] = acc;
             }
         }
     }

@@ -464,6 +464,93 @@ SABAH_API int sabah_rt_unregister_bank(const void* source_key) {
 // ===========================================================================
 // MUL_MAT_ID
 // ===========================================================================
+// ---------------------------------------------------------------------------
+// Grouped MUL_MAT_ID (IQ3_S, many tokens): the (token, slot) pairs are grouped
+// by expert on the device and each expert's rows are read once per call, with
+// int8 MFMA over up to 16 pairs at a time.  The integer block sums and every
+// fp32 step are the token-major kernel's, so the results are bit-identical to
+// it; the choice between the two paths changes no value.
+//   mode 0 (default): grouped when eligible and the call has at least
+//     kGroupedMinPairsPerExpert pairs per expert on average;
+//   mode 1: never; mode 2: whenever eligible.
+// ---------------------------------------------------------------------------
+constexpr int kGroupedMinPairsPerExpert = 2;   // IQ3_S top-10 of 512: grouped wins from 128 tokens (2.5 per expert)
+std::atomic<int> g_mmid_grouping{0};
+
+SABAH_API int sabah_rt_set_mmid_grouping(int mode) {
+    if (mode < 0 || mode > 2) return fail("MUL_MAT_ID grouping mode %d outside {0 auto, 1 never, 2 always}", mode);
+    g_mmid_grouping.store(mode);
+    return 0;
+}
+
+// 0: not eligible; 1: down-shaped kernel (64-row tiles, k <= 1024); 2: gate/up-shaped (32-row tiles)
+static int grouped_mmid_form(int qt, bool packed, size_t ids_id_stride, size_t ids_token_stride, size_t x_id_stride,
+                             size_t x_token_stride, int x_rows, int n_ids, int n_tokens, int rows, int k,
+                             int n_experts) {
+    if (qt != QT_IQ3_S || !packed || n_experts > 4096) return 0;
+    if (ids_id_stride != 4 || ids_token_stride != 4 * (size_t)n_ids) return 0;
+    if (x_id_stride != 4 * (size_t)k || x_token_stride != 4 * (size_t)k * x_rows) return 0;
+    if ((size_t)n_tokens * n_ids > (size_t)1 << 24) return 0;
+    if (k % 256 == 0 && k / 256 <= kDownBlocks && rows % kDownRows == 0) return 1;
+    if (k % 512 == 0 && k / 256 <= 2 * kGuBlocksPerWave && rows % (2 * kGuRows) == 0) return 2;
+    return 0;
+}
+
+static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, const float* d_x, int x_rows,
+                        const int32_t* d_ids, int n_ids, int n_tokens, float* d_dst, size_t dst_id_stride,
+                        size_t dst_token_stride, int rows, int k, int n_experts, hipStream_t st) {
+    const size_t P = (size_t)n_tokens * n_ids;
+    const int E = n_experts, nx = n_tokens * x_rows;
+    const ActLayout XL(k, QT_Q8_K);
+    const int xq_stride = (int)XL.bytes;
+    int* off = static_cast<int*>(scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
+    int* pair_of = static_cast<int*>(scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
+    uint8_t* xq = static_cast<uint8_t*>(scratch(g_scratch_gxq, (size_t)xq_stride * nx, st));
+    if (!off || !pair_of || !xq) return -1;
+    int* pos_of = pair_of + P;
+    GroupArgs ga{d_ids, n_tokens, n_ids, E, off, pair_of, pos_of, g_err_dev, d_dst, dst_id_stride, dst_token_stride, rows};
+    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);
+    const int xq_rows = nx * (k / 256);
+    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, nx, k,
+                       (int)QT_Q8_K, xq, xq_stride);
+    const int x_div = x_rows == 1 ? n_ids : 1;      // pair p = t * n_ids + s reads x row p / x_div
+    if (form == 1) {
+        GroupedDownArgs dn{};
+        dn.down = bank;
+        dn.expert_stride = expert_stride;
+        dn.off = off;
+        dn.hq = xq;
+        dn.hq_stride = xq_stride;
+        dn.d_model = rows;
+        dn.d_ff = k;
+        dn.pair_of = pair_of;
+        dn.n_ids = n_ids;
+        dn.x_div = x_div;
+        dn.dst = d_dst;
+        dn.dst_nb1 = dst_id_stride;
+        dn.dst_nb2 = dst_token_stride;
+        launch_kernel(KK_MMID, k_grouped_down<true>, dim3((unsigned)(rows / kDownRows), (unsigned)E), 0, st, dn);
+    } else {
+        GroupedGateUpArgs gu{};
+        gu.gate = bank;
+        gu.expert_stride = expert_stride;
+        gu.off = off;
+        gu.pair_of = pair_of;
+        gu.k = n_ids;
+        gu.xq = xq;
+        gu.xq_stride = xq_stride;
+        gu.d_model = k;
+        gu.d_ff = rows;
+        gu.x_div = x_div;
+        gu.dst = d_dst;
+        gu.dst_nb1 = dst_id_stride;
+        gu.dst_nb2 = dst_token_stride;
+        launch_kernel(KK_MMID, k_grouped_gate_up<true>, dim3((unsigned)(rows / (2 * kGuRows)), (unsigned)E), 0, st,
+                      gu);
+    }
+    return ck(hipGetLastError(), "grouped MUL_MAT_ID launch") ? 0 : -1;
+}
+
 SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, size_t row_stride, const void* d_x,
                                      size_t x_id_stride, int x_rows, size_t x_token_stride, const void* d_ids,
                                      size_t ids_id_stride, size_t ids_token_stride, int n_ids, int n_tokens,
@@ -497,6 +584,22 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
             }
     }
 
+    const bool packed = row_stride == sabah_row_bytes(qt, k);
+    const int mode = g_mmid_grouping.load();
+    const int form = mode == 1 ? 0
+                   : grouped_mmid_form(qt, packed, ids_id_stride, ids_token_stride, x_id_stride, x_token_stride,
+                                       x_rows, n_ids, n_tokens, rows, k, n_experts);
+    if (form && (mode == 2 || (long long)n_tokens * n_ids >= (long long)kGroupedMinPairsPerExpert * n_experts)) {
+        if (mmid_grouped(form, bank, expert_stride, static_cast<const float*>(d_x), x_rows,
+                         static_cast<const int32_t*>(d_ids), n_ids, n_tokens, d_dst, dst_id_stride, dst_token_stride,
+                         rows, k, n_experts, st))
+            return -1;
+        ++g_calls;
+        g_tokens += (unsigned long long)n_tokens;
+        g_lookups += (unsigned long long)n_tokens * (unsigned long long)n_ids;
+        return 0;
+    }
+
     MmidArgs a{};
     a.W.base = bank;
     a.W.ptrs = nullptr;
@@ -517,7 +620,6 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
     a.dst_token_stride = dst_token_stride;
     a.rows = rows;
     a.k = k;
-    const bool packed = row_stride == sabah_row_bytes(qt, k);
     a.R = rows_mmid(qt, k, packed);
     if (packed)   // several tokens: longer row tiles in passes (as for the fused layer's kernels)
         a.R = grow_rows(a.R, rows, (long long)n_ids * n_tokens, kMaxPassesGateUp,
@@ -830,7 +932,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     const float* shared = nullptr;
     if (shared_expert(L, d_x, n_tokens, st, &shared)) return -1;
 
-    GroupArgs ga{d_ids, n_tokens, n_used, E, off, pair_of, pos_of, g_err_dev};
+    GroupArgs ga{d_ids, n_tokens, n_used, E, off, pair_of, pos_of, g_err_dev, nullptr, 0, 0, 0};
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);
     const int xq_rows = n_tokens * (D / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, n_tokens, D,
@@ -847,7 +949,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     gu.h = h;
     gu.d_model = D;
     gu.d_ff = F;
-    launch_kernel(KK_GGATE_UP, k_grouped_gate_up, dim3((unsigned)(F / kGuRows), (unsigned)E), 0, st, gu);
+    launch_kernel(KK_GGATE_UP, k_grouped_gate_up<false>, dim3((unsigned)(F / kGuRows), (unsigned)E), 0, st, gu);
     const size_t hq_rows = P * (size_t)(F / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((hq_rows + 15) / 16)), dim3(kThreads), 0, st, h, (int)P, F,
                        (int)QT_Q8_K, hq, hq_stride);
@@ -860,7 +962,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     dn.y = y;
     dn.d_model = D;
     dn.d_ff = F;
-    launch_kernel(KK_GDOWN, k_grouped_down, dim3((unsigned)(D / kDownRows), (unsigned)E), 0, st, dn);
+    launch_kernel(KK_GDOWN, k_grouped_down<false>, dim3((unsigned)(D / kDownRows), (unsigned)E), 0, st, dn);
     CombineArgs cb{y, pos_of, d_w, shared, d_resid, d_out, n_used, D};
     hipLaunchKernelGGL(k_combine, dim3((unsigned)((D + kThreads - 1) / kThreads), (unsigned)n_tokens), dim3(kThreads), 0,
                        st, cb);

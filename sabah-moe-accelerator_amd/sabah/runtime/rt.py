@@ -82,6 +82,7 @@ SIGNATURES = {
     "sabah_moe_chain": ([ctypes.POINTER(MoeLayerDesc), c_i, c_vp, c_vp, c_vp, c_i, c_i, c_vp], c_i),
     "sabah_moe_prefill_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
     "sabah_moe_route": ([c_vp, c_i, c_i, c_i, c_i, ctypes.c_float, c_vp, c_vp, c_vp], c_i),
+    "sabah_rt_set_mmid_grouping": ([c_i], c_i),
 }
 
 # harness-only exports (not part of the drop-in header)

@@ -32,6 +32,15 @@ def test_binding_covers_the_header():
     assert set(declared_functions()) == set(rt.SIGNATURES)
 
 
+def test_grouping_mode_setter_validates_without_a_device():
+    from sabah.runtime import rt
+    L = rt.lib()
+    assert L.sabah_rt_set_mmid_grouping(3) == -1
+    assert "grouping mode" in rt.last_error()
+    for mode in (1, 2, 0):
+        assert L.sabah_rt_set_mmid_grouping(mode) == 0
+
+
 def test_build_info_and_row_bytes():
     from sabah.runtime import rt
     L = rt.lib()

@@ -1,0 +1,142 @@
+"""Grouped MUL_MAT_ID (IQ3_S over many tokens) through sabah_rt_mul_mat_id_v2.
+
+The grouped path groups the (token, slot) pairs by expert on the device and
+reads each expert once per call (int8 MFMA over up to 16 pairs at a time).
+Its integer block sums are exact and its fp32 steps are the token-major
+kernel's, so the bar is bit-identity with both the token-major path and the
+oracle (ggml's CPU MUL_MAT_ID).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+IQ3_S = 21
+DEV = torch.device("cuda:0")
+AUTO, NEVER, ALWAYS = 0, 1, 2
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+@pytest.fixture
+def grouping(hip_rt):
+    lib = hip_rt.lib()
+
+    def set_mode(mode):
+        hip_rt.check(lib.sabah_rt_set_mmid_grouping(mode), "set grouping")
+
+    yield set_mode
+    set_mode(AUTO)
+
+
+def v2(hip_rt, bank, rb, rows, k, E, x, ids, out):
+    return hip_rt.lib().sabah_rt_mul_mat_id_v2(
+        vp(bank), ctypes.c_size_t(rows * rb), ctypes.c_size_t(rb),
+        vp(x), ctypes.c_size_t(x.stride(1) * 4), x.shape[1], ctypes.c_size_t(x.stride(0) * 4),
+        vp(ids), ctypes.c_size_t(4), ctypes.c_size_t(ids.stride(0) * 4), ids.shape[1], ids.shape[0],
+        vp(out), ctypes.c_size_t(out.stride(1) * 4), ctypes.c_size_t(out.stride(0) * 4), rows, k, E, IQ3_S,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), None)
+
+
+def run(hip_rt, bank, rb, rows, k, E, x, ids):
+    out = torch.full((ids.shape[0], ids.shape[1], rows), float("nan"), dtype=torch.float32, device=DEV)
+    hip_rt.check(v2(hip_rt, bank, rb, rows, k, E, x, ids, out), "v2")
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def case(orc, seed, E, rows, k, Tn, K, x_rows):
+    """E experts (the last one never selected), Tn tokens x K distinct ids, a
+    duplicate id in token 3; about Tn * K / (E - 1) pairs per expert, so most
+    experts take several 16-pair tiles."""
+    rng = np.random.default_rng(seed)
+    raw = orc.quantize_weights(IQ3_S, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    ids = np.stack([rng.choice(E - 1, K, replace=False) for _ in range(Tn)]).astype(np.int32)
+    ids[3, K - 1] = ids[3, 0]
+    x = rng.standard_normal((Tn, x_rows, k)).astype(np.float32)
+    return raw, ids, x
+
+
+# (k, rows): k <= 1024 runs the 64-row down-shaped kernel, k = 1536 / 2048 the
+# gate/up-shaped one (two 16-row groups, k split over two waves)
+SHAPES = [(768, 2048), (1024, 128), (256, 64), (2048, 768), (1536, 64)]
+
+
+@pytest.mark.parametrize("k,rows", SHAPES)
+@pytest.mark.parametrize("x_rows_is_n_ids", [False, True])
+def test_grouped_mul_mat_id_is_bit_identical(hip_rt, orc, grouping, k, rows, x_rows_is_n_ids):
+    E, Tn, K = 12, 40, 6
+    raw, ids, x = case(orc, k + rows + x_rows_is_n_ids, E, rows, k, Tn, K, K if x_rows_is_n_ids else 1)
+    bank, rb = T(raw), raw.shape[-1]
+    xd, idd = T(x), T(ids)
+    grouping(ALWAYS)
+    got = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    grouping(NEVER)
+    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    want = orc.mul_mat_id(raw, x, ids, rows, k, IQ3_S)
+    assert_parity(got, want, "grouped k=%d rows=%d" % (k, rows))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
+    if not x_rows_is_n_ids:
+        assert np.array_equal(got[3, K - 1], got[3, 0])
+
+
+def test_grouped_mul_mat_id_at_512_tokens_matches_token_major(hip_rt, orc, grouping):
+    """The shipped gate shape (2048 -> 768) over 512 tokens x top-10 of 64
+    experts: the automatic choice takes the grouped path (80 pairs per
+    expert); bit-identical to the token-major path and to the oracle."""
+    E, Tn, K, k, rows = 64, 512, 10, 2048, 768
+    raw, ids, x = case(orc, 5, E, rows, k, Tn, K, 1)
+    bank, rb = T(raw), raw.shape[-1]
+    xd, idd = T(x), T(ids)
+    grouping(AUTO)
+    got = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    grouping(NEVER)
+    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
+    want = orc.mul_mat_id(raw, x[:64], ids[:64], rows, k, IQ3_S)
+    assert np.array_equal(got[:64].view(np.uint32), want.view(np.uint32))
+
+
+def test_grouped_mul_mat_id_poisons_a_bad_slot_and_fails_the_next_call(hip_rt, orc, grouping):
+    E, Tn, K, k, rows = 12, 40, 6, 768, 128
+    raw, ids, x = case(orc, 9, E, rows, k, Tn, K, 1)
+    ids[7, 2] = E + 3
+    bank, rb = T(raw), raw.shape[-1]
+    grouping(ALWAYS)
+    out = torch.full((Tn, K, rows), 0.0, dtype=torch.float32, device=DEV)
+    hip_rt.check(v2(hip_rt, bank, rb, rows, k, E, T(x), T(ids), out), "v2")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isnan(got[7, 2]).all()
+    good = np.ones((Tn, K), bool)
+    good[7, 2] = False
+    assert not np.isnan(got[good]).any()
+    ok_ids = ids.copy()
+    ok_ids[7, 2] = 0
+    want = orc.mul_mat_id(raw, x, ok_ids, rows, k, IQ3_S)
+    assert np.array_equal(got[good].view(np.uint32), want[good].view(np.uint32))
+    lib = hip_rt.lib()
+    assert lib.sabah_rt_check_errors() == -1                # the sticky word reports the bad id once
+    assert "outside" in hip_rt.last_error()
+    assert lib.sabah_rt_check_errors() == 0
+
+
+def test_grouping_mode_is_validated(hip_rt):
+    lib = hip_rt.lib()
+    assert lib.sabah_rt_set_mmid_grouping(3) == -1
+    assert lib.sabah_rt_set_mmid_grouping(-1) == -1
+    assert lib.sabah_rt_set_mmid_grouping(AUTO) == 0
