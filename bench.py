@@ -231,10 +231,38 @@ def bench_batch(args, W):
     out = torch.empty_like(x)
     ex = MoEExecutor(bank, max_used=W.top_k, max_tokens=W.n_tokens, shared=shared)
     grouped = W.qt_gate == W.qt_up == W.qt_down == rt.QTYPE["IQ3_S"]
-    run = ex.run_prefill_layer if grouped else ex.run_layer
     T, k = W.n_tokens, W.top_k
+    mmid = W.op == "mul_mat_id"
+    if mmid:
+        # the drop-in path: three sabah_rt_mul_mat_id_v2 calls per layer, as ggml's graph makes
+        # them; h is synthetic (SwiGLU between the calls is ggml's op, outside the path)
+        L0 = rt.lib()
+        x3 = x.view(T, 1, W.d_model)
+        h_in = torch.randn(T, k, W.d_ff, device=dev)
+        g_out = torch.empty(T, k, W.d_ff, device=dev)
+        u_out = torch.empty_like(g_out)
+        d_out = torch.empty(T, k, W.d_model, device=dev)
+
+        def run(l, x_, ids_, w_, out=None):
+            ex.mul_mat_id(l, "gate", x3, ids_, out=g_out)
+            ex.mul_mat_id(l, "up", x3, ids_, out=u_out)
+            ex.mul_mat_id(l, "down", h_in, ids_, out=d_out)
+            return d_out
+
+        def run_token_major(l, x_, ids_, w_, out=None):
+            rt.check(L0.sabah_rt_set_mmid_grouping(1), "grouping mode")
+            try:
+                return run(l, x_, ids_, w_)
+            finally:
+                rt.check(L0.sabah_rt_set_mmid_grouping(0), "grouping mode")
+    else:
+        run = ex.run_prefill_layer if grouped else ex.run_layer
+        run_token_major = ex.run_layer
     U = [len(np.unique(ids_np[p])) for p in range(P)]
-    act = 4 * T * W.d_model * 2 + 2 * 4 * T * k * W.d_ff
+    if mmid:
+        act = 4 * T * W.d_model * 2 + 3 * 4 * T * k * W.d_ff + 4 * T * k * W.d_model
+    else:
+        act = 4 * T * W.d_model * 2 + 2 * 4 * T * k * W.d_ff
     step_bytes = [U[p] * W.expert_bytes() + W.shared_bytes() + act for p in range(P)]
 
     def step(i, fn):
@@ -260,11 +288,13 @@ def bench_batch(args, W):
     parity = None
     ms_token_major = None
     if grouped:
-        a = ex.run_prefill_layer(0, x, ids[0], wts[0]).clone()
-        b = ex.run_layer(0, x, ids[0], wts[0])
+        outs = []
+        for fn in (run, run_token_major):
+            r = fn(0, x, ids[0], wts[0])
+            outs.append(torch.cat([g_out.flatten(), u_out.flatten(), r.flatten()]) if mmid else r.clone())
         torch.cuda.synchronize()
-        parity = {"grouped_equals_token_major": bool(torch.equal(a, b))}
-        ms_token_major = timed(ex.run_layer, max(1, steps // 4)) / max(1, steps // 4)
+        parity = {"grouped_equals_token_major": bool(torch.equal(outs[0], outs[1]))}
+        ms_token_major = timed(run_token_major, max(1, steps // 4)) / max(1, steps // 4)
     L = rt.lib()
     L.sabah_rt_set_kernel_timing(1)
     for kind in rt.KERNEL_KINDS:
@@ -291,7 +321,7 @@ def bench_batch(args, W):
         "gate_up": (u_mean * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + sh_gu
                     + 4 * T * D * (2 if Fs else 1) + 4 * pairs * F + 4 * T * Fs),
         "down": u_mean * W.matrix_bytes("down") + 4 * pairs * F + 4 * T * (2 * D + k),
-        "mmid": sh_down + 4 * T * Fs + 4 * T * D,
+        "mmid": (u_mean * W.expert_bytes() + act) if mmid else sh_down + 4 * T * Fs + 4 * T * D,
     }
     launches_per_step = kernels[dom]["launches"] / (args.warmup + steps)
     per_launch = step_kind_bytes[dom] / launches_per_step
@@ -309,8 +339,10 @@ def bench_batch(args, W):
         "data": "synthetic (N(0,0.02) weights quantised on device; seeded routing)",
         "config": {"workload": W.name, "n_experts": W.n_experts, "top_k": k, "d_model": W.d_model, "d_ff": W.d_ff,
                    "n_tokens": T, "quant": "%d/%d/%d" % (W.qt_gate, W.qt_up, W.qt_down),
-                   "shared_d_ff": W.shared_d_ff, "mode": "group-major (sabah_moe_prefill_layer)" if grouped
-                   else "token-major (sabah_moe_layer)"},
+                   "shared_d_ff": W.shared_d_ff,
+                   "mode": ("drop-in sabah_rt_mul_mat_id_v2: gate, up, down (grouped by expert)" if mmid
+                            else "group-major (sabah_moe_prefill_layer)" if grouped
+                            else "token-major (sabah_moe_layer)")},
         "us_per_layer": round(us_step, 2), "tok_s": round(T / (us_step * 1e-6), 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "unique_experts": {"mean": u_mean, "min": min(U), "max": max(U)},
         "int8_tops": round(flops / (us_step * 1e-6) / 1e12, 2),
@@ -320,17 +352,17 @@ def bench_batch(args, W):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
                      "bytes_per_launch": int(per_launch), "avg_launch_us": kernels[dom]["avg_us"]},
-        "cpu_baseline": None if args.no_cpu else cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np),
+        "cpu_baseline": None if args.no_cpu else cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid),
         "parity": parity,
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np):
+def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid=False):
     """The oracle's layer (token-major, as ggml's CPU MUL_MAT_ID) on the host's
     cores, over a sample of the batch's tokens whose routed experts are read
-    back from HBM."""
+    back from HBM; for the drop-in workload, the oracle's three MUL_MAT_ID calls."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -344,8 +376,15 @@ def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np):
     qts = (W.qt_gate, W.qt_up, W.qt_down)
     t0 = time.perf_counter()
     tokens = 0
+    h_np = np.random.default_rng(1).standard_normal((n, W.top_k, W.d_ff)).astype(np.float32)
     while True:
-        O.moe_layer(sub["gate"], sub["up"], sub["down"], qts, x_np[:n], lid, w_np[0, :n], n_threads=threads)
+        if mmid:
+            for role, xx, rows, kk, qt in (("gate", x_np[:n, None], W.d_ff, W.d_model, W.qt_gate),
+                                           ("up", x_np[:n, None], W.d_ff, W.d_model, W.qt_up),
+                                           ("down", h_np, W.d_model, W.d_ff, W.qt_down)):
+                O.mul_mat_id(sub[role], xx, lid, rows, kk, qt, n_threads=threads)
+        else:
+            O.moe_layer(sub["gate"], sub["up"], sub["down"], qts, x_np[:n], lid, w_np[0, :n], n_threads=threads)
         tokens += n
         if time.perf_counter() - t0 >= args.cpu_seconds / 3:
             break

@@ -31,6 +31,7 @@ class Workload:
     routing: str                      # "distinct_uniform" | "topk_normal" | "zipf"
     shared_d_ff: int = 0              # dense shared expert (0: none)
     qt_shared: int = QTYPE["Q8_0"]
+    op: str = "layer"                 # "layer": the fused MoE layer; "mul_mat_id": the drop-in calls
     note: str = ""
 
     def matrix_bytes(self, role: str) -> int:
@@ -86,6 +87,10 @@ WORKLOADS = {
                                   note="IQ3_S decode, 48 MoE layers, bank fully HBM-resident"),
     "iq3s_prefill_t512": Workload("iq3s_prefill_t512", 1, 512, 10, 2048, 768, 512, IQ3_S, IQ3_S, IQ3_S, "zipf",
                                   note="group-major prefill, one layer"),
+    "iq3s_mmid_t512": Workload("iq3s_mmid_t512", 1, 512, 10, 2048, 768, 512, IQ3_S, IQ3_S, IQ3_S, "zipf",
+                               op="mul_mat_id",
+                               note="the drop-in operator over a 512-token prompt batch: one layer's gate, up "
+                                    "and down MUL_MAT_ID calls"),
     "mixed_t32_q4k_q6k_shared": Workload("mixed_t32_q4k_q6k_shared", 1, 512, 10, 2048, 768, 32, Q4_K, Q4_K, Q6_K,
                                          "topk_normal", shared_d_ff=512, qt_shared=Q8_0,
                                          note="mixed-quant small-batch decode with a dense shared expert"),
