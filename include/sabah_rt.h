@@ -212,8 +212,8 @@ int sabah_moe_route(const float *d_logits, int n_tokens, int n_experts, int n_us
  * expert on the device and each expert is read once per call (int8 MFMA);
  * eligible calls have packed rows, dense ids and x, n_experts <= 4096, and
  * k <= 1024 with rows % 64 == 0, or k % 512 == 0, k <= 2048, rows % 32 == 0.
- * mode 0 (default): grouped when eligible with at least 2 pairs per expert on
- * average; 1: never; 2: whenever eligible.  The results are bit-identical
+ * mode 0 (default): grouped when eligible with at least 1 (k <= 1024) or 2
+ * (larger k) pairs per expert on average; 1: never; 2: whenever eligible.  The results are bit-identical
  * either way.  Returns -1 for another mode. */
 int sabah_rt_set_mmid_grouping(int mode);
 

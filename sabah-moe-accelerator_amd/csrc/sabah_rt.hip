@@ -471,10 +471,12 @@ SABAH_API int sabah_rt_unregister_bank(const void* source_key) {
 // fp32 step are the token-major kernel's, so the results are bit-identical to
 // it; the choice between the two paths changes no value.
 //   mode 0 (default): grouped when eligible and the call has at least
-//     kGroupedMinPairsPerExpert pairs per expert on average;
+//     kGroupedMinPairs[form] pairs per expert on average;
 //   mode 1: never; mode 2: whenever eligible.
 // ---------------------------------------------------------------------------
-constexpr int kGroupedMinPairsPerExpert = 2;   // IQ3_S top-10 of 512: grouped wins from 128 tokens (2.5 per expert)
+// measured on IQ3_S top-10 of 512: the down-shaped form (k <= 1024) wins from
+// 64 tokens (1.25 pairs per expert), the gate/up-shaped form from 128 (2.5)
+constexpr int kGroupedMinPairs[3] = {0, 1, 2};
 std::atomic<int> g_mmid_grouping{0};
 
 SABAH_API int sabah_rt_set_mmid_grouping(int mode) {
@@ -589,7 +591,7 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
     const int form = mode == 1 ? 0
                    : grouped_mmid_form(qt, packed, ids_id_stride, ids_token_stride, x_id_stride, x_token_stride,
                                        x_rows, n_ids, n_tokens, rows, k, n_experts);
-    if (form && (mode == 2 || (long long)n_tokens * n_ids >= (long long)kGroupedMinPairsPerExpert * n_experts)) {
+    if (form && (mode == 2 || (long long)n_tokens * n_ids >= (long long)kGroupedMinPairs[form] * n_experts)) {
         if (mmid_grouped(form, bank, expert_stride, static_cast<const float*>(d_x), x_rows,
                          static_cast<const int32_t*>(d_ids), n_ids, n_tokens, d_dst, dst_id_stride, dst_token_stride,
                          rows, k, n_experts, st))

@@ -157,8 +157,13 @@ def test_mul_mat_id_many_tokens_in_multi_pass_row_tiles(hip_rt, orc, qt, k, rows
     bank = T(raw)
     out = torch.full((Tn, K, rows), float("nan"), dtype=torch.float32, device=DEV)
     rb = raw.shape[-1]
-    hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * rb, rb, T(x), T(ids), out, rows, k, E, qt), "v2")
-    torch.cuda.synchronize()
+    L = hip_rt.lib()
+    hip_rt.check(L.sabah_rt_set_mmid_grouping(1), "grouping")   # the token-major kernel (IQ3_S would group)
+    try:
+        hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * rb, rb, T(x), T(ids), out, rows, k, E, qt), "v2")
+        torch.cuda.synchronize()
+    finally:
+        hip_rt.check(L.sabah_rt_set_mmid_grouping(0), "grouping")
     got = out.cpu().numpy()
     want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
     assert_parity(got, want, "qt=%d k=%d rows=%d" % (qt, k, rows))
