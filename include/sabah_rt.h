@@ -213,8 +213,11 @@ int sabah_moe_route(const float *d_logits, int n_tokens, int n_experts, int n_us
  * eligible calls have packed rows, dense ids and x, n_experts <= 4096, and
  * k <= 1024 with rows % 64 == 0, or k % 512 == 0, k <= 2048, rows % 32 == 0.
  * mode 0 (default): grouped when eligible with at least 1 (k <= 1024) or 2
- * (larger k) pairs per expert on average; 1: never; 2: whenever eligible.  The results are bit-identical
- * either way.  Returns -1 for another mode. */
+ * (larger k) pairs per expert on average; 1: never; 2: whenever eligible.
+ * The results are bit-identical either way.  Grouped calls use library
+ * scratch (pair lists, q8 rows) shared by every stream: calls that may
+ * overlap on different streams need mode 1 (the token-major kernel uses no
+ * scratch).  Returns -1 for another mode. */
 int sabah_rt_set_mmid_grouping(int mode);
 
 #ifdef __cplusplus
