@@ -48,6 +48,8 @@ std::vector<BankEntry> g_banks;
 std::unordered_set<uintptr_t> g_device_sources;   // sources already proven to be device memory
 
 std::atomic<unsigned long long> g_calls{0}, g_empty_calls{0}, g_tokens{0}, g_lookups{0}, g_layer_calls{0};
+// MUL_MAT_ID calls that took the grouped (expert-major) path
+std::atomic<unsigned long long> g_grouped_calls{0};
 
 // grow-only device scratch, one per purpose
 struct Scratch {
@@ -76,8 +78,8 @@ unsigned long long g_kind_launches[KK_COUNT] = {0};
 // Launch a kernel; with kernel timing on, the dispatch itself records a
 // start and a stop event (hipExtLaunchKernelGGL), so the pair brackets that
 // kernel's execution on its stream and nothing else.
-template <typename K, typename A>
-void launch_kernel(int kind, K kernel, dim3 grid, int lds, hipStream_t st, const A& args, int threads = kThreads) {
+template <typename K, typename... A>
+void launch_kernel(int kind, K kernel, dim3 grid, dim3 block, int lds, hipStream_t st, A... args) {
     if (g_timing) {
         if (g_ev_free.empty()) {
             EvPair p{};
@@ -87,12 +89,12 @@ void launch_kernel(int kind, K kernel, dim3 grid, int lds, hipStream_t st, const
             EvPair ev = g_ev_free.back();
             g_ev_free.pop_back();
             ev.kind = kind;
-            hipExtLaunchKernelGGL(kernel, grid, dim3(threads), (uint32_t)lds, st, ev.a, ev.b, 0u, args);
+            hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, st, ev.a, ev.b, 0u, args...);
             g_ev_pending.push_back(ev);
             return;
         }
     }
-    hipLaunchKernelGGL(kernel, grid, dim3(threads), lds, st, args);
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
 }
 
 int fail(const char* fmt, ...) {
@@ -113,17 +115,35 @@ bool ck(hipError_t e, const char* what) {
 // HIP API (the entry points without a stream argument use the library stream)
 hipStream_t pick_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Scratch that has been outgrown is retired, not freed: a HIP graph captured
+// earlier still holds its address and reads it on every replay, so it lives
+// until sabah_rt_shutdown.  Growth allocates, which a stream capture cannot
+// record: during a capture a call that needs more scratch than any call
+// before it fails and names the size (make the same call once outside the
+// capture first).
+std::vector<void*> g_retired;
+
+bool stream_capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return cs != hipStreamCaptureStatusNone;
+}
+
 void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     if (s.bytes >= bytes) return s.p;
-    if (s.p) {
-        // the old buffer may still be read by queued kernels
-        if (!ck(hipStreamSynchronize(stream), "scratch resize sync")) return nullptr;
-        (void)hipFree(s.p);
-        s.p = nullptr;
-        s.bytes = 0;
+    if (stream_capturing(stream)) {
+        fail("library scratch must grow to %zu bytes (from %zu) during a stream capture, which cannot "
+             "allocate: make the same call once before the capture", bytes, s.bytes);
+        return nullptr;
     }
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    if (!ck(hipMalloc(&s.p, want), "scratch allocation")) return nullptr;
+    size_t want = std::max(bytes, std::max(2 * s.bytes, (size_t)1 << 20));
+    void* p = nullptr;
+    if (!ck(hipMalloc(&p, want), "scratch allocation")) return nullptr;
+    if (s.p) g_retired.push_back(s.p);
+    s.p = p;
     s.bytes = want;
     return s.p;
 }
@@ -233,7 +253,7 @@ hipError_t launch_mmid(const MmidArgs& a, hipStream_t st) {
     const Plan P = make_plan(QT, a.k, 1, a.R * contribs_per_row(QT, a.k));
     if (const hipError_t e = fit_lds(k_mmid<QT>, P.bytes, launch_lds(QT, P))) return e;
     dim3 grid((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)a.n_ids, (unsigned)a.n_tokens);
-    launch_kernel(KK_MMID, k_mmid<QT>, grid, P.bytes, st, a);
+    launch_kernel(KK_MMID, k_mmid<QT>, grid, dim3(kThreads), P.bytes, st, a);
     return hipGetLastError();
 }
 
@@ -260,12 +280,12 @@ hipError_t launch_gate_up(const GateUpArgs& a, int n_tokens, hipStream_t st) {
             constexpr int NT = kGateUpRoundThreads;
             const int dyn = gate_up_rounds_lds(P, GateUpRounds<QT, NT, 2>::STAGE);
             if (const hipError_t e = fit_lds(k_gate_up_rounds<QT, NT>, dyn, kLdsTables + dyn)) return e;
-            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT, NT>, grid, dyn, st, a, NT);
+            launch_kernel(KK_GATE_UP, k_gate_up_rounds<QT, NT>, grid, dim3(NT), dyn, st, a);
             return hipGetLastError();
         }
     }
     if (const hipError_t e = fit_lds(k_gate_up<QT>, P.bytes, launch_lds(QT, P))) return e;
-    launch_kernel(KK_GATE_UP, k_gate_up<QT>, grid, P.bytes, st, a);
+    launch_kernel(KK_GATE_UP, k_gate_up<QT>, grid, dim3(kThreads), P.bytes, st, a);
     return hipGetLastError();
 }
 
@@ -291,11 +311,11 @@ hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
     dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
     if (a.hq) {
         if (const hipError_t e = fit_lds(k_down_combine<QT, NT, true>, P.bytes, launch_lds(QT, P))) return e;
-        launch_kernel(KK_DOWN, k_down_combine<QT, NT, true>, grid, P.bytes, st, a, NT);
+        launch_kernel(KK_DOWN, k_down_combine<QT, NT, true>, grid, dim3(NT), P.bytes, st, a);
         return hipGetLastError();
     }
     if (const hipError_t e = fit_lds(k_down_combine<QT, NT>, P.bytes, launch_lds(QT, P))) return e;
-    launch_kernel(KK_DOWN, k_down_combine<QT, NT>, grid, P.bytes, st, a, NT);
+    launch_kernel(KK_DOWN, k_down_combine<QT, NT>, grid, dim3(NT), P.bytes, st, a);
     return hipGetLastError();
 }
 
@@ -321,7 +341,8 @@ int validate_mmid(const void* source, const void* d_x, const void* d_ids, const 
                     k, rows, n_ids, n_tokens, n_experts);
     if (x_rows <= 0 || (x_rows != 1 && x_rows != n_ids))
         return fail("Sabah MUL_MAT_ID input rows %d must be 1 (broadcast) or n_ids %d", x_rows, n_ids);
-    if (!supported_weight_type(qt)) return fail("unsupported quant type %d (supported: 8 Q8_0, 12 Q4_K, 14 Q6_K, 21 IQ3_S)", qt);
+    if (!supported_weight_type(qt)) return fail("unsupported quant type %d (supported: 8 Q8_0, 12 Q4_K, 14 Q6_K, 18 IQ3_XXS, 20 IQ4_NL, 21 IQ3_S, "
+                                            "22 IQ2_S, 23 IQ4_XS)", qt);
     if (k % block_elems(qt)) return fail("k=%d is not a whole number of type-%d blocks", k, qt);
     if (row_stride < row_bytes(qt, k)) return fail("row stride %zu is shorter than a row (%zu bytes)", row_stride, row_bytes(qt, k));
     return 0;
@@ -371,6 +392,8 @@ SABAH_API int sabah_rt_shutdown(void) {
         s->p = nullptr;
         s->bytes = 0;
     }
+    for (void* p : g_retired) (void)hipFree(p);
+    g_retired.clear();
     if (g_nearest_dev) (void)hipFree(g_nearest_dev);
     g_nearest_dev = nullptr;
     if (g_err_host) (void)hipHostFree(g_err_host);
@@ -511,10 +534,13 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
     if (!off || !pair_of || !xq) return -1;
     int* pos_of = pair_of + P;
     GroupArgs ga{d_ids, n_tokens, n_ids, E, off, pair_of, pos_of, g_err_dev, d_dst, dst_id_stride, dst_token_stride, rows};
-    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);
+    // the grouping and quantisation launches time as part of the call
+    // (KK_MMID), so a call's kernel time covers all three of its launches
+    launch_kernel(KK_MMID, k_group_pairs, dim3(1), dim3(kGroupThreads), (int)sizeof(int) * (2 * E + kGroupThreads), st,
+                  ga);
     const int xq_rows = nx * (k / 256);
-    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, nx, k,
-                       (int)QT_Q8_K, xq, xq_stride);
+    launch_kernel(KK_MMID, k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, nx, k,
+                  (int)QT_Q8_K, xq, xq_stride);
     const int x_div = x_rows == 1 ? n_ids : 1;      // pair p = t * n_ids + s reads x row p / x_div
     if (form == 1) {
         GroupedDownArgs dn{};
@@ -531,7 +557,7 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
         dn.dst = d_dst;
         dn.dst_nb1 = dst_id_stride;
         dn.dst_nb2 = dst_token_stride;
-        launch_kernel(KK_MMID, k_grouped_down<true>, dim3((unsigned)(rows / kDownRows), (unsigned)E), 0, st, dn);
+        launch_kernel(KK_MMID, k_grouped_down<true>, dim3((unsigned)(rows / kDownRows), (unsigned)E), dim3(kThreads), 0, st, dn);
     } else {
         GroupedGateUpArgs gu{};
         gu.gate = bank;
@@ -547,8 +573,8 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
         gu.dst = d_dst;
         gu.dst_nb1 = dst_id_stride;
         gu.dst_nb2 = dst_token_stride;
-        launch_kernel(KK_MMID, k_grouped_gate_up<true>, dim3((unsigned)(rows / (2 * kGuRows)), (unsigned)E), 0, st,
-                      gu);
+        launch_kernel(KK_MMID, k_grouped_gate_up<true>, dim3((unsigned)(rows / (2 * kGuRows)), (unsigned)E),
+                      dim3(kThreads), 0, st, gu);
     }
     return ck(hipGetLastError(), "grouped MUL_MAT_ID launch") ? 0 : -1;
 }
@@ -597,6 +623,7 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
                          rows, k, n_experts, st))
             return -1;
         ++g_calls;
+        ++g_grouped_calls;
         g_tokens += (unsigned long long)n_tokens;
         g_lookups += (unsigned long long)n_tokens * (unsigned long long)n_ids;
         return 0;
@@ -674,9 +701,9 @@ SABAH_API int sabah_rt_snapshot(char* buf, size_t n) {
     const int w = snprintf(buf, n,
                            "{\"calls\":%llu,\"empty_calls\":%llu,\"tokens\":%llu,\"lookups\":%llu,\"hits\":%llu,"
                            "\"misses\":0,\"evictions\":0,\"bytes_fetched\":0,\"resident_bytes\":%llu,"
-                           "\"banks\":%zu,\"layer_calls\":%llu,\"device\":%d,\"sentinel\":0}",
+                           "\"banks\":%zu,\"layer_calls\":%llu,\"grouped_calls\":%llu,\"device\":%d,\"sentinel\":0}",
                            g_calls.load(), g_empty_calls.load(), g_tokens.load(), g_lookups.load(), g_lookups.load(),
-                           resident_bytes(), nbanks, g_layer_calls.load(), g_device);
+                           resident_bytes(), nbanks, g_layer_calls.load(), g_grouped_calls.load(), g_device);
     return (w < 0 || (size_t)w >= n) ? fail("snapshot buffer too small") : 0;
 }
 
@@ -951,7 +978,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     gu.h = h;
     gu.d_model = D;
     gu.d_ff = F;
-    launch_kernel(KK_GGATE_UP, k_grouped_gate_up<false>, dim3((unsigned)(F / kGuRows), (unsigned)E), 0, st, gu);
+    launch_kernel(KK_GGATE_UP, k_grouped_gate_up<false>, dim3((unsigned)(F / kGuRows), (unsigned)E), dim3(kThreads), 0, st, gu);
     const size_t hq_rows = P * (size_t)(F / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((hq_rows + 15) / 16)), dim3(kThreads), 0, st, h, (int)P, F,
                        (int)QT_Q8_K, hq, hq_stride);
@@ -964,7 +991,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     dn.y = y;
     dn.d_model = D;
     dn.d_ff = F;
-    launch_kernel(KK_GDOWN, k_grouped_down<false>, dim3((unsigned)(D / kDownRows), (unsigned)E), 0, st, dn);
+    launch_kernel(KK_GDOWN, k_grouped_down<false>, dim3((unsigned)(D / kDownRows), (unsigned)E), dim3(kThreads), 0, st, dn);
     CombineArgs cb{y, pos_of, d_w, shared, d_resid, d_out, n_used, D};
     hipLaunchKernelGGL(k_combine, dim3((unsigned)((D + kThreads - 1) / kThreads), (unsigned)n_tokens), dim3(kThreads), 0,
                        st, cb);

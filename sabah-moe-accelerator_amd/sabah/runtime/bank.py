@@ -177,6 +177,10 @@ class DenseExpert:
     def ptrs(self):
         return tuple(self.mats[r].data_ptr() for r in ROLES)
 
+    def read(self, role: str) -> np.ndarray:
+        """Host copy of one matrix [rows, row_bytes]."""
+        return self.mats[role].cpu().numpy()
+
     def load(self, role: str, raw: np.ndarray) -> None:
         self.mats[role].copy_(torch.from_numpy(np.ascontiguousarray(raw, np.uint8).reshape(self.mats[role].shape)))
 

@@ -172,8 +172,13 @@ class ChainGraph:
     """The decode chain (every layer's gate/up and down kernels) captured once
     as a HIP graph over static x / ids / weights buffers.  replay() copies one
     step's inputs in and replays the graph: the host submits one graph per
-    step instead of two kernels per layer.  The library allocates its scratch
-    in an eager call before the capture, so nothing is allocated inside it."""
+    step instead of two kernels per layer.  An eager call before the capture
+    sizes the library scratch, so nothing is allocated inside it.  The graph
+    keeps the scratch it was captured with: a later, larger call grows the
+    library scratch by allocating new buffers and retires the old ones without
+    freeing them (they live until sabah_rt_shutdown), so replays stay valid.
+    Replays and eager calls must not overlap on different streams: both use
+    the same scratch while no call has outgrown it."""
 
     def __init__(self, ex: MoEExecutor, n_tokens: int, k: int, descs=None):
         L = ex.bank.n_layers

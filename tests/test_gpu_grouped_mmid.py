@@ -51,10 +51,18 @@ def v2(hip_rt, bank, rb, rows, k, E, x, ids, out):
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), None)
 
 
-def run(hip_rt, bank, rb, rows, k, E, x, ids):
+def grouped_calls(hip_rt):
+    return hip_rt.snapshot()["grouped_calls"]
+
+
+def run(hip_rt, bank, rb, rows, k, E, x, ids, grouped=None):
+    """One v2 call; `grouped` (if given) is whether it must take the grouped path."""
     out = torch.full((ids.shape[0], ids.shape[1], rows), float("nan"), dtype=torch.float32, device=DEV)
+    before = grouped_calls(hip_rt)
     hip_rt.check(v2(hip_rt, bank, rb, rows, k, E, x, ids, out), "v2")
     torch.cuda.synchronize()
+    if grouped is not None:
+        assert grouped_calls(hip_rt) == before + int(grouped)
     return out.cpu().numpy()
 
 
@@ -83,9 +91,9 @@ def test_grouped_mul_mat_id_is_bit_identical(hip_rt, orc, grouping, k, rows, x_r
     bank, rb = T(raw), raw.shape[-1]
     xd, idd = T(x), T(ids)
     grouping(ALWAYS)
-    got = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    got = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=True)
     grouping(NEVER)
-    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=False)
     want = orc.mul_mat_id(raw, x, ids, rows, k, IQ3_S)
     assert_parity(got, want, "grouped k=%d rows=%d" % (k, rows))
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -103,9 +111,9 @@ def test_grouped_mul_mat_id_at_512_tokens_matches_token_major(hip_rt, orc, group
     bank, rb = T(raw), raw.shape[-1]
     xd, idd = T(x), T(ids)
     grouping(AUTO)
-    got = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    got = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=True)
     grouping(NEVER)
-    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd)
+    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=False)
     assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
     want = orc.mul_mat_id(raw, x[:64], ids[:64], rows, k, IQ3_S)
     assert np.array_equal(got[:64].view(np.uint32), want.view(np.uint32))
@@ -133,6 +141,79 @@ def test_grouped_mul_mat_id_poisons_a_bad_slot_and_fails_the_next_call(hip_rt, o
     assert lib.sabah_rt_check_errors() == -1                # the sticky word reports the bad id once
     assert "outside" in hip_rt.last_error()
     assert lib.sabah_rt_check_errors() == 0
+
+
+def test_auto_grouping_keeps_few_pairs_per_expert_token_major(hip_rt, orc, grouping):
+    """Below the automatic threshold (here 4 tokens x 5 ids over 12 experts,
+    1.7 pairs per expert where k = 2048 needs 2) the call stays token-major."""
+    E, Tn, K, k, rows = 12, 4, 5, 2048, 64
+    raw, ids, x = case(orc, 11, E, rows, k, Tn, K, 1)
+    bank, rb = T(raw), raw.shape[-1]
+    grouping(AUTO)
+    got = run(hip_rt, bank, rb, rows, k, E, T(x), T(ids), grouped=False)
+    assert np.array_equal(got.view(np.uint32), orc.mul_mat_id(raw, x, ids, rows, k, IQ3_S).view(np.uint32))
+
+
+def test_grouped_call_captured_in_a_graph_survives_larger_eager_calls(hip_rt, orc, grouping):
+    """A grouped call captured in a HIP graph keeps the scratch it was captured
+    with: eager calls that grow the library scratch afterwards retire the old
+    buffers instead of freeing them, so the replays stay bit-identical (and
+    memory torch allocates meanwhile is not overwritten by them)."""
+    E, Tn, K, k, rows = 12, 40, 6, 2048, 64
+    raw, ids, x = case(orc, 13, E, rows, k, Tn, K, 1)
+    bank, rb = T(raw), raw.shape[-1]
+    grouping(ALWAYS)
+    xd, idd = T(x), T(ids)
+    want = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=True)   # eager: sizes the scratch
+    out = torch.full((Tn, K, rows), float("nan"), dtype=torch.float32, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = v2(hip_rt, bank, rb, rows, k, E, xd, idd, out)
+    assert rc == 0, hip_rt.last_error()
+    # larger eager calls: x with one row per slot over many tokens, so the
+    # quantised-x scratch grows well past anything sized before
+    rng = np.random.default_rng(14)
+    for big_t in (200, 400):
+        bid = np.stack([rng.choice(E - 1, K, replace=False) for _ in range(big_t)]).astype(np.int32)
+        bx = rng.standard_normal((big_t, K, k)).astype(np.float32)
+        run(hip_rt, bank, rb, rows, k, E, T(bx), T(bid), grouped=True)
+    fill = torch.full((64 << 20,), 7.0, dtype=torch.float32, device=DEV)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), "replay %d" % rep
+        (fill * 1.0).sum().item()                           # eager work between the replays
+    assert bool((fill == 7.0).all().item())
+
+
+def test_scratch_growth_inside_a_capture_fails_and_says_why(hip_rt, orc, grouping):
+    """A call that would have to grow the library scratch during a stream
+    capture returns -1 before enqueuing anything, with a message naming the
+    capture; the same call made eagerly first then captures fine."""
+    E, K, k, rows = 12, 6, 2048, 64
+    rng = np.random.default_rng(15)
+    raw = orc.quantize_weights(IQ3_S, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    bank, rb = T(raw), raw.shape[-1]
+    big_t = 800                                             # x: 800 x 6 rows, larger than any call before
+    bid = T(np.stack([rng.choice(E - 1, K, replace=False) for _ in range(big_t)]).astype(np.int32))
+    bx = T(rng.standard_normal((big_t, K, k)).astype(np.float32))
+    out = torch.empty((big_t, K, rows), dtype=torch.float32, device=DEV)
+    grouping(ALWAYS)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = v2(hip_rt, bank, rb, rows, k, E, bx, bid, out)
+    assert rc == -1
+    assert "capture" in hip_rt.last_error()
+    eager = run(hip_rt, bank, rb, rows, k, E, bx, bid, grouped=True)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        rc = v2(hip_rt, bank, rb, rows, k, E, bx, bid, out)
+    assert rc == 0, hip_rt.last_error()
+    out.zero_()
+    g2.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), eager.view(np.uint32))
 
 
 def test_grouping_mode_is_validated(hip_rt):

@@ -301,9 +301,11 @@ def test_moe_block_single_token_q8_0(hip_rt, orc):
 # (IQ3_XXS gate/up, IQ4_NL down; results/bench_moe_blk0_iq3s.json) at its
 # inferred shape, d_model 2560 and expert d_ff 640 (REPORT.md:345-347)
 # iq3s_t32: 32 tokens, so gate/up and down run grown multi-pass row tiles and
-# down reads h quantised once per (token, slot) row
+# down reads h quantised once per (token, slot) row (q8_K rows); q8_0_t4_hq and
+# iq4nl_down_t3_hq take that path with q8_0 rows (Q8_0 / IQ4_NL down, d_ff 768)
 @pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small", "iq3s_t32",
-                                  "iq3xxs_iq4nl_artifact_shape", "iq4xs_small", "iq2s_iq3s_mix"])
+                                  "iq3xxs_iq4nl_artifact_shape", "iq4xs_small", "iq2s_iq3s_mix", "q8_0_t4_hq",
+                                  "iq4nl_down_t3_hq"])
 def test_moe_layer_matches_oracle(hip_rt, orc, name):
     from sabah.runtime import routing
     from sabah.runtime.bank import DenseExpert
@@ -328,6 +330,12 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     elif name == "iq4xs_small":
         E, D, F, K, Tn, qts = 32, 2048, 768, 8, 2, (IQ4_XS, IQ4_XS, IQ4_XS)
         ids, w = routing.uniform_routing(rng, Tn, E, K)
+    elif name == "q8_0_t4_hq":
+        E, D, F, K, Tn, qts = 16, 1024, 768, 4, 4, (Q8_0, Q8_0, Q8_0)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
+    elif name == "iq4nl_down_t3_hq":
+        E, D, F, K, Tn, qts = 24, 2048, 768, 6, 3, (IQ3_XXS, IQ3_XXS, IQ4_NL)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
     else:
         E, D, F, K, Tn, qts = 64, 2048, 768, 10, 4, (IQ3_S, IQ3_S, IQ3_S)
         ids, w = routing.zipf_routing(rng, Tn, E, K)
@@ -347,6 +355,36 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     sh = None if sh_raw is None else (sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3)
     want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], qts, x, ids, w, shared=sh)
     assert_parity(out.cpu().numpy(), want, name)
+
+
+def test_mixed_layer_at_512_experts_on_a_synthetic_bank(hip_rt, orc):
+    """The mixed small-batch decode workload at its full size: 32 tokens x
+    top-10 of 512 experts from uniform router logits (about 240 distinct
+    experts), Q4_K gate/up, Q6_K down, a Q8_0 shared expert of d_ff 512.  The
+    bank is generated on the device; the oracle reads back the routed experts'
+    bytes and the shared expert's."""
+    from sabah.runtime import routing
+    from sabah.runtime.bank import DenseExpert, ExpertBank
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(532)
+    E, D, F, K, Tn, Fs = 512, 2048, 768, 10, 32, 512
+    qts = (Q4_K, Q4_K, Q6_K)
+    bank = ExpertBank(1, E, D, F, {"gate": Q4_K, "up": Q4_K, "down": Q6_K}, device="cuda:0")
+    bank.fill_synthetic(seed=532)
+    shared = DenseExpert(D, Fs, Q8_0, device="cuda:0")
+    shared.fill_synthetic(seed=533)
+    ids, w = routing.uniform_routing(rng, Tn, E, K)
+    used = np.unique(ids)
+    assert 200 <= len(used) <= 280
+    x = rng.standard_normal((Tn, D)).astype(np.float32)
+    out = MoEExecutor(bank, max_used=K, shared=shared).run_layer(0, T(x), T(ids), T(w))
+    torch.cuda.synchronize()
+    remap = {int(e): i for i, e in enumerate(used)}
+    sub = {r: np.stack([bank.read_expert(0, r, int(e)) for e in used]) for r in ("gate", "up", "down")}
+    sh = tuple(shared.read(r) for r in ("gate", "up", "down")) + ((Q8_0,) * 3,)
+    want = orc.moe_layer(sub["gate"], sub["up"], sub["down"], qts, x, np.vectorize(remap.get)(ids).astype(np.int32),
+                         w, shared=sh)
+    assert_parity(out.cpu().numpy(), want, "mixed layer, 512 experts")
 
 
 def test_moe_layer_with_a_sigmoid_gated_shared_expert(hip_rt, orc):
