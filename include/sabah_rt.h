@@ -169,6 +169,21 @@ int sabah_moe_layer(const sabah_moe_layer_desc *layer, const float *d_x, const i
                     const float *d_w, int n_used, int n_tokens, float *d_out, const float *d_resid,
                     void *stream);
 
+/* sabah_moe_layer with the same arguments and bit-identical results, for
+ * callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  No reference
+ * counterpart (the reference allocates its staging at init and on growth).
+ * Every piece of device scratch the layer needs (h, the shared expert's
+ * rows, q8 rows of h) comes from one static device array of 8 MiB that the
+ * library holds on each GPU until the process ends; the call allocates
+ * nothing and never synchronises.  A call whose scratch exceeds 8 MiB
+ * (about 200 tokens x top-10 at d_ff 768) fails before enqueuing anything.
+ * Calls on one GPU share the array: calls that overlap on different streams
+ * race.  Kernel timing does not record its launches. */
+int sabah_moe_layer_noalloc(const sabah_moe_layer_desc *layer, const float *d_x, const int32_t *d_ids,
+                            const float *d_w, int n_used, int n_tokens, float *d_out, const float *d_resid,
+                            void *stream);
+
 /* n_layers MoE layers in sequence on a residual stream:
  *   x <- x + layer_l(x)  for l = 0 .. n_layers-1
  * with per-layer ids/weights at d_ids + l*n_tokens*n_used (same for d_w).

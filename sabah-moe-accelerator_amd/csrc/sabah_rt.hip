@@ -28,6 +28,10 @@
 
 using namespace sabah;
 
+// the no-alloc layer's scratch (sabah_moe_layer_noalloc): 8 MiB per GPU
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 char g_err[512] = {0};
@@ -71,6 +75,7 @@ struct EvPair {
     int kind;
 };
 bool g_timing = false;
+bool g_launch_plain = false;   // set during sabah_moe_layer_noalloc: no timing events are created
 std::vector<EvPair> g_ev_free, g_ev_pending;
 double g_kind_ms[KK_COUNT] = {0};
 unsigned long long g_kind_launches[KK_COUNT] = {0};
@@ -80,7 +85,7 @@ unsigned long long g_kind_launches[KK_COUNT] = {0};
 // kernel's execution on its stream and nothing else.
 template <typename K, typename... A>
 void launch_kernel(int kind, K kernel, dim3 grid, dim3 block, int lds, hipStream_t st, A... args) {
-    if (g_timing) {
+    if (g_timing && !g_launch_plain) {
         if (g_ev_free.empty()) {
             EvPair p{};
             if (hipEventCreate(&p.a) == hipSuccess && hipEventCreate(&p.b) == hipSuccess) g_ev_free.push_back(p);
@@ -122,6 +127,7 @@ hipStream_t pick_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // before it fails and names the size (make the same call once outside the
 // capture first).
 std::vector<void*> g_retired;
+size_t g_scratch_total = 0;   // bytes of every grow-only buffer allocated (live and retired)
 
 bool stream_capturing(hipStream_t st) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -132,7 +138,7 @@ bool stream_capturing(hipStream_t st) {
     return cs != hipStreamCaptureStatusNone;
 }
 
-void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
+void* grow_scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     if (s.bytes >= bytes) return s.p;
     if (stream_capturing(stream)) {
         fail("library scratch must grow to %zu bytes (from %zu) during a stream capture, which cannot "
@@ -145,8 +151,16 @@ void* scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     if (s.p) g_retired.push_back(s.p);
     s.p = p;
     s.bytes = want;
+    g_scratch_total += want;
     return s.p;
 }
+
+// Scratch of sabah_moe_layer_noalloc: the fixed device array `scratch`, which
+// each GPU the library runs on holds until the process ends.  In host code
+// its name is a host-side stand-in, not a device address: host code uses
+// only the address hipGetSymbolAddress gives at sabah_rt_init, kept per device.
+constexpr int kMaxDevices = 64;
+void* g_noalloc_scratch[kMaxDevices] = {};
 
 // LDS a workgroup may allocate (the device's limit: 160 KB on gfx950)
 int g_max_lds = 65536;
@@ -379,6 +393,12 @@ SABAH_API int sabah_rt_init(int device) {
     *g_err_host = 0;
     if (!ck(hipHostGetDevicePointer(reinterpret_cast<void**>(&g_err_dev), g_err_host, 0), "sticky error word map"))
         return -1;
+    if (device >= 0 && device < kMaxDevices && !g_noalloc_scratch[device]) {
+        static_assert(sizeof(scratch) == kNoAllocScratchBytes, "the static scratch array has its stated size");
+        void* p = nullptr;
+        if (!ck(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address")) return -1;
+        g_noalloc_scratch[device] = p;
+    }
     g_device = device;
     return 0;
 }
@@ -394,6 +414,7 @@ SABAH_API int sabah_rt_shutdown(void) {
     }
     for (void* p : g_retired) (void)hipFree(p);
     g_retired.clear();
+    g_scratch_total = 0;
     if (g_nearest_dev) (void)hipFree(g_nearest_dev);
     g_nearest_dev = nullptr;
     if (g_err_host) (void)hipHostFree(g_err_host);
@@ -528,9 +549,9 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
     const int E = n_experts, nx = n_tokens * x_rows;
     const ActLayout XL(k, QT_Q8_K);
     const int xq_stride = (int)XL.bytes;
-    int* off = static_cast<int*>(scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
-    int* pair_of = static_cast<int*>(scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
-    uint8_t* xq = static_cast<uint8_t*>(scratch(g_scratch_gxq, (size_t)xq_stride * nx, st));
+    int* off = static_cast<int*>(grow_scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
+    int* pair_of = static_cast<int*>(grow_scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
+    uint8_t* xq = static_cast<uint8_t*>(grow_scratch(g_scratch_gxq, (size_t)xq_stride * nx, st));
     if (!off || !pair_of || !xq) return -1;
     int* pos_of = pair_of + P;
     GroupArgs ga{d_ids, n_tokens, n_ids, E, off, pair_of, pos_of, g_err_dev, d_dst, dst_id_stride, dst_token_stride, rows};
@@ -701,9 +722,11 @@ SABAH_API int sabah_rt_snapshot(char* buf, size_t n) {
     const int w = snprintf(buf, n,
                            "{\"calls\":%llu,\"empty_calls\":%llu,\"tokens\":%llu,\"lookups\":%llu,\"hits\":%llu,"
                            "\"misses\":0,\"evictions\":0,\"bytes_fetched\":0,\"resident_bytes\":%llu,"
-                           "\"banks\":%zu,\"layer_calls\":%llu,\"grouped_calls\":%llu,\"device\":%d,\"sentinel\":0}",
+                           "\"banks\":%zu,\"layer_calls\":%llu,\"grouped_calls\":%llu,\"scratch_bytes\":%zu,"
+                           "\"device\":%d,\"sentinel\":0}",
                            g_calls.load(), g_empty_calls.load(), g_tokens.load(), g_lookups.load(), g_lookups.load(),
-                           resident_bytes(), nbanks, g_layer_calls.load(), g_grouped_calls.load(), g_device);
+                           resident_bytes(), nbanks, g_layer_calls.load(), g_grouped_calls.load(), g_scratch_total,
+                           g_device);
     return (w < 0 || (size_t)w >= n) ? fail("snapshot buffer too small") : 0;
 }
 
@@ -748,10 +771,11 @@ SABAH_API int sabah_quantize_act(const float* d_x, void* d_y, int qt, int n_rows
     return ck(hipGetLastError(), "quantize launch") ? 0 : -1;
 }
 
-// one layer on `st`: gate/up (+SwiGLU) -> h, then down + routed combine -> out
+// one layer on `st`: gate/up (+SwiGLU) -> h, then down + routed combine ->
+// out; hq (or null) receives h quantised once per (token, slot) row
 static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D, const Routing& rt, int n_slots,
                      int d_model, int d_ff, int n_tokens, const float* w, const float* shared, const float* resid,
-                     float* out, int accumulate, hipStream_t st) {
+                     float* out, int accumulate, uint8_t* hq, hipStream_t st) {
     if (!ck(dispatch_gate_up(qtg, gu, n_tokens, st), "gate/up launch")) return -1;
     DownArgs a{};
     a.D = D;
@@ -767,20 +791,22 @@ static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D,
     a.R = rows_down(qtd, d_ff, n_slots, d_model, n_tokens);
     a.accumulate = accumulate;
     a.err = g_err_dev;
-    // several tokens: quantise h once per (token, slot) row rather than in
-    // every down workgroup (one launch; a single token keeps the fused form)
-    if (n_tokens >= 2 && down_hq_fits(qtd, d_ff, n_slots) && d_ff % 256 == 0) {
+    if (hq) {
         const int hb = down_hq_row_bytes(qtd, d_ff);
         const int n_rows = n_tokens * n_slots;
-        uint8_t* hq = static_cast<uint8_t*>(scratch(g_scratch_hq, (size_t)hb * n_rows, st));
-        if (!hq) return -1;
         const int chunk_rows = n_rows * (d_ff / 256);
-        hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((chunk_rows + 15) / 16)), dim3(kThreads), 0, st, gu.h, n_rows,
-                           d_ff, act_type(qtd), hq, hb);
+        launch_kernel(KK_DOWN, k_quant_rows, dim3((unsigned)((chunk_rows + 15) / 16)), dim3(kThreads), 0, st, gu.h,
+                      n_rows, d_ff, act_type(qtd), hq, hb);
         if (!ck(hipGetLastError(), "h quantisation launch")) return -1;
         a.hq = hq;
     }
     return ck(dispatch_down(qtd, a, n_tokens, st), "down/combine launch") ? 0 : -1;
+}
+
+// several tokens: h is quantised once per (token, slot) row rather than in
+// every down workgroup (one launch; a single token keeps the fused form)
+static bool layer_quantises_h_once(int qtd, int d_ff, int n_slots, int n_tokens) {
+    return n_tokens >= 2 && down_hq_fits(qtd, d_ff, n_slots) && d_ff % 256 == 0;
 }
 
 static bool layer_types_ok(int qtg, int qtu, int qtd, int d_model, int d_ff) {
@@ -811,20 +837,68 @@ SABAH_API int sabah_moe_block(const float* d_x, float* d_out, float* d_h, const 
     const ExpertSrc D{nullptr, d_ptrs + 2 * n_used, 0};
     ++g_layer_calls;
     return run_layer(gu, qt_gate, qt_down, D, gu.rt, n_used, d_model, ff, 1, d_w, nullptr, nullptr, d_out, accumulate,
-                     g_stream);
+                     nullptr, g_stream);
 }
 
-// dense shared expert of a layer: gate/up + SwiGLU -> hs, down -> ys; *ys_out
-// is ys (added by the routed combine), or nullptr when the layer has none
-static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_tokens, hipStream_t st,
-                         const float** ys_out) {
-    *ys_out = nullptr;
+// Device scratch of a layer call: h, the shared expert's hs and ys, and the
+// several-token q8 rows of h.  A Workspace hands them out either from the
+// library's grow-only buffers (arena null) or from a fixed arena, carved
+// front to back at 256-byte alignment.
+struct LayerBufs {
+    float *h = nullptr, *hs = nullptr, *ys = nullptr;
+    uint8_t* hq = nullptr;
+};
+struct Workspace {
+    uint8_t* arena = nullptr;
+    size_t cap = 0, used = 0;
+    void* get(Scratch& s, size_t bytes, hipStream_t st) {
+        if (!arena) return grow_scratch(s, bytes, st);
+        const size_t off = (used + 255) & ~(size_t)255;
+        if (off + bytes > cap) return nullptr;   // callers check the total first (layer_scratch_bytes)
+        used = off + bytes;
+        return arena + off;
+    }
+};
+static size_t layer_hq_bytes(const sabah_moe_layer_desc* L, int n_used, int n_tokens) {
+    if (!layer_quantises_h_once(L->qt_down, L->d_ff, n_used, n_tokens)) return 0;
+    return (size_t)down_hq_row_bytes(L->qt_down, L->d_ff) * n_tokens * n_used;
+}
+// bytes a Workspace arena must hold for one layer call (the same requests,
+// in the same order and alignment, as layer_bufs makes)
+static size_t layer_scratch_bytes(const sabah_moe_layer_desc* L, int n_used, int n_tokens) {
+    size_t used = 0;
+    auto take = [&](size_t b) { used = ((used + 255) & ~(size_t)255) + b; };
+    if (L->shared_gate) {
+        take(sizeof(float) * (size_t)n_tokens * L->d_ff_shared);
+        take(sizeof(float) * (size_t)n_tokens * L->d_model);
+    }
+    take(sizeof(float) * (size_t)n_tokens * n_used * L->d_ff);
+    if (const size_t hq = layer_hq_bytes(L, n_used, n_tokens)) take(hq);
+    return used;
+}
+static int layer_bufs(const sabah_moe_layer_desc* L, int n_used, int n_tokens, Workspace& ws, hipStream_t st,
+                      LayerBufs& b) {
+    if (L->shared_gate) {
+        b.hs = static_cast<float*>(ws.get(g_scratch_hs, sizeof(float) * (size_t)n_tokens * L->d_ff_shared, st));
+        b.ys = static_cast<float*>(ws.get(g_scratch_ys, sizeof(float) * (size_t)n_tokens * L->d_model, st));
+        if (!b.hs || !b.ys) return -1;
+    }
+    b.h = static_cast<float*>(ws.get(g_scratch_h, sizeof(float) * (size_t)n_tokens * n_used * L->d_ff, st));
+    if (!b.h) return -1;
+    if (const size_t hq = layer_hq_bytes(L, n_used, n_tokens)) {
+        b.hq = static_cast<uint8_t*>(ws.get(g_scratch_hq, hq, st));
+        if (!b.hq) return -1;
+    }
+    return 0;
+}
+
+// dense shared expert of a layer: gate/up + SwiGLU -> hs, down -> ys (added
+// by the routed combine); nothing when the layer has none
+static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_tokens, float* hs, float* ys,
+                         hipStream_t st) {
     if (!L->shared_gate) return 0;
     const int D = L->d_model;
     const int Fs = L->d_ff_shared;
-    float* hs = static_cast<float*>(scratch(g_scratch_hs, sizeof(float) * (size_t)n_tokens * Fs, st));
-    float* ys = static_cast<float*>(scratch(g_scratch_ys, sizeof(float) * (size_t)n_tokens * D, st));
-    if (!hs || !ys) return -1;
     GateUpArgs gs{};
     gs.G = {reinterpret_cast<const uint8_t*>(L->shared_gate), nullptr, 0};
     gs.U = {reinterpret_cast<const uint8_t*>(L->shared_up), nullptr, 0};
@@ -857,32 +931,30 @@ static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_
     a.sg_w = L->shared_gate_inp;                 // ggml_mul(ffn_shexp, sigmoid(gate_inp_shexp . x))
     a.sg_x = d_x;
     a.sg_n = D;
-    if (!ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch")) return -1;
-    *ys_out = ys;
-    return 0;
+    return ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch") ? 0 : -1;
 }
 
 static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const int32_t* d_ids, const float* d_w,
-                        int n_used, int n_tokens, float* d_out, const float* d_resid, hipStream_t st) {
+                        int n_used, int n_tokens, float* d_out, const float* d_resid, Workspace& ws, hipStream_t st) {
     const int D = L->d_model, F = L->d_ff;
-    const float* shared = nullptr;
-    if (shared_expert(L, d_x, n_tokens, st, &shared)) return -1;
-    float* h = static_cast<float*>(scratch(g_scratch_h, sizeof(float) * (size_t)n_tokens * n_used * F, st));
-    if (!h) return -1;
+    LayerBufs b;
+    if (layer_bufs(L, n_used, n_tokens, ws, st, b)) return -1;
+    if (shared_expert(L, d_x, n_tokens, b.hs, b.ys, st)) return -1;
     const Routing rt{reinterpret_cast<const uint8_t*>(d_ids), 4, (size_t)n_used * 4, L->n_experts};
     GateUpArgs gu{};
     gu.G = {reinterpret_cast<const uint8_t*>(L->gate), nullptr, row_bytes(L->qt_gate, D) * (size_t)F};
     gu.U = {reinterpret_cast<const uint8_t*>(L->up), nullptr, row_bytes(L->qt_up, D) * (size_t)F};
     gu.rt = rt;
     gu.x = d_x;
-    gu.h = h;
+    gu.h = b.h;
     gu.n_slots = n_used;
     gu.d_model = D;
     gu.d_ff = F;
     gu.R = rows_gate_up(L->qt_gate, D, F, n_used, n_tokens);
     gu.err = g_err_dev;
     const ExpertSrc DS{reinterpret_cast<const uint8_t*>(L->down), nullptr, row_bytes(L->qt_down, F) * (size_t)D};
-    return run_layer(gu, L->qt_gate, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, shared, d_resid, d_out, 0, st);
+    return run_layer(gu, L->qt_gate, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, b.ys, d_resid, d_out, 0, b.hq,
+                     st);
 }
 
 static int check_layer_desc(const sabah_moe_layer_desc* L) {
@@ -911,7 +983,39 @@ SABAH_API int sabah_moe_layer(const sabah_moe_layer_desc* layer, const float* d_
     if (n_tokens == 0) return 0;
     ++g_layer_calls;
     g_lookups += (unsigned long long)n_tokens * n_used;
-    return moe_layer_on(layer, d_x, d_ids, d_w, n_used, n_tokens, d_out, d_resid, pick_stream(stream));
+    Workspace ws;
+    return moe_layer_on(layer, d_x, d_ids, d_w, n_used, n_tokens, d_out, d_resid, ws, pick_stream(stream));
+}
+
+// sabah_moe_layer with all of its device scratch in the library's static
+// array (8 MiB per GPU): no allocation of any kind, so it may be called
+// where allocating is not allowed (stream capture, serving loops).  Calls on
+// one GPU share the array: calls that overlap on different streams race.
+SABAH_API int sabah_moe_layer_noalloc(const sabah_moe_layer_desc* layer, const float* d_x, const int32_t* d_ids,
+                                      const float* d_w, int n_used, int n_tokens, float* d_out, const float* d_resid,
+                                      void* stream) {
+    if (check_layer_desc(layer)) return -1;
+    if (!d_x || !d_ids || !d_w || !d_out || n_used <= 0 || n_tokens < 0) return fail("invalid MoE layer arguments");
+    if (n_used > kMaxTiles) return fail("n_used %d exceeds the supported maximum %d", n_used, kMaxTiles);
+    if (g_device < 0) return fail("sabah_rt_init has not been called");
+    if (!check_sticky()) return -1;
+    if (n_tokens == 0) return 0;
+    const size_t need = layer_scratch_bytes(layer, n_used, n_tokens);
+    if (need > kNoAllocScratchBytes)
+        return fail("sabah_moe_layer_noalloc: %d tokens x %d experts (d_ff %d) need %zu bytes of scratch, more "
+                    "than the %zu bytes of its static scratch; split the tokens or call sabah_moe_layer",
+                    n_tokens, n_used, layer->d_ff, need, kNoAllocScratchBytes);
+    if (g_device >= kMaxDevices || !g_noalloc_scratch[g_device])
+        return fail("sabah_moe_layer_noalloc: no static scratch on device %d", g_device);
+    ++g_layer_calls;
+    g_lookups += (unsigned long long)n_tokens * n_used;
+    Workspace ws;
+    ws.arena = static_cast<uint8_t*>(g_noalloc_scratch[g_device]);
+    ws.cap = kNoAllocScratchBytes;
+    g_launch_plain = true;
+    const int rc = moe_layer_on(layer, d_x, d_ids, d_w, n_used, n_tokens, d_out, d_resid, ws, pick_stream(stream));
+    g_launch_plain = false;
+    return rc;
 }
 
 SABAH_API int sabah_moe_chain(const sabah_moe_layer_desc* layers, int n_layers, float* d_x, const int32_t* d_ids,
@@ -927,7 +1031,9 @@ SABAH_API int sabah_moe_chain(const sabah_moe_layer_desc* layers, int n_layers, 
     hipStream_t st = pick_stream(stream);
     const size_t per = (size_t)n_tokens * n_used;
     for (int l = 0; l < n_layers; ++l) {
-        if (moe_layer_on(layers + l, d_x, d_ids + per * l, d_w + per * l, n_used, n_tokens, d_x, d_x, st)) return -1;
+        Workspace ws;
+        if (moe_layer_on(layers + l, d_x, d_ids + per * l, d_w + per * l, n_used, n_tokens, d_x, d_x, ws, st))
+            return -1;
     }
     g_layer_calls += (unsigned long long)n_layers;
     g_lookups += (unsigned long long)n_layers * per;
@@ -950,16 +1056,21 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     const size_t P = (size_t)n_tokens * n_used;
     const ActLayout XL(D, QT_Q8_K), HL(F, QT_Q8_K);
     const int xq_stride = (int)XL.bytes, hq_stride = (int)HL.bytes;
-    int* off = static_cast<int*>(scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
-    int* pair_of = static_cast<int*>(scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
-    uint8_t* xq = static_cast<uint8_t*>(scratch(g_scratch_gxq, (size_t)xq_stride * n_tokens, st));
-    float* h = static_cast<float*>(scratch(g_scratch_gh, sizeof(float) * P * F, st));
-    uint8_t* hq = static_cast<uint8_t*>(scratch(g_scratch_ghq, (size_t)hq_stride * P, st));
-    float* y = static_cast<float*>(scratch(g_scratch_gy, sizeof(float) * P * D, st));
+    int* off = static_cast<int*>(grow_scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
+    int* pair_of = static_cast<int*>(grow_scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
+    uint8_t* xq = static_cast<uint8_t*>(grow_scratch(g_scratch_gxq, (size_t)xq_stride * n_tokens, st));
+    float* h = static_cast<float*>(grow_scratch(g_scratch_gh, sizeof(float) * P * F, st));
+    uint8_t* hq = static_cast<uint8_t*>(grow_scratch(g_scratch_ghq, (size_t)hq_stride * P, st));
+    float* y = static_cast<float*>(grow_scratch(g_scratch_gy, sizeof(float) * P * D, st));
     if (!off || !pair_of || !xq || !h || !hq || !y) return -1;
     int* pos_of = pair_of + P;
-    const float* shared = nullptr;
-    if (shared_expert(L, d_x, n_tokens, st, &shared)) return -1;
+    float *hs = nullptr, *shared = nullptr;
+    if (L->shared_gate) {
+        hs = static_cast<float*>(grow_scratch(g_scratch_hs, sizeof(float) * (size_t)n_tokens * L->d_ff_shared, st));
+        shared = static_cast<float*>(grow_scratch(g_scratch_ys, sizeof(float) * (size_t)n_tokens * D, st));
+        if (!hs || !shared) return -1;
+    }
+    if (shared_expert(L, d_x, n_tokens, hs, shared, st)) return -1;
 
     GroupArgs ga{d_ids, n_tokens, n_used, E, off, pair_of, pos_of, g_err_dev, nullptr, 0, 0, 0};
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);

@@ -79,6 +79,7 @@ SIGNATURES = {
     "sabah_quantize_act": ([c_vp, c_vp, c_i, c_i, c_i, c_vp], c_i),
     "sabah_moe_block": ([c_vp, c_vp, c_vp, c_vp, c_vp, c_i, c_i, c_i, c_i, c_i, c_i, c_i], c_i),
     "sabah_moe_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
+    "sabah_moe_layer_noalloc": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
     "sabah_moe_chain": ([ctypes.POINTER(MoeLayerDesc), c_i, c_vp, c_vp, c_vp, c_i, c_i, c_vp], c_i),
     "sabah_moe_prefill_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
     "sabah_moe_route": ([c_vp, c_i, c_i, c_i, c_i, ctypes.c_float, c_vp, c_vp, c_vp], c_i),
