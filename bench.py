@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--layer-fusion", type=int, default=1, choices=(0, 1),
+                    help="1 (the library's default): one fused launch per layer; 0: gate/up then down + combine")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="finish with one device-to-device copy of this many MiB (a plain copy kernel of known "
                          "size, to calibrate the FETCH_SIZE / WRITE_SIZE counters)")
@@ -68,6 +70,7 @@ def main() -> int:
         return bench_batch(args, W)
     dev = torch.device("cuda:0")
     rt.init(0)
+    rt.check(rt.lib().sabah_rt_set_layer_fusion(args.layer_fusion), "layer fusion mode")
     t0 = time.time()
     bank = ExpertBank(W.n_layers, W.n_experts, W.d_model, W.d_ff,
                       {"gate": W.qt_gate, "up": W.qt_up, "down": W.qt_down}, device="cuda:0")
@@ -147,6 +150,7 @@ def main() -> int:
         "gate_up": k_used * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * W.d_model + 4 * k_used * W.d_ff,
         "down": k_used * W.matrix_bytes("down") + 4 * k_used * W.d_ff + 4 * (2 * W.d_model + k_used),
     }
+    per_launch["layer"] = per_launch["gate_up"] + per_launch["down"]    # the fused launch does both
     achieved = per_launch[dom] / (kernels[dom]["avg_us"] * 1e3)          # GB/s
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(W.name, dom),
@@ -166,7 +170,11 @@ def main() -> int:
         "config": {"workload": W.name, "n_layers": W.n_layers, "n_experts": W.n_experts, "top_k": W.top_k,
                    "d_model": W.d_model, "d_ff": W.d_ff, "n_tokens": W.n_tokens, "quant": "IQ3_S",
                    "bank_bytes": bank.total_bytes, "expert_bytes_per_step": nbytes // args.steps,
-                   "mode": "chain of per-layer kernels (gate/up+SwiGLU, down+combine) replayed as one HIP graph per token"},
+                   "mode": ("one fused launch per layer (gate/up+SwiGLU and down+combine workgroups in one grid, h "
+                            "handed over in the kernel), the 48 launches replayed as one HIP graph per token"
+                            if "layer" in kernels else
+                            "chain of per-layer kernels (gate/up+SwiGLU, down+combine) replayed as one HIP graph per "
+                            "token")},
         "tok_s": round(1000.0 / ms_step, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "us_per_layer": round(1000.0 * ms_step / W.n_layers, 3),
         "kernels": {k: {"launches": v["launches"], "avg_us": round(v["avg_us"], 3)} for k, v in kernels.items()},
@@ -188,6 +196,7 @@ def main() -> int:
 
 # kernel symbols of each timing kind, as the traffic summaries name them
 KERNEL_SYMBOL = {"gate_up": ("k_gate_up_rounds", "k_gate_up"), "down": ("k_down_combine",), "mmid": ("k_mmid",),
+                 "layer": ("k_layer_decode",),
                  "grouped_gate_up": ("k_grouped_gate_up",), "grouped_down": ("k_grouped_down",)}
 INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
 

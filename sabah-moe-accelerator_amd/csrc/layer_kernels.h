@@ -1,0 +1,281 @@
+// One launch per MoE layer at one token (IQ3_S gate, up and down): the
+// gate/up + SwiGLU workgroups and the down + combine workgroups run in the
+// same grid, so the down weights stream from HBM while gate/up decodes.
+//
+// The layer is the one the two-kernel form computes (k_gate_up_rounds, then
+// k_down_combine: ggml's MUL_MAT_ID + GLU, MUL_MAT_ID on h, the slot-ordered
+// weighted sum; qwen4exp.cpp:848-862, sabah_rt.cu:2725-2785), with the same
+// unit decoders, integer sums and fp32 steps in the same order, so the
+// results are bit-identical to it.
+//
+// Grid: n_g gate/up workgroups (ids 0 .. n_g-1), then n_d down workgroups.
+// Workgroups are dispatched in id order, so every gate/up workgroup has been
+// dispatched before any down workgroup: a down workgroup waits only for
+// workgroups that are running or done, and gate/up workgroups wait for
+// nothing.  Every wait is also bounded in time (kLayerWaitTicks): one that
+// runs out poisons its rows, sets the sticky error word to 2 and ends, so
+// every wave of the grid exits.
+//
+// The h handoff, per workgroup and without shared counters:
+//   gate/up: h rows stored write-through to memory (agent-scope stores), the
+//     stores waited for, then its flag sync[g] set (an agent-scope store);
+//   down: the codebook table built, the weights loaded and staged in LDS,
+//     and each lane's half unit decoded to int8 in registers, all while
+//     gate/up runs; then wave 0 waits for the flags, h is read with ordinary
+//     loads, quantised, and dotted with the decoded weights.  Down
+//     workgroups 0-7 (one per XCD) poll the n_g flags with agent-scope loads
+//     (16 bytes per lane per poll) and then store their XCD's flag (agent
+//     scope), which the XCD's other down workgroups poll, one word each, so
+//     the gate/up workgroups' stores do not queue behind 256 pollers of the
+//     same lines.  The XCD is the hardware's XCC_ID register; an XCD without
+//     a polling workgroup would leave its other workgroups to their bounded
+//     wait.  An XCD's L2 and
+//     a CU's L1 start each launch without lines of h (kernel-boundary
+//     coherence of device memory), and no workgroup reads h before the flags,
+//     so the first read of a line on an XCD fetches it from memory and the
+//     XCD's other down workgroups hit the line in L2.
+// Flags never go back to zero: every entry of sync (kSyncG flags, then
+// kSyncD down counters) advances by one per launch.  A workgroup reads its
+// own entry at start (the number of launches so far, n) and waits for or
+// writes n + 1; down workgroup 0 advances the entries this launch does not
+// use.  So a HIP graph can replay the kernel with unchanged arguments.
+#pragma once
+#include "mmid_kernels.h"
+
+namespace sabah {
+
+// Layout in 32-bit words: kSyncG gate/up flags (dense, polled 16 bytes per
+// lane), kSyncD down counters (each read and written only by its owner, at
+// its start and end), kSyncXcds per-XCD flags (one 128-byte line each,
+// written as a whole line).  (Gate/up flags one per line, written whole,
+// measured slower: the pollers then read 240 lines per poll.)
+constexpr int kLine = 32;                               // words per 128-byte line
+constexpr int kSyncG = 1024, kSyncD = 1024, kSyncXcds = 8;
+constexpr int kSyncDOff = kSyncG;
+constexpr int kSyncX = kSyncDOff + kSyncD;              // first per-XCD flag (line aligned)
+constexpr int kSyncWords = kSyncX + kSyncXcds * kLine;
+constexpr unsigned long long kLayerWaitTicks = 200000;   // 2 ms of s_memrealtime (100 MHz)
+constexpr unsigned kErrLayerWait = 2u;                  // sticky error word: a down workgroup's wait ran out
+constexpr int kLayerThreads = 512;
+
+struct LayerArgs {
+    GateUpArgs gu;              // gate/up workgroups: h of token 0
+    DownArgs dn;                // down workgroups
+    int n_g, g_tiles;           // gate/up workgroups (g_tiles row tiles per slot)
+    int n_d;                    // down workgroups
+    uint32_t* sync;             // [kSyncWords] lockstep flags (layout above)
+    uint32_t wait_skew;         // 0; a test of the timeout path sets 1: the down workgroups wait for a
+                                // flag value no gate/up workgroup writes, so their bounded wait runs out
+};
+
+// LDS of the fused kernel: the down role's static layout (IQ3_S table, tile
+// leads, staging area; the gate/up role stages its rounds in the same area),
+// dynamic: the larger of the two roles' plans
+__host__ __device__ inline int layer_dyn_lds(const GateUpArgs& gu, const DownArgs& dn) {
+    const Plan Pg = make_plan(QT_IQ3_S, gu.d_model, 1, 2 * gu.R * contribs_per_row(QT_IQ3_S, gu.d_model));
+    const Plan Pd = make_plan(QT_IQ3_S, dn.d_ff, dn.n_slots, dn.n_slots * dn.R * contribs_per_row(QT_IQ3_S, dn.d_ff));
+    return max(Pg.bytes, Pd.bytes);
+}
+
+__device__ inline unsigned long long wall_ticks() { return __builtin_amdgcn_s_memrealtime(); }
+
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ inline unsigned xcc_id() {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & (unsigned)(kSyncXcds - 1);
+}
+
+// Wave 0 waits until the word at p holds `target` (agent-scope loads)
+__device__ inline bool wait_word(const uint32_t* p, uint32_t target) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p), (short)0, 4, 0x00020000);
+    const unsigned long long t0 = wall_ticks();
+    for (;;) {
+        const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 16));
+        if (v == target) return true;
+        if (wall_ticks() - t0 > kLayerWaitTicks) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Wave 0 waits until the gate/up flags [0, n) all hold `target`; true when
+// they do, false when the wait ran out.  Lane l reads flags l, l + 64, ...
+// (one agent-scope dword load per flag line per poll).
+// Wave 0 waits until the gate/up flags [0, n) all hold `target`; true when
+// they do, false when the wait ran out.  One 16-byte agent-scope load per
+// lane per poll covers 256 flags (loads past n return 0 and are masked).
+__device__ inline bool wait_flags(const uint32_t* sync, int n, uint32_t target) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(sync), (short)0, n * 4, 0x00020000);
+    const int lane = (int)(threadIdx.x & 63u);
+    const unsigned long long t0 = wall_ticks();
+    for (;;) {
+        bool mine = true;
+        for (int base = 0; base < n; base += 256) {
+            const int f = base + 4 * lane;
+            if (f < n) {
+                const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, f * 4, 0, 16);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (f + j < n && v[j] != target) mine = false;
+            }
+        }
+        if (__all(mine)) return true;
+        if (wall_ticks() - t0 > kLayerWaitTicks) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+// a whole 128-byte flag line set to v by the first 32 lanes of wave 0 (one
+// store instruction), agent scope
+__device__ inline void store_flag_line(uint32_t* line, uint32_t v) {
+    if (threadIdx.x < kLine) __hip_atomic_store(line + threadIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
+    constexpr int QT = QT_IQ3_S;
+    SABAH_STATIC_LDS(QT)
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int b = (int)blockIdx.x;
+    if (b < a.n_g) {
+        // ---- gate/up + SwiGLU: rows of one slot, published for the down workgroups
+        __builtin_amdgcn_s_setprio(1);                      // ahead of the down waves on a shared SIMD
+        const uint32_t target = a.sync[b] + 1u;
+        const int tile = b % a.g_tiles, s = b / a.g_tiles;
+        gate_up_rounds_tile<QT, NT, 2>(a.gu, 0, s, tile * a.gu.R, tabs, smem, stage, true);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // this thread's h stores are in memory
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_store(a.sync + b, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    // ---- down + routed combine of rows row0 .. row0 + R (k_down_combine's steps)
+    const DownArgs& d = a.dn;
+    const int dj = b - a.n_g;
+    uint32_t* my = a.sync + kSyncDOff + dj;
+    const uint32_t target = *my + 1u;
+    if (dj == 0) {                                          // advance the entries no workgroup of this launch owns
+        for (int i = a.n_g + (int)threadIdx.x; i < kSyncG; i += NT) a.sync[i] = target;
+        for (int i = a.n_d + (int)threadIdx.x; i < kSyncD; i += NT) a.sync[kSyncDOff + i] = target;
+    }
+    const int NCB = contribs_per_row(QT, d.d_ff);
+    const Plan P = make_plan(QT, d.d_ff, d.n_slots, d.n_slots * d.R * NCB);
+    const int row0 = dj * d.R;
+    const int nrows = min(d.R, d.d_model - row0);
+    const size_t rb = row_bytes(QT, d.d_ff);
+    uint8_t* act = smem + P.off_act;
+    float* part = reinterpret_cast<float*>(smem + P.off_part);
+    // lane s of every wave holds slot s's tile (lanes past n_slots repeat the
+    // last slot); a slot with an invalid id stages expert 0's rows, never used
+    const int lane = (int)(threadIdx.x & 63u);
+    const SlotWord sw = load_slot_word(d.D, d.rt, 0, min(lane, d.n_slots - 1), d.n_slots);
+    __builtin_amdgcn_sched_barrier(0);
+    const float* wt = d.w;
+    const float rcp_r = __builtin_amdgcn_rcpf((float)d.R);
+    const int i0 = (int)threadIdx.x, r0 = (int)threadIdx.x;
+    const float w0 = i0 < d.n_slots * d.R ? wt[div_small(i0, rcp_r)] : 0.0f;
+    const size_t orow = (size_t)row0 + r0;
+    const float sh0 = d.shared && r0 < nrows ? d.shared[orow] : 0.0f;
+    const float rs0 = d.resid && r0 < nrows ? d.resid[orow] : 0.0f;
+    const float ac0 = d.accumulate && r0 < nrows ? d.out[orow] : 0.0f;
+    // the codebook table first: this workgroup's weight loads then follow the
+    // gate/up workgroups', whose bytes are needed sooner
+    store_tables<QT, NT>(tabs, load_tables<QT, NT>((int)threadIdx.x), (int)threadIdx.x);
+    const uint8_t* e = resolve_slot_word(d.D, d.rt, sw);
+    const bool bad = __any(e == nullptr);
+    const uint8_t* mine = (e ? e : d.D.base) + (size_t)row0 * rb;
+    auto tile_ptr = [&](int m) { return lane_ptr(mine, m); };
+    TileRun<QT, NT> S{TileWalk<QT, NT>(d.n_slots, nrows, rb, d.d_ff)};
+    tiles_begin(S, tile_ptr);                               // the whole tile in one pass (checked by the host)
+    pass_store(S, stage, leads);
+    __syncthreads();                                        // staged units and table written
+    // While gate/up runs: each lane pair's unit (tile-major, as pass_decode
+    // numbers them; at most one per pair, checked by the host) decoded to
+    // int8 weights in registers, half a unit per lane.
+    const int u = (int)threadIdx.x >> 1, half = (int)threadIdx.x & 1;
+    const bool has = u < S.T.n_mat * S.nv;                  // alike for both lanes of a pair
+    Iq3sHalf W;
+    uint32_t dbits = 0;
+    int ut = 0, ur = 0, us = 0;
+    if (has) {
+        ut = div_small(u, __builtin_amdgcn_rcpf((float)S.nv));
+        const int v = S.v0 + (u - ut * S.nv);
+        ur = div_small(v, S.T.rcp_nus);
+        us = v - ur * S.T.NUS;
+        const uint8_t* unit = stage + 16 * S.cpt * ut + leads[ut] + (int)((size_t)ur * S.T.rb) +
+                              us * UnitFmt<QT>::BYTES - S.b0;
+        uint32_t G[UnitFmt<QT>::NF];
+        iq3s_half_fields(unit, half, G, dbits);
+        iq3s_half_decode(G, tabs, W);
+    }
+    __shared__ int ok;
+    if (threadIdx.x < 64) {
+        const unsigned x = xcc_id();
+        uint32_t* xf = a.sync + kSyncX + kLine * x;
+        bool done;
+        if (dj < kSyncXcds || a.n_d <= kSyncXcds) {
+            done = wait_flags(a.sync, a.n_g, target + a.wait_skew);
+            if (done) {
+                store_flag_line(xf, target);
+            }
+        } else {
+            done = wait_word(xf, target + a.wait_skew);
+        }
+        if (threadIdx.x == 0) ok = done ? 1 : 0;
+    }
+    __syncthreads();                                        // flags seen
+    float* o = d.out + row0;
+    if (!ok) {
+        if (threadIdx.x == 0) *reinterpret_cast<volatile unsigned int*>(d.err) = kErrLayerWait;
+        for (int r = threadIdx.x; r < nrows; r += blockDim.x) o[r] = __builtin_nanf("");
+        if (threadIdx.x == 0) *my = target;
+        return;
+    }
+    const ActBatch hb{d.h, (size_t)d.d_ff, d.n_slots, d.d_ff, act_type(QT), act, P.act_bytes};
+    ActRegs<1> ha;
+    act_prefetch<1>(hb, ha);
+    act_quantize<1>(hb, ha);
+    __syncthreads();                                        // q8 h rows ready
+    if (has) {
+        const uint8_t* arow = act + ut * P.act_bytes;
+        uint32_t A[4][8];
+        act_half(arow + us * kActChunkStride, half, A);
+        int bs = iq3s_half_dot(W, A);
+        bs += (int)dpp<kDppXor1>((uint32_t)bs);             // the partner lane's half
+        if (half == 0) {
+            const ActLayout AL(d.d_ff, QT_Q8_K);
+            part[(ut * d.R + ur) * NCB + us] =
+                __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(arow + AL.off_d)[us]), (float)bs);
+        }
+    }
+    __syncthreads();
+    if (bad) {
+        flag_error(d.err);
+        for (int r = threadIdx.x; r < nrows; r += blockDim.x) o[r] = __builtin_nanf("");
+        if (threadIdx.x == 0) *my = target;
+        return;
+    }
+    // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
+    for (int i = i0; i < d.n_slots * d.R; i += blockDim.x) {
+        const int sl = div_small(i, rcp_r);
+        if (i - sl * d.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : wt[sl]);
+    }
+    __syncthreads();
+    for (int r = r0; r < nrows; r += blockDim.x) {
+        float acc = ordered_sum_from(part[r * NCB], part + r * NCB, d.R * NCB, d.n_slots);
+        const size_t q = (size_t)row0 + r;
+        if (d.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : d.shared[q]);
+        if (d.resid) acc = __fadd_rn(r == r0 ? rs0 : d.resid[q], acc);
+        if (d.accumulate) acc = __fadd_rn(r == r0 ? ac0 : o[r], acc);
+        o[r] = acc;
+    }
+    if (threadIdx.x == 0) *my = target;
+}
+
+// every entry of the lockstep flags to zero (at init, and after a wait ran out)
+__global__ void k_clear_sync(uint32_t* sync) {
+    for (int i = threadIdx.x; i < kSyncWords; i += blockDim.x) sync[i] = 0u;
+}
+
+}  // namespace sabah

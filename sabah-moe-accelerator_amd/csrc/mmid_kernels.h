@@ -263,6 +263,22 @@ __device__ inline float row_sum(const float* part_row, int n) {
     return s;
 }
 
+// acc + v[1] + v[2] + ... + v[n-1] in that order, v[i] = p[i * stride]: the
+// loads of eight terms are issued before their adds, so the chain waits for
+// LDS once per eight terms instead of once per term
+__device__ inline float ordered_sum_from(float acc, const float* p, int stride, int n) {
+    int i = 1;
+    for (; i + 8 <= n; i += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = p[(i + j) * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __fadd_rn(acc, t[j]);
+    }
+    for (; i < n; ++i) acc = __fadd_rn(acc, p[i * stride]);
+    return acc;
+}
+
 // One workgroup's tiles.  Tile t is matrix tile_ptr(t) from its first row on
 // (row0 already folded into the pointer): `nrows` rows of k elements at rb
 // bytes, so its unit v = r * NUS + us sits at byte r * rb + us * unit bytes.
@@ -629,19 +645,27 @@ constexpr int kGateUpRoundThreads = 2 * kThreads;
 // dynamic LDS of a launch: the plan, then the staging regions
 __host__ __device__ inline int gate_up_rounds_lds(const Plan& P, int stage) { return align16i(P.bytes) + stage; }
 
-template <int QT, int NT, int PER = 2>
-__global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
+// h row r of a workgroup: a plain store, or (publish) an agent-scope store
+// written through to memory, so a workgroup of the same grid on another XCD
+// can read it once this one has waited for its stores and set its flag
+__device__ inline void store_h(float* p, float v, bool publish) {
+    if (publish) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
+// One workgroup of k_gate_up_rounds: token t, slot s, rows row0 .. row0 + R.
+// tabs: the IQ3_S table (kLdsTables bytes); smem: the plan's dynamic LDS;
+// stage: the waves' staging regions (GateUpRounds::STAGE bytes).
+template <int QT, int NT, int PER>
+__device__ inline void gate_up_rounds_tile(const GateUpArgs& a, int t, int s, int row0, uint8_t* tabs, uint8_t* smem,
+                                           uint8_t* stage, bool publish) {
     using GR = GateUpRounds<QT, NT, PER>;
     constexpr int UB = UnitFmt<QT>::BYTES;
     constexpr int UPW = GR::UPW, WPM = GR::WPM, RD = GR::RD;
     constexpr int WCH = GR::WCH, N = WaveRoundChunks<QT, PER>::LOADS;
     static_assert(PER == 1 || QT == QT_IQ3_S, "split units are IQ3_S only");
-    __shared__ __align__(16) uint8_t tabs[QT == QT_IQ3_S ? kLdsTables : 16];
-    extern __shared__ __align__(16) uint8_t smem[];
     const int NUS = units_per_row(QT, a.d_model), NCB = contribs_per_row(QT, a.d_model);
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * NCB);
-    uint8_t* const stage = smem + align16i(P.bytes);
-    const int t = blockIdx.z, s = blockIdx.y, row0 = blockIdx.x * a.R;
     const int nrows = min(a.R, a.d_ff - row0);
     const size_t rb = row_bytes(QT, a.d_model);
     float* h = a.h + ((size_t)t * a.n_slots + s) * a.d_ff + row0;
@@ -656,7 +680,7 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) h[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += blockDim.x) store_h(h + r, __builtin_nanf(""), publish);
         return;
     }
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63u);
@@ -729,8 +753,17 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
-        h[r] = __fmul_rn(silu_f32(g), up);
+        store_h(h + r, __fmul_rn(silu_f32(g), up), publish);
     }
+}
+
+template <int QT, int NT, int PER = 2>
+__global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
+    __shared__ __align__(16) uint8_t tabs[QT == QT_IQ3_S ? kLdsTables : 16];
+    extern __shared__ __align__(16) uint8_t smem[];
+    const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * contribs_per_row(QT, a.d_model));
+    gate_up_rounds_tile<QT, NT, PER>(a, blockIdx.z, blockIdx.y, blockIdx.x * a.R, tabs, smem, smem + align16i(P.bytes),
+                                     false);
 }
 
 // ---------------------------------------------------------------------------
@@ -839,8 +872,7 @@ __global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_down_combine(DownArg
     __syncthreads();
     for (int r = r0; r < nrows; r += blockDim.x) {
         const size_t q = (size_t)t * a.d_model + row0 + r;
-        float acc = part[r * NCB];
-        for (int s = 1; s < a.n_slots; ++s) acc = __fadd_rn(acc, part[(s * a.R + r) * NCB]);
+        float acc = ordered_sum_from(part[r * NCB], part + r * NCB, a.R * NCB, a.n_slots);
         if (a.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : a.shared[q]);
         if (a.resid) acc = __fadd_rn(r == r0 ? rs0 : a.resid[q], acc);
         if (a.accumulate) acc = __fadd_rn(r == r0 ? ac0 : o[r], acc);

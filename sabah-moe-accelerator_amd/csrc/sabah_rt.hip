@@ -18,6 +18,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "layer_kernels.h"
 #include "mmid_kernels.h"
 #include "prefill_kernels.h"
 #include "route_kernels.h"
@@ -28,9 +29,13 @@
 
 using namespace sabah;
 
-// the no-alloc layer's scratch (sabah_moe_layer_noalloc): 8 MiB per GPU
+// The library's static device array, one per GPU: the fused decode layer's
+// lockstep flags (k_layer_decode; persistent, cleared at init), then the
+// 8 MiB arena of sabah_moe_layer_noalloc's per-call scratch.
 constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
-static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr size_t kSyncBytes = (size_t)kSyncWords * 4;
+static_assert(kSyncBytes % 256 == 0, "the arena after the flags stays 256-byte aligned");
+static __device__ __align__(256) uint8_t scratch[kSyncBytes + kNoAllocScratchBytes];
 
 namespace {
 
@@ -69,7 +74,8 @@ uint16_t* g_nearest_dev = nullptr;   // IQ3_S encoder table, uploaded on first u
 // kind (the reference's SABAH_LLAMA_EVENTS probe, sabah_rt.cu:118-151): each
 // dispatch records its own start/stop event pair (launch_kernel); elapsed
 // times are collected when the caller asks for them.
-enum KernelKind { KK_MMID = 0, KK_GATE_UP = 1, KK_DOWN = 2, KK_CHAIN = 3, KK_GGATE_UP = 4, KK_GDOWN = 5, KK_COUNT = 6 };
+enum KernelKind { KK_MMID = 0, KK_GATE_UP = 1, KK_DOWN = 2, KK_CHAIN = 3, KK_GGATE_UP = 4, KK_GDOWN = 5, KK_LAYER = 6,
+                  KK_COUNT = 7 };
 struct EvPair {
     hipEvent_t a, b;
     int kind;
@@ -155,12 +161,23 @@ void* grow_scratch(Scratch& s, size_t bytes, hipStream_t stream) {
     return s.p;
 }
 
-// Scratch of sabah_moe_layer_noalloc: the fixed device array `scratch`, which
-// each GPU the library runs on holds until the process ends.  In host code
-// its name is a host-side stand-in, not a device address: host code uses
+// The fixed device array `scratch`, which each GPU the library runs on holds
+// until the process ends: its flags (g_layer_sync) and its arena
+// (g_noalloc_scratch, sabah_moe_layer_noalloc's scratch).  In host code the
+// array's name is a host-side stand-in, not a device address: host code uses
 // only the address hipGetSymbolAddress gives at sabah_rt_init, kept per device.
 constexpr int kMaxDevices = 64;
 void* g_noalloc_scratch[kMaxDevices] = {};
+uint32_t* g_layer_sync[kMaxDevices] = {};
+// 1 (default): one-token IQ3_S layers run as one fused launch
+// (k_layer_decode) when eligible; 0: always the two-kernel form.  The
+// results are bit-identical; on the 48-layer decode the fused launch
+// measured 1,510 GB/s against 1,433 - 1,449 (same box, interleaved runs).
+std::atomic<int> g_layer_fusion{1};
+// set when a fused launch's wait ran out: the next fused launch first clears the flags
+bool g_sync_reset_pending = false;
+// one-shot test of the timeout path (sabah_rt_set_layer_fusion(2))
+bool g_layer_wait_test = false;
 
 // LDS a workgroup may allocate (the device's limit: 160 KB on gfx950)
 int g_max_lds = 65536;
@@ -215,13 +232,18 @@ int rows_down(int qt, int k, int n_slots, int d_model, int n_tokens) {
 }
 
 bool check_sticky() {
-    if (g_err_host && __atomic_load_n(g_err_host, __ATOMIC_ACQUIRE) != 0) {
-        __atomic_store_n(g_err_host, 0u, __ATOMIC_RELEASE);
+    const unsigned int w = g_err_host ? __atomic_load_n(g_err_host, __ATOMIC_ACQUIRE) : 0u;
+    if (w == 0) return true;
+    __atomic_store_n(g_err_host, 0u, __ATOMIC_RELEASE);
+    if (w == kErrLayerWait) {
+        g_sync_reset_pending = true;
+        fail("an earlier fused layer kernel's down workgroups waited too long for its gate/up workgroups "
+             "(calls overlapping on different streams?); their rows were set to NaN");
+    } else {
         fail("an earlier expert kernel read an expert id outside [0, n_experts); "
              "its slot outputs were set to NaN");
-        return false;
     }
-    return true;
+    return false;
 }
 
 // Resolve a MUL_MAT_ID source to device memory: a registered bank range, or a
@@ -394,10 +416,15 @@ SABAH_API int sabah_rt_init(int device) {
     if (!ck(hipHostGetDevicePointer(reinterpret_cast<void**>(&g_err_dev), g_err_host, 0), "sticky error word map"))
         return -1;
     if (device >= 0 && device < kMaxDevices && !g_noalloc_scratch[device]) {
-        static_assert(sizeof(scratch) == kNoAllocScratchBytes, "the static scratch array has its stated size");
+        static_assert(sizeof(scratch) == kSyncBytes + kNoAllocScratchBytes, "the static array has its stated size");
         void* p = nullptr;
         if (!ck(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address")) return -1;
-        g_noalloc_scratch[device] = p;
+        uint32_t* flags = static_cast<uint32_t*>(p);
+        hipLaunchKernelGGL(k_clear_sync, dim3(1), dim3(256), 0, g_stream, flags);
+        if (!ck(hipGetLastError(), "layer flags clear") || !ck(hipStreamSynchronize(g_stream), "layer flags clear sync"))
+            return -1;
+        g_layer_sync[device] = flags;
+        g_noalloc_scratch[device] = static_cast<uint8_t*>(p) + kSyncBytes;
     }
     g_device = device;
     return 0;
@@ -441,6 +468,21 @@ SABAH_API int sabah_rt_check_errors(void) { return check_sticky() ? 0 : -1; }
 
 SABAH_API int sabah_rt_set_kernel_timing(int on) {
     g_timing = on != 0;
+    return 0;
+}
+
+// 1 (default): one-token IQ3_S layers run as one fused launch when
+// eligible; 0: always gate/up then down + combine.  The results are
+// bit-identical.
+// 2: as 1, and the next fused launch tests its timeout path: its down
+// workgroups wait for a flag value that no workgroup writes, so their
+// bounded wait runs out (2 ms), their rows become NaN and the next call
+// fails with the message; the flags are then cleared before the next fused
+// launch.
+SABAH_API int sabah_rt_set_layer_fusion(int mode) {
+    if (mode < 0 || mode > 2) return fail("layer fusion mode %d outside {0 off, 1 on, 2 on + timeout test}", mode);
+    g_layer_fusion.store(mode == 0 ? 0 : 1);
+    g_layer_wait_test = mode == 2;
     return 0;
 }
 
@@ -934,6 +976,52 @@ static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_
     return ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch") ? 0 : -1;
 }
 
+// A one-token IQ3_S layer as one launch (k_layer_decode) when it applies:
+// returns 1 when launched, 0 when the two-kernel form must run, -1 on error.
+static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, const ExpertSrc& DS, const Routing& rt,
+                       int n_used, const float* w, const float* shared, const float* resid, float* out,
+                       hipStream_t st) {
+    constexpr int QT = QT_IQ3_S;
+    if (!g_layer_fusion.load() || g_device < 0 || g_device >= kMaxDevices || !g_layer_sync[g_device]) return 0;
+    if (L->qt_gate != QT || L->qt_up != QT || L->qt_down != QT) return 0;
+    const int D = L->d_model, F = L->d_ff;
+    if (!gate_up_rounds_ok(QT, D) || gu.R != rows_gate_up_rounds(QT, D) || F % 256) return 0;
+    static_assert(GateUpRounds<QT, kLayerThreads, 2>::STAGE <= kStageBytes, "gate/up rounds stage in the static area");
+    DownArgs dn{};
+    dn.D = DS;
+    dn.rt = rt;
+    dn.h = gu.h;
+    dn.w = w;
+    dn.shared = shared;
+    dn.resid = resid;
+    dn.out = out;
+    dn.n_slots = n_used;
+    dn.d_model = D;
+    dn.d_ff = F;
+    dn.R = rows_down(QT, F, n_used, D, 1);
+    dn.err = g_err_dev;
+    const int g_tiles = (F + gu.R - 1) / gu.R;
+    const int n_g = g_tiles * n_used, n_d = (D + dn.R - 1) / dn.R;
+    if (n_g > kSyncG || n_d > kSyncD) return 0;
+    // the down workgroup's tiles stage in one pass (TileWalk's pass size at kLayerThreads threads)
+    const int cap = std::min(kStageChunks / n_used, stage_iters_nt(QT, kLayerThreads) * (kLayerThreads / n_used));
+    if (dn.R * units_per_row(QT, F) > std::max(1, (16 * cap - 30) / UnitFmt<QT>::BYTES)) return 0;
+    // at most one unit per lane pair: each lane holds its decoded half unit
+    if (n_used * dn.R * units_per_row(QT, F) > kLayerThreads / 2) return 0;
+    const int dyn = layer_dyn_lds(gu, dn);
+    if (StaticLds<QT>::BYTES + dyn + 64 > g_max_lds) return 0;
+    if (!ck(fit_lds(k_layer_decode<kLayerThreads>, dyn, StaticLds<QT>::BYTES + dyn), "fused layer LDS")) return -1;
+    uint32_t* sync = g_layer_sync[g_device];
+    if (g_sync_reset_pending) {
+        launch_kernel(KK_LAYER, k_clear_sync, dim3(1), dim3(256), 0, st, sync);
+        g_sync_reset_pending = false;
+    }
+    LayerArgs a{gu, dn, n_g, g_tiles, n_d, sync, g_layer_wait_test ? 1u : 0u};
+    g_layer_wait_test = false;
+    launch_kernel(KK_LAYER, k_layer_decode<kLayerThreads>, dim3((unsigned)(n_g + n_d)), dim3(kLayerThreads), dyn, st, a);
+    return ck(hipGetLastError(), "fused layer launch") ? 1 : -1;
+}
+
 static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const int32_t* d_ids, const float* d_w,
                         int n_used, int n_tokens, float* d_out, const float* d_resid, Workspace& ws, hipStream_t st) {
     const int D = L->d_model, F = L->d_ff;
@@ -953,6 +1041,10 @@ static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const i
     gu.R = rows_gate_up(L->qt_gate, D, F, n_used, n_tokens);
     gu.err = g_err_dev;
     const ExpertSrc DS{reinterpret_cast<const uint8_t*>(L->down), nullptr, row_bytes(L->qt_down, F) * (size_t)D};
+    if (n_tokens == 1) {
+        const int f = layer_fused(L, gu, DS, rt, n_used, d_w, b.ys, d_resid, d_out, st);
+        if (f) return f > 0 ? 0 : -1;
+    }
     return run_layer(gu, L->qt_gate, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, b.ys, d_resid, d_out, 0, b.hq,
                      st);
 }

@@ -358,6 +358,29 @@ __device__ inline int iq3s_half_bsum(const uint32_t (&G)[27], const uint8_t* sme
     return bsum;
 }
 
+// The same sum in two steps: the weights of the half decoded to int8 first
+// (no activations needed), dotted with them later.  The integer sum is the
+// same as iq3s_half_bsum's.
+struct Iq3sHalf {
+    uint32_t v[4][8];       // int8 weights of items 0..3 of the half
+    int ls[4];              // their scales 2 * nibble + 1
+};
+__device__ inline void iq3s_half_decode(const uint32_t (&G)[27], const uint8_t* smem, Iq3sHalf& W) {
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) W.ls[ib] = iq3s_item(G, ib, smem, W.v[ib]);
+}
+__device__ inline int iq3s_half_dot(const Iq3sHalf& W, const uint32_t (&A)[4][8]) {
+    int bsum = 0;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = sdot4(W.v[ib][i], A[ib][i], s);
+        bsum += __mul24(W.ls[ib], s);
+    }
+    return bsum;
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K: element 32j + l = d*sc_j*nib - dmin*m_j, nibble low (j even) / high (j
 // odd) of qs[32*(j/2) + l].  F[0] = d | dmin << 16, F[1..3] packed 6-bit

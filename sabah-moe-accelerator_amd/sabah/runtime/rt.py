@@ -92,10 +92,11 @@ EXTRA_SIGNATURES = {
     "sabah_sync_compute": ([], c_i),
     "sabah_synth_weights": ([c_vp, c_i, ctypes.c_longlong, c_i, ctypes.c_ulonglong, ctypes.c_float, c_vp], c_i),
     "sabah_rt_set_kernel_timing": ([c_i], c_i),
+    "sabah_rt_set_layer_fusion": ([c_i], c_i),
     "sabah_rt_get_kernel_timing": ([c_i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_u64), c_i], c_i),
 }
 
-KERNEL_KINDS = {"mmid": 0, "gate_up": 1, "down": 2, "chain": 3, "grouped_gate_up": 4, "grouped_down": 5}
+KERNEL_KINDS = {"mmid": 0, "gate_up": 1, "down": 2, "chain": 3, "grouped_gate_up": 4, "grouped_down": 5, "layer": 6}
 
 
 def kernel_timing(kind: str, reset: bool = False) -> tuple[float, int]:
