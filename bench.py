@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--pool", type=int, default=128, help="distinct tokens rotated through the steps")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU time of the cpu_baseline sample")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0: every CPU this process may run on (OMP_NUM_THREADS when set: the host's CPU share)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layer-fusion", type=int, default=1, choices=(0, 1),
                     help="1 (the library's default): one fused launch per layer; 0: gate/up then down + combine")
@@ -375,7 +376,7 @@ def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid=False):
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads = cpu_threads(args)
     n = 8
     e_ids = ids_np[0, :n]
     used = np.unique(e_ids)
@@ -401,7 +402,8 @@ def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid=False):
     return {"value": round(tokens * W.top_k * W.expert_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "tok_s": round(tokens / dt, 2),
             "sample": "%d tokens of the batch, their %d routed experts read back from HBM, %.1f s "
-                      "(token-major: each (token, slot) reads its expert)" % (tokens, len(used), dt)}
+                      "(token-major: each (token, slot) reads its expert)" % (tokens, len(used), dt),
+            "host": host_info(threads)}
 
 
 def measured_traffic(workload, kind):
@@ -419,6 +421,38 @@ def measured_traffic(workload, kind):
     return None
 
 
+def cpu_threads(args):
+    """Threads of the CPU baseline: --cpu-threads, else OMP_NUM_THREADS (the
+    CPU share a shared host grants this process), else every CPU in this
+    process's affinity mask."""
+    if args.cpu_threads:
+        return args.cpu_threads
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+def host_info(threads):
+    """What the CPU baseline ran on: model, logical CPUs, this process's
+    affinity, NUMA nodes, and the thread count used."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        nodes = len([d for d in os.listdir("/sys/devices/system/node") if d.startswith("node") and d[4:].isdigit()])
+    except OSError:
+        nodes = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "numa_nodes": nodes, "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"), "threads_used": threads}
+
+
 def cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np, dev):
     """The oracle (C restatement of ggml's CPU MUL_MAT_ID path) on this host's
     cores, over the routed experts of one decode token read back from HBM, and
@@ -428,7 +462,7 @@ def cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np, dev):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads = cpu_threads(args)
     p = 0
     layers = []
     for l in range(W.n_layers):
@@ -449,23 +483,30 @@ def cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np, dev):
     parity = {"layer": 0, "max_rel": float(np.abs(d).max() / np.abs(r).max()),
               "cos": float((got.ravel() @ r) / np.sqrt((got.ravel() @ got.ravel()) * (r @ r))),
               "tolerance": {"max_rel": 1e-3, "cos": 0.99999}}
-    # timing: whole tokens (48 chained layers) until the target CPU time is reached
-    t0 = time.perf_counter()
-    tokens = 0
-    nbytes = 0
-    while True:
-        x = x0.copy()
-        for sub, lid, lw in layers:
-            x = x + O.moe_layer(sub["gate"], sub["up"], sub["down"], qts, x, lid, lw, n_threads=threads)
-            nbytes += len(np.unique(lid)) * W.expert_bytes()
-        tokens += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    dt = time.perf_counter() - t0
+    # timing: whole tokens (48 chained layers) until the target CPU time is
+    # reached, with every thread of the host's share and with one thread
+    def time_tokens(nt, seconds):
+        t0 = time.perf_counter()
+        tokens = nbytes = 0
+        while True:
+            x = x0.copy()
+            for sub, lid, lw in layers:
+                x = x + O.moe_layer(sub["gate"], sub["up"], sub["down"], qts, x, lid, lw, n_threads=nt)
+                nbytes += len(np.unique(lid)) * W.expert_bytes()
+            tokens += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        return tokens, nbytes, time.perf_counter() - t0
+
+    tokens, nbytes, dt = time_tokens(threads, args.cpu_seconds)
+    tok1, nb1, dt1 = time_tokens(1, args.cpu_seconds / 3)
     cpu = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
            "tok_s": round(tokens / dt, 3),
            "sample": "%d decode token(s) x %d layers (%.0f MB of routed expert bytes read back from HBM), %.1f s"
-                     % (tokens, W.n_layers, nbytes / tokens / 1e6, dt)}
+                     % (tokens, W.n_layers, nbytes / tokens / 1e6, dt),
+           "one_thread": {"value": round(nb1 / dt1 / 1e9, 3), "unit": "GB/s", "tok_s": round(tok1 / dt1, 3),
+                          "sample": "%d decode token(s), %.1f s" % (tok1, dt1)},
+           "host": host_info(threads)}
     return cpu, parity
 
 

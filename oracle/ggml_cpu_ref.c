@@ -816,68 +816,129 @@ int orc_mul_mat_id(const void *source, size_t expert_stride, size_t row_stride,
 /* ------------------------------------------------------------------------ */
 static inline float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
-/* dense y[r] = W[r] . q(x) for r < rows (ggml MUL_MAT with the same vec_dot) */
-static void dense_matvec(const uint8_t *W, int qt, int rows, int k, const float *x, float *y, int nt) {
-    const size_t rb = orc_row_bytes(qt, k);
-    uint8_t *act = (uint8_t *)malloc(orc_act_row_bytes(qt, k));
-    orc_quantize_act(qt, x, act, k);
-    #pragma omp parallel for num_threads(nt) schedule(static)
-    for (int r = 0; r < rows; ++r) y[r] = orc_vec_dot(qt, W + (size_t)r * rb, act, k);
-    free(act);
-}
-
+/* One MoE layer as ggml's graph computes it (qwen4exp.cpp:848-892): x
+ * quantised to the gate/up vec_dot type once per token; the gate and up
+ * MUL_MAT_IDs over every (token, slot, row); h = silu(g) * u; h quantised to
+ * the down vec_dot type once per (token, slot); the down MUL_MAT_ID; then per
+ * token the router-weighted sum over the slots in slot order and the
+ * (optionally sigmoid-gated) shared expert.  The phases run inside one
+ * OpenMP parallel region (one fork per call); every value is computed by one
+ * thread in the order stated, so the result does not depend on the thread
+ * count. */
 int orc_moe_layer(const orc_moe_layer_desc *L, const float *x, const int32_t *ids,
                   const float *w, int n_used, int n_tokens, float *out, float *h_out, int n_threads) {
-    const int D = L->d_model, F = L->d_ff;
+    const int D = L->d_model, F = L->d_ff, T = n_tokens, K = n_used;
     const size_t rbg = orc_row_bytes(L->qt_gate, D), rbu = orc_row_bytes(L->qt_up, D);
     const size_t rbd = orc_row_bytes(L->qt_down, F);
-    if (!rbg || !rbu || !rbd || n_used <= 0) return -1;
-    for (int p = 0; p < n_tokens * n_used; ++p)
+    if (!rbg || !rbu || !rbd || K <= 0 || T < 0) return -1;
+    for (int p = 0; p < T * K; ++p)
         if (ids[p] < 0 || ids[p] >= L->n_experts) return -1;
+    if (T == 0) return 0;
     const int nt = threads_or_default(n_threads);
     const size_t esg = rbg * (size_t)F, esu = rbu * (size_t)F, esd = rbd * (size_t)D;
-    float *g = (float *)malloc(sizeof(float) * (size_t)F);
-    float *u = (float *)malloc(sizeof(float) * (size_t)F);
-    float *h = (float *)malloc(sizeof(float) * (size_t)F * n_used);
-    float *y = (float *)malloc(sizeof(float) * (size_t)D * n_used);
-    for (int t = 0; t < n_tokens; ++t) {
-        const float *xt = x + (size_t)t * D;
-        for (int s = 0; s < n_used; ++s) {
-            const int e = ids[t * n_used + s];
-            dense_matvec((const uint8_t *)L->gate + (size_t)e * esg, L->qt_gate, F, D, xt, g, nt);
-            dense_matvec((const uint8_t *)L->up + (size_t)e * esu, L->qt_up, F, D, xt, u, nt);
-            float *hs = h + (size_t)s * F;
-            for (int j = 0; j < F; ++j) hs[j] = silu_f32(g[j]) * u[j];
-            dense_matvec((const uint8_t *)L->down + (size_t)e * esd, L->qt_down, D, F, hs, y + (size_t)s * D, nt);
-        }
-        if (h_out) memcpy(h_out + (size_t)t * n_used * F, h, sizeof(float) * (size_t)F * n_used);
-        float *ot = out + (size_t)t * D;
-        for (int i = 0; i < D; ++i) {
-            float acc = y[i] * w[t * n_used + 0];
-            for (int s = 1; s < n_used; ++s) acc = acc + y[(size_t)s * D + i] * w[t * n_used + s];
-            ot[i] = acc;
-        }
-        if (L->shared_gate) {
-            const int Fs = L->d_ff_shared;
-            float *gs = (float *)malloc(sizeof(float) * (size_t)Fs);
-            float *us = (float *)malloc(sizeof(float) * (size_t)Fs);
-            float *ys = (float *)malloc(sizeof(float) * (size_t)D);
-            dense_matvec((const uint8_t *)L->shared_gate, L->qt_shared_gate, Fs, D, xt, gs, nt);
-            dense_matvec((const uint8_t *)L->shared_up, L->qt_shared_up, Fs, D, xt, us, nt);
-            for (int j = 0; j < Fs; ++j) gs[j] = silu_f32(gs[j]) * us[j];
-            dense_matvec((const uint8_t *)L->shared_down, L->qt_shared_down, D, Fs, gs, ys, nt);
-            if (L->shared_gate_inp) {
-                double dot = 0.0;
-                for (int i = 0; i < D; ++i) dot += (double)L->shared_gate_inp[i] * (double)xt[i];
-                const float gl = (float)dot;
-                const float g = 1.0f / (1.0f + expf(-gl));       /* ggml_vec_sigmoid_f32 */
-                for (int i = 0; i < D; ++i) ys[i] = ys[i] * g;
+    const size_t abg = orc_act_row_bytes(L->qt_gate, D), abu = orc_act_row_bytes(L->qt_up, D);
+    const size_t abd = orc_act_row_bytes(L->qt_down, F);
+    const int P = T * K;
+    const int Fs = L->shared_gate ? L->d_ff_shared : 0;
+    const size_t abs_g = Fs ? orc_act_row_bytes(L->qt_shared_gate, D) : 0;
+    const size_t abs_u = Fs ? orc_act_row_bytes(L->qt_shared_up, D) : 0;
+    const size_t abs_d = Fs ? orc_act_row_bytes(L->qt_shared_down, Fs) : 0;
+    const size_t rbs_g = Fs ? orc_row_bytes(L->qt_shared_gate, D) : 0, rbs_u = Fs ? orc_row_bytes(L->qt_shared_up, D) : 0;
+    const size_t rbs_d = Fs ? orc_row_bytes(L->qt_shared_down, Fs) : 0;
+    uint8_t *xg = (uint8_t *)malloc(abg * (size_t)T), *xu = (uint8_t *)malloc(abu * (size_t)T);
+    float *g = (float *)malloc(sizeof(float) * (size_t)P * F), *u = (float *)malloc(sizeof(float) * (size_t)P * F);
+    uint8_t *hq = (uint8_t *)malloc(abd * (size_t)P);
+    float *y = (float *)malloc(sizeof(float) * (size_t)P * D);
+    uint8_t *xsg = Fs ? (uint8_t *)malloc(abs_g * (size_t)T) : NULL, *xsu = Fs ? (uint8_t *)malloc(abs_u * (size_t)T) : NULL;
+    float *gs = Fs ? (float *)malloc(sizeof(float) * (size_t)T * Fs) : NULL;
+    float *us = Fs ? (float *)malloc(sizeof(float) * (size_t)T * Fs) : NULL;
+    uint8_t *hsq = Fs ? (uint8_t *)malloc(abs_d * (size_t)T) : NULL;
+    float *ys = Fs ? (float *)malloc(sizeof(float) * (size_t)T * D) : NULL;
+    #pragma omp parallel num_threads(nt)
+    {
+        #pragma omp for schedule(static)
+        for (int t = 0; t < T; ++t) {
+            const float *xt = x + (size_t)t * D;
+            orc_quantize_act(L->qt_gate, xt, xg + (size_t)t * abg, D);
+            orc_quantize_act(L->qt_up, xt, xu + (size_t)t * abu, D);
+            if (Fs) {
+                orc_quantize_act(L->qt_shared_gate, xt, xsg + (size_t)t * abs_g, D);
+                orc_quantize_act(L->qt_shared_up, xt, xsu + (size_t)t * abs_u, D);
             }
-            for (int i = 0; i < D; ++i) ot[i] = ot[i] + ys[i];
-            free(gs); free(us); free(ys);
+        }
+        /* gate and up MUL_MAT_ID: (token, slot, row) */
+        #pragma omp for schedule(static)
+        for (long q = 0; q < (long)P * F; ++q) {
+            const int p = (int)(q / F), j = (int)(q % F), t = p / K;
+            const int e = ids[p];
+            g[q] = orc_vec_dot(L->qt_gate, (const uint8_t *)L->gate + (size_t)e * esg + (size_t)j * rbg, xg + (size_t)t * abg, D);
+            u[q] = orc_vec_dot(L->qt_up, (const uint8_t *)L->up + (size_t)e * esu + (size_t)j * rbu, xu + (size_t)t * abu, D);
+        }
+        if (Fs) {
+            #pragma omp for schedule(static)
+            for (long q = 0; q < (long)T * Fs; ++q) {
+                const int t = (int)(q / Fs), j = (int)(q % Fs);
+                gs[q] = orc_vec_dot(L->qt_shared_gate, (const uint8_t *)L->shared_gate + (size_t)j * rbs_g, xsg + (size_t)t * abs_g, D);
+                us[q] = orc_vec_dot(L->qt_shared_up, (const uint8_t *)L->shared_up + (size_t)j * rbs_u, xsu + (size_t)t * abs_u, D);
+            }
+        }
+        /* h = silu(g) * u (ggml_swiglu), then h -> the down vec_dot type per (token, slot) */
+        #pragma omp for schedule(static)
+        for (int p = 0; p < P; ++p) {
+            float *hp = g + (size_t)p * F;
+            const float *up = u + (size_t)p * F;
+            for (int j = 0; j < F; ++j) hp[j] = silu_f32(hp[j]) * up[j];
+            orc_quantize_act(L->qt_down, hp, hq + (size_t)p * abd, F);
+        }
+        if (Fs) {
+            #pragma omp for schedule(static)
+            for (int t = 0; t < T; ++t) {
+                float *hp = gs + (size_t)t * Fs;
+                const float *up = us + (size_t)t * Fs;
+                for (int j = 0; j < Fs; ++j) hp[j] = silu_f32(hp[j]) * up[j];
+                orc_quantize_act(L->qt_shared_down, hp, hsq + (size_t)t * abs_d, Fs);
+            }
+        }
+        /* down MUL_MAT_ID: (token, slot, row) */
+        #pragma omp for schedule(static)
+        for (long q = 0; q < (long)P * D; ++q) {
+            const int p = (int)(q / D), i = (int)(q % D);
+            y[q] = orc_vec_dot(L->qt_down, (const uint8_t *)L->down + (size_t)ids[p] * esd + (size_t)i * rbd,
+                               hq + (size_t)p * abd, F);
+        }
+        if (Fs) {
+            #pragma omp for schedule(static)
+            for (long q = 0; q < (long)T * D; ++q) {
+                const int t = (int)(q / D), i = (int)(q % D);
+                ys[q] = orc_vec_dot(L->qt_shared_down, (const uint8_t *)L->shared_down + (size_t)i * rbs_d,
+                                    hsq + (size_t)t * abs_d, Fs);
+            }
+        }
+        /* combine: sum over the slots in slot order, then the shared expert */
+        #pragma omp for schedule(static)
+        for (int t = 0; t < T; ++t) {
+            float *ot = out + (size_t)t * D;
+            const float *yt = y + (size_t)t * K * D;
+            for (int i = 0; i < D; ++i) {
+                float acc = yt[i] * w[t * K + 0];
+                for (int s2 = 1; s2 < K; ++s2) acc = acc + yt[(size_t)s2 * D + i] * w[t * K + s2];
+                ot[i] = acc;
+            }
+            if (Fs) {
+                const float *yst = ys + (size_t)t * D;
+                float gl = 1.0f;
+                if (L->shared_gate_inp) {
+                    double dot = 0.0;
+                    for (int i = 0; i < D; ++i) dot += (double)L->shared_gate_inp[i] * (double)x[(size_t)t * D + i];
+                    gl = 1.0f / (1.0f + expf(-(float)dot));       /* ggml_vec_sigmoid_f32 */
+                }
+                for (int i = 0; i < D; ++i) ot[i] = ot[i] + (L->shared_gate_inp ? yst[i] * gl : yst[i]);
+            }
         }
     }
-    free(g); free(u); free(h); free(y);
+    if (h_out) memcpy(h_out, g, sizeof(float) * (size_t)P * F);
+    free(xg); free(xu); free(g); free(u); free(hq); free(y);
+    free(xsg); free(xsu); free(gs); free(us); free(hsq); free(ys);
     return 0;
 }
 

@@ -257,9 +257,26 @@ __device__ inline void unit_into_part(const LdsWindow<QT>& Wn, const uint8_t* ta
     }
 }
 
+// the n block terms of a row summed in block order from zero (ggml's
+// vec_dot); the loads of eight terms are issued before their adds
 __device__ inline float row_sum(const float* part_row, int n) {
     float s = 0.0f;
-    for (int b = 0; b < n; ++b) s = __fadd_rn(s, part_row[b]);
+    int b = 0;
+    for (; b + 8 <= n; b += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = part_row[b + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = __fadd_rn(s, t[j]);
+    }
+    if (b < n) {                                            // the last 1..7 terms, also loaded first
+        float t[7];
+#pragma unroll
+        for (int j = 0; j < 7; ++j) t[j] = b + j < n ? part_row[b + j] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 7; ++j)
+            if (b + j < n) s = __fadd_rn(s, t[j]);
+    }
     return s;
 }
 
