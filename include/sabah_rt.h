@@ -120,6 +120,60 @@ int sabah_rt_snapshot(char *buf, size_t n);
 
 /* ---- harness entry points ----------------------------------------------- */
 
+/* Device memory, pinned host memory, copies, events and the two library
+ * streams, for the Python harness: the reference's rt.lib() binds these by
+ * name (sabah/runtime/rt.py:70-107) and its executor, expert bank and hot
+ * tier call them.  Same names, signatures and return conventions as
+ * sabah_rt.cu:3240-3353: allocators return NULL on failure (message in
+ * sabah_rt_last_error); int calls return 0 / -1; sabah_event_query returns
+ * 1 (complete), 0 (in flight) or -1; sabah_event_elapsed_ms waits for b and
+ * returns -1 on error.  The copy stream is the library's second stream
+ * (sabah_h2d_async, sabah_event_record_copy, sabah_copy_wait_event); the
+ * compute stream is the one sabah_moe_block and sabah_dequant use.
+ * sabah_host_alloc returns pinned memory from hipHostMalloc (the reference
+ * pools and reuses its pinned blocks; here each call allocates). */
+void *sabah_dev_alloc(size_t bytes);
+void sabah_dev_free(void *p);
+void *sabah_host_alloc(size_t bytes);
+void sabah_host_free(void *p);
+int sabah_dev_mem(size_t *free_bytes, size_t *total_bytes);
+int sabah_memcpy_h2d(void *dst, const void *src, size_t n);
+int sabah_memcpy_d2h(void *dst, const void *src, size_t n);
+int sabah_memset_d(void *dst, int v, size_t n);
+int sabah_h2d_async(void *dst, const void *src, size_t n);
+void *sabah_event_create(void);
+void sabah_event_destroy(void *ev);
+int sabah_event_record_copy(void *ev);
+int sabah_event_record_compute(void *ev);
+int sabah_compute_wait_event(void *ev);
+int sabah_copy_wait_event(void *ev);
+float sabah_event_elapsed_ms(void *a, void *b);
+int sabah_event_sync(void *ev);
+int sabah_event_query(void *ev);
+int sabah_sync_copy(void);
+int sabah_sync_compute(void);
+int sabah_sync_all(void);
+
+/* A device slab: one allocation of capacity_bytes whose ranges are handed
+ * out (256-byte aligned) and returned.  Replaces sabah_slab_* (sabah_rt.cu:
+ * 3889-3903, allocator 332-420), which backs the reference's VRAM tier; the
+ * HBM-resident bank needs no tier, and the slab remains for harness callers.
+ * init on an existing slab is a no-op; alloc returns NULL when no free range
+ * fits; free merges the range with its free neighbours. */
+int sabah_slab_init(size_t capacity_bytes);
+void *sabah_slab_alloc(size_t bytes);
+void sabah_slab_free(void *ptr);
+void sabah_slab_destroy(void);
+
+/* n elements of type qt (a whole number of blocks) at host address src,
+ * decoded into n floats at host address dst.  Replaces sabah_rt_host_dequant
+ * (sabah_rt.cu:3845-3847), whose decoders run on the host; here the bytes are
+ * decoded on the device by the same decoders as sabah_dequant.  Synchronous;
+ * callable before sabah_rt_init, like the reference's (the library is then
+ * initialised on the current HIP device).  Returns -1 for an unsupported type
+ * or a partial block. */
+int sabah_rt_host_dequant(const void *src, float *dst, int qt, int n);
+
 /* Bytes of one row of n elements of type qt (0 if unsupported or n is not a
  * whole number of blocks).  Replaces sabah_row_bytes (sabah_rt.cu:3887). */
 size_t sabah_row_bytes(int qt, int n);

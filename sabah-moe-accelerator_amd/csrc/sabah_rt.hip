@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <unordered_set>
 #include <vector>
@@ -43,6 +44,7 @@ char g_err[512] = {0};
 std::mutex g_mu;
 int g_device = -1;
 hipStream_t g_stream = nullptr;
+hipStream_t g_copy = nullptr;     // the harness's copy stream (sabah_h2d_async, sabah_event_record_copy)
 unsigned int* g_err_host = nullptr;   // host-mapped sticky error word
 unsigned int* g_err_dev = nullptr;    // its device address
 
@@ -384,6 +386,28 @@ int validate_mmid(const void* source, const void* d_x, const void* d_ids, const 
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Device slab: one allocation carved into ranges (the reference's slab,
+// sabah_rt.cu:332-420, serves its VRAM tier; here it serves harness callers
+// that bind it).  Free ranges are kept by offset and merged with their
+// neighbours on free; allocation takes the smallest free range that fits.
+// ---------------------------------------------------------------------------
+std::mutex g_slab_mu;
+uint8_t* g_slab = nullptr;
+size_t g_slab_cap = 0;
+std::map<size_t, size_t> g_slab_free_ranges;     // offset -> bytes
+std::map<size_t, size_t> g_slab_used;            // offset -> bytes
+constexpr size_t kSlabAlign = 256;
+
+void slab_release() {
+    std::lock_guard<std::mutex> lk(g_slab_mu);
+    if (g_slab) (void)hipFree(g_slab);
+    g_slab = nullptr;
+    g_slab_cap = 0;
+    g_slab_free_ranges.clear();
+    g_slab_used.clear();
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -410,6 +434,7 @@ SABAH_API int sabah_rt_init(int device) {
     if (!ck(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device), "LDS limit")) return -1;
     g_max_lds = lds;
     if (!ck(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "create stream")) return -1;
+    if (!ck(hipStreamCreateWithFlags(&g_copy, hipStreamNonBlocking), "create copy stream")) return -1;
     if (!ck(hipHostMalloc(reinterpret_cast<void**>(&g_err_host), sizeof(unsigned int), hipHostMallocMapped),
             "sticky error word")) return -1;
     *g_err_host = 0;
@@ -449,6 +474,9 @@ SABAH_API int sabah_rt_shutdown(void) {
     g_err_dev = nullptr;
     if (g_stream) (void)hipStreamDestroy(g_stream);
     g_stream = nullptr;
+    if (g_copy) (void)hipStreamDestroy(g_copy);
+    g_copy = nullptr;
+    slab_release();
     {
         std::lock_guard<std::mutex> lk(g_mu);
         g_banks.clear();
@@ -485,6 +513,150 @@ SABAH_API int sabah_rt_set_layer_fusion(int mode) {
     g_layer_wait_test = mode == 2;
     return 0;
 }
+
+// ===========================================================================
+// memory, copies and events for the harness (the reference's rt.py binds
+// these by name, rt.py:70-107; semantics as sabah_rt.cu:3240-3353)
+// ===========================================================================
+SABAH_API void* sabah_dev_alloc(size_t bytes) {
+    void* p = nullptr;
+    return ck(hipMalloc(&p, bytes), "device allocation") ? p : nullptr;
+}
+SABAH_API void sabah_dev_free(void* p) {
+    if (p) (void)hipFree(p);
+}
+// pinned host memory (hipHostMalloc), released by sabah_host_free
+SABAH_API void* sabah_host_alloc(size_t bytes) {
+    void* p = nullptr;
+    return ck(hipHostMalloc(&p, bytes, hipHostMallocDefault), "pinned host allocation") ? p : nullptr;
+}
+SABAH_API void sabah_host_free(void* p) {
+    if (p) (void)hipHostFree(p);
+}
+SABAH_API int sabah_dev_mem(size_t* free_bytes, size_t* total_bytes) {
+    return ck(hipMemGetInfo(free_bytes, total_bytes), "device memory info") ? 0 : -1;
+}
+SABAH_API int sabah_memcpy_h2d(void* dst, const void* src, size_t n) {
+    return ck(hipMemcpy(dst, src, n, hipMemcpyHostToDevice), "copy to device") ? 0 : -1;
+}
+SABAH_API int sabah_memcpy_d2h(void* dst, const void* src, size_t n) {
+    return ck(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost), "copy to host") ? 0 : -1;
+}
+SABAH_API int sabah_memset_d(void* dst, int v, size_t n) {
+    return ck(hipMemset(dst, v, n), "device memset") ? 0 : -1;
+}
+// host to device on the library's copy stream (ordered against the compute
+// stream only through the event calls below)
+SABAH_API int sabah_h2d_async(void* dst, const void* src, size_t n) {
+    if (!g_copy) return fail("sabah_rt_init has not been called");
+    return ck(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_copy), "async copy to device") ? 0 : -1;
+}
+SABAH_API void* sabah_event_create(void) {
+    hipEvent_t e = nullptr;
+    return ck(hipEventCreate(&e), "event create") ? reinterpret_cast<void*>(e) : nullptr;
+}
+SABAH_API void sabah_event_destroy(void* ev) {
+    if (ev) (void)hipEventDestroy(reinterpret_cast<hipEvent_t>(ev));
+}
+SABAH_API int sabah_event_record_copy(void* ev) {
+    if (!g_copy) return fail("sabah_rt_init has not been called");
+    return ck(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), g_copy), "record on the copy stream") ? 0 : -1;
+}
+SABAH_API int sabah_event_record_compute(void* ev) {
+    if (!g_stream) return fail("sabah_rt_init has not been called");
+    return ck(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), g_stream), "record on the compute stream") ? 0 : -1;
+}
+SABAH_API int sabah_compute_wait_event(void* ev) {
+    if (!g_stream) return fail("sabah_rt_init has not been called");
+    return ck(hipStreamWaitEvent(g_stream, reinterpret_cast<hipEvent_t>(ev), 0), "compute stream wait") ? 0 : -1;
+}
+SABAH_API int sabah_copy_wait_event(void* ev) {
+    if (!g_copy) return fail("sabah_rt_init has not been called");
+    return ck(hipStreamWaitEvent(g_copy, reinterpret_cast<hipEvent_t>(ev), 0), "copy stream wait") ? 0 : -1;
+}
+// milliseconds from event a to event b, after b has completed; -1 on error
+SABAH_API float sabah_event_elapsed_ms(void* a, void* b) {
+    float ms = -1.0f;
+    if (!ck(hipEventSynchronize(reinterpret_cast<hipEvent_t>(b)), "event sync")) return -1.0f;
+    if (!ck(hipEventElapsedTime(&ms, reinterpret_cast<hipEvent_t>(a), reinterpret_cast<hipEvent_t>(b)),
+            "event elapsed time"))
+        return -1.0f;
+    return ms;
+}
+SABAH_API int sabah_event_sync(void* ev) {
+    return ck(hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev)), "event sync") ? 0 : -1;
+}
+// 1: complete, 0: still in flight, -1: error
+SABAH_API int sabah_event_query(void* ev) {
+    const hipError_t e = hipEventQuery(reinterpret_cast<hipEvent_t>(ev));
+    if (e == hipSuccess) return 1;
+    if (e == hipErrorNotReady) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    ck(e, "event query");
+    return -1;
+}
+SABAH_API int sabah_sync_copy(void) {
+    if (!g_copy) return fail("sabah_rt_init has not been called");
+    return ck(hipStreamSynchronize(g_copy), "sync copy stream") ? 0 : -1;
+}
+
+// The slab (sabah_rt.cu:3889-3903): one device allocation of capacity_bytes,
+// ranges of it handed out 256-byte aligned.  Init on an existing slab is a
+// no-op; alloc returns NULL when no free range fits; free of a pointer the
+// slab did not hand out does nothing.
+SABAH_API int sabah_slab_init(size_t capacity_bytes) {
+    std::lock_guard<std::mutex> lk(g_slab_mu);
+    if (g_slab) return 0;
+    if (capacity_bytes == 0) return fail("slab capacity must be positive");
+    void* p = nullptr;
+    if (!ck(hipMalloc(&p, capacity_bytes), "slab allocation")) return -1;
+    g_slab = static_cast<uint8_t*>(p);
+    g_slab_cap = capacity_bytes;
+    g_slab_free_ranges = {{0, capacity_bytes}};
+    g_slab_used.clear();
+    return 0;
+}
+SABAH_API void* sabah_slab_alloc(size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_slab_mu);
+    if (!g_slab || bytes == 0) return nullptr;
+    const size_t want = (bytes + kSlabAlign - 1) & ~(kSlabAlign - 1);
+    auto best = g_slab_free_ranges.end();
+    for (auto it = g_slab_free_ranges.begin(); it != g_slab_free_ranges.end(); ++it)
+        if (it->second >= want && (best == g_slab_free_ranges.end() || it->second < best->second)) best = it;
+    if (best == g_slab_free_ranges.end()) return nullptr;
+    const size_t off = best->first, avail = best->second;
+    g_slab_free_ranges.erase(best);
+    if (avail > want) g_slab_free_ranges[off + want] = avail - want;
+    g_slab_used[off] = want;
+    return g_slab + off;
+}
+SABAH_API void sabah_slab_free(void* ptr) {
+    std::lock_guard<std::mutex> lk(g_slab_mu);
+    if (!g_slab || !ptr) return;
+    const uint8_t* p = static_cast<const uint8_t*>(ptr);
+    if (p < g_slab || p >= g_slab + g_slab_cap) return;
+    auto u = g_slab_used.find((size_t)(p - g_slab));
+    if (u == g_slab_used.end()) return;
+    size_t off = u->first, len = u->second;
+    g_slab_used.erase(u);
+    auto next = g_slab_free_ranges.lower_bound(off);
+    if (next != g_slab_free_ranges.begin()) {                  // merge with the range before
+        auto prev = std::prev(next);
+        if (prev->first + prev->second == off) {
+            off = prev->first;
+            len += prev->second;
+            g_slab_free_ranges.erase(prev);
+        }
+    }
+    if (next != g_slab_free_ranges.end() && off + len == next->first) {   // and the one after
+        len += next->second;
+        g_slab_free_ranges.erase(next);
+    }
+    g_slab_free_ranges[off] = len;
+}
+SABAH_API void sabah_slab_destroy(void) { slab_release(); }
 
 // Accumulated kernel time (ms) and launch count of one kernel kind
 // (0 MUL_MAT_ID, 1 gate/up, 2 down+combine, 3 decode chain); waits for the
@@ -799,6 +971,31 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
     }
     if (!ck(hipGetLastError(), "dequant launch")) return -1;
     return ck(hipStreamSynchronize(g_stream), "dequant sync") ? 0 : -1;
+}
+
+// n elements of type qt at host address src, decoded on the device by the same
+// decoders (sabah_dequant) into n floats at host address dst; synchronous.
+// Callable before sabah_rt_init, as the reference's host routine is: the
+// library is then initialised on the current HIP device.
+SABAH_API int sabah_rt_host_dequant(const void* src, float* dst, int qt, int n) {
+    if (!src || !dst || n <= 0) return fail("invalid host dequant arguments");
+    if (!supported_weight_type(qt) || row_bytes(qt, n) == 0)
+        return fail("host dequant: unsupported type %d or %d elements", qt, n);
+    if (g_device < 0) {
+        int dev = 0;
+        if (!ck(hipGetDevice(&dev), "host dequant: current device") || sabah_rt_init(dev) != 0) return -1;
+    }
+    const size_t nb = row_bytes(qt, n);
+    uint8_t* d = nullptr;
+    if (!ck(hipMalloc(reinterpret_cast<void**>(&d), nb + sizeof(float) * (size_t)n + 256), "host dequant buffers"))
+        return -1;
+    float* df = reinterpret_cast<float*>(d + ((nb + 255) & ~(size_t)255));
+    int rc = ck(hipMemcpy(d, src, nb, hipMemcpyHostToDevice), "host dequant upload") ? 0 : -1;
+    if (rc == 0) rc = sabah_dequant(d, df, qt, 1, n);
+    if (rc == 0 && !ck(hipMemcpy(dst, df, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost), "host dequant download"))
+        rc = -1;
+    (void)hipFree(d);
+    return rc;
 }
 
 SABAH_API int sabah_quantize_act(const float* d_x, void* d_y, int qt, int n_rows, int k, void* stream) {

@@ -84,12 +84,37 @@ SIGNATURES = {
     "sabah_moe_prefill_layer": ([ctypes.POINTER(MoeLayerDesc), c_vp, c_vp, c_vp, c_i, c_i, c_vp, c_vp, c_vp], c_i),
     "sabah_moe_route": ([c_vp, c_i, c_i, c_i, c_i, ctypes.c_float, c_vp, c_vp, c_vp], c_i),
     "sabah_rt_set_mmid_grouping": ([c_i], c_i),
+    # memory, copies, events and streams for the harness (the reference binds them, rt.py:70-107)
+    "sabah_dev_alloc": ([c_sz], c_vp),
+    "sabah_dev_free": ([c_vp], None),
+    "sabah_host_alloc": ([c_sz], c_vp),
+    "sabah_host_free": ([c_vp], None),
+    "sabah_dev_mem": ([ctypes.POINTER(c_sz), ctypes.POINTER(c_sz)], c_i),
+    "sabah_memcpy_h2d": ([c_vp, c_vp, c_sz], c_i),
+    "sabah_memcpy_d2h": ([c_vp, c_vp, c_sz], c_i),
+    "sabah_memset_d": ([c_vp, c_i, c_sz], c_i),
+    "sabah_h2d_async": ([c_vp, c_vp, c_sz], c_i),
+    "sabah_event_create": ([], c_vp),
+    "sabah_event_destroy": ([c_vp], None),
+    "sabah_event_record_copy": ([c_vp], c_i),
+    "sabah_event_record_compute": ([c_vp], c_i),
+    "sabah_compute_wait_event": ([c_vp], c_i),
+    "sabah_copy_wait_event": ([c_vp], c_i),
+    "sabah_event_elapsed_ms": ([c_vp, c_vp], ctypes.c_float),
+    "sabah_event_sync": ([c_vp], c_i),
+    "sabah_event_query": ([c_vp], c_i),
+    "sabah_sync_copy": ([], c_i),
+    "sabah_sync_compute": ([], c_i),
+    "sabah_sync_all": ([], c_i),
+    "sabah_slab_init": ([c_sz], c_i),
+    "sabah_slab_alloc": ([c_sz], c_vp),
+    "sabah_slab_free": ([c_vp], None),
+    "sabah_slab_destroy": ([], None),
+    "sabah_rt_host_dequant": ([c_vp, c_vp, c_i, c_i], c_i),
 }
 
 # harness-only exports (not part of the drop-in header)
 EXTRA_SIGNATURES = {
-    "sabah_sync_all": ([], c_i),
-    "sabah_sync_compute": ([], c_i),
     "sabah_synth_weights": ([c_vp, c_i, ctypes.c_longlong, c_i, ctypes.c_ulonglong, ctypes.c_float, c_vp], c_i),
     "sabah_rt_set_kernel_timing": ([c_i], c_i),
     "sabah_rt_set_layer_fusion": ([c_i], c_i),

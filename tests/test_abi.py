@@ -140,3 +140,41 @@ def test_route_rejects_invalid_shapes_without_a_device(args, msg):
     assert msg in rt.last_error()
     assert L.sabah_moe_route(vp(1), 3, 512, 10, 1, 0.0, vp(1), vp(1), None) == -1
     assert "w_scale" in rt.last_error()
+
+
+# The names the reference harness's rt.lib() binds with getattr (its
+# sabah/runtime/rt.py:70-107 signature table) and the five the llama.cpp bridge
+# resolves with dlsym (patch 0001:158-165, plus the bank registration this
+# library adds): loading either caller fails on the first name missing.
+REFERENCE_HARNESS_NAMES = [
+    "sabah_rt_last_error", "sabah_rt_init", "sabah_rt_shutdown", "sabah_rt_device_count",
+    "sabah_dev_alloc", "sabah_dev_free", "sabah_host_alloc", "sabah_host_free", "sabah_dev_mem",
+    "sabah_memcpy_h2d", "sabah_memcpy_d2h", "sabah_memset_d", "sabah_h2d_async",
+    "sabah_event_create", "sabah_event_destroy", "sabah_event_record_copy", "sabah_event_record_compute",
+    "sabah_compute_wait_event", "sabah_copy_wait_event", "sabah_event_elapsed_ms", "sabah_event_sync",
+    "sabah_event_query", "sabah_sync_copy", "sabah_sync_compute", "sabah_sync_all", "sabah_moe_block",
+    "sabah_dequant", "sabah_row_bytes", "sabah_slab_init", "sabah_slab_alloc", "sabah_slab_free",
+    "sabah_slab_destroy",
+]
+BRIDGE_NAMES = ["sabah_rt_init", "sabah_rt_mul_mat_id_v2", "sabah_rt_last_error", "sabah_rt_get_metrics",
+                "sabah_rt_register_bank"]
+
+
+def test_library_exports_every_name_the_reference_harness_and_bridge_bind():
+    from sabah.runtime import rt
+    L = rt.lib()
+    missing = [n for n in REFERENCE_HARNESS_NAMES + BRIDGE_NAMES if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(REFERENCE_HARNESS_NAMES) <= set(rt.SIGNATURES)
+
+
+def test_slab_and_events_fail_cleanly_without_init():
+    """Calls that need the library's streams fail with a message before
+    sabah_rt_init instead of touching a null stream."""
+    from sabah.runtime import rt
+    L = rt.lib()
+    if rt._initialised is not None:
+        pytest.skip("the library is already initialised in this process")
+    assert L.sabah_sync_copy() == -1 and "sabah_rt_init" in rt.last_error()
+    assert L.sabah_h2d_async(None, None, 0) == -1
+    assert L.sabah_slab_alloc(256) is None                  # no slab yet
