@@ -32,6 +32,7 @@ int orc_block_elems(int qt) {
     case ORC_Q8_0: case ORC_IQ4_NL: return 32;
     case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS:
     case ORC_IQ2_S: return 256;
+    case ORC_Q2_0: return 64;
     }
     return 0;
 }
@@ -47,6 +48,7 @@ int orc_block_bytes(int qt) {
     case ORC_IQ2_S: return 82;   /* d, qs[32], signs[32], qh[8], scales[8]       */
     case ORC_IQ4_NL: return 18;  /* d, 16 B nibbles                          */
     case ORC_IQ4_XS: return 136; /* d, scales_h u16, scales_l[4], qs[128]     */
+    case ORC_Q2_0: return 18;    /* d, 16 B of 2-bit codes (sabah_rt.cu:2166)  */
     }
     return 0;
 }
@@ -59,7 +61,7 @@ size_t orc_row_bytes(int qt, int n) {
 
 int orc_vec_dot_type(int qt) {
     switch (qt) {
-    case ORC_Q8_0: case ORC_IQ4_NL: return ORC_Q8_0;
+    case ORC_Q8_0: case ORC_IQ4_NL: case ORC_Q2_0: return ORC_Q8_0;
     case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: case ORC_IQ2_S:
         return ORC_Q8_K;
     }
@@ -313,6 +315,13 @@ int orc_dequantize_row(int qt, const uint8_t *x, float *y, int k) {
             y += 32;
         }
         return 0;
+    case ORC_Q2_0:      /* sabah_rt.cu:2411-2419; quants.py:224-235: (q - 1) * d */
+        for (int b = 0; b < k / 64; ++b, x += 18) {
+            const float d = ld_f16(x);
+            for (int j = 0; j < 64; ++j) y[j] = (float)(((x[2 + j / 4] >> (2 * (j % 4))) & 3) - 1) * d;
+            y += 64;
+        }
+        return 0;
     case ORC_IQ4_XS:    /* sabah_rt.cu:2391-2409; quants.py:1385-1411 */
         for (int b = 0; b < k / 256; ++b, x += 136) {
             const float d = ld_f16(x);
@@ -518,6 +527,30 @@ static float dot_iq4_nl(const uint8_t *w, const uint8_t *a, int k) {
     return sumf;
 }
 
+/* Q2_0 x q8_0.  ggml's CPU source for this type is not in the reference, so
+ * the activation type and the float order are a choice (parity unpinned for
+ * them): q8_0 activations, as ggml pairs its other 32-element-grouped legacy
+ * formats, and per 32-element half of a 64-element block, in element order,
+ * sumf += (float)sumi * (d_w * d_8), the form of ggml_vec_dot_q8_0_q8_0.
+ * The codes and their offset follow the reference's decoders
+ * (sabah_rt.cu:2411-2419 host, 2547-2557 device). */
+static float dot_q2_0(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 64; ++b, w += 18) {
+        const float dw = ld_f16(w);
+        for (int h = 0; h < 2; ++h, a += 34) {
+            const int8_t *q8 = (const int8_t *)(a + 2);
+            int sumi = 0;
+            for (int j = 0; j < 32; ++j) {
+                const int e = 32 * h + j;
+                sumi += (int)q8[j] * (((w[2 + e / 4] >> (2 * (e % 4))) & 3) - 1);
+            }
+            sumf += (float)sumi * (dw * ld_f16(a));
+        }
+    }
+    return sumf;
+}
+
 /* ggml_vec_dot_iq4_xs_q8_K (generic): per 32-element sub-block
  * sumf += ((dw*d8) * (ls - 32)) * sum(kv[q]*q8), sub-blocks in order. */
 static float dot_iq4_xs(const uint8_t *w, const uint8_t *a, int k) {
@@ -551,6 +584,7 @@ float orc_vec_dot(int qt, const uint8_t *w, const uint8_t *a, int k) {
     case ORC_IQ2_S: return dot_iq2_s(w, a, k);
     case ORC_IQ4_NL: return dot_iq4_nl(w, a, k);
     case ORC_IQ4_XS: return dot_iq4_xs(w, a, k);
+    case ORC_Q2_0: return dot_q2_0(w, a, k);
     }
     return NAN;
 }
@@ -743,6 +777,21 @@ static void enc_iq4_xs(const float *x, uint8_t *y, int k) {
     }
 }
 
+/* simple Q2_0 encoder (synthetic data): d = amax / 2 per 64-block, nearest of
+ * (q - 1) * d for q in 0..3 */
+static void enc_q2_0(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 64; ++b, x += 64, y += 18) {
+        float amax = 0.0f;
+        for (int j = 0; j < 64; ++j) amax = fmaxf(amax, fabsf(x[j]));
+        const uint16_t dh = orc_fp32_to_fp16(amax / 2.0f);
+        const float d = orc_fp16_to_fp32(dh), id = d > 0.0f ? 1.0f / d : 0.0f;
+        y[0] = (uint8_t)dh; y[1] = (uint8_t)(dh >> 8);
+        memset(y + 2, 0, 16);
+        for (int j = 0; j < 64; ++j)
+            y[2 + j / 4] |= (uint8_t)(clampi((int)lrintf(x[j] * id) + 1, 0, 3) << (2 * (j % 4)));
+    }
+}
+
 int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k) {
     if (orc_row_bytes(qt, k) == 0) return -1;
     switch (qt) {
@@ -752,6 +801,7 @@ int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k) {
     case ORC_IQ3_S: enc_iq3_s(x, y, k); return 0;
     case ORC_IQ4_NL: enc_iq4_nl(x, y, k); return 0;
     case ORC_IQ4_XS: enc_iq4_xs(x, y, k); return 0;
+    case ORC_Q2_0: enc_q2_0(x, y, k); return 0;
     }
     return -1;
 }

@@ -73,6 +73,7 @@ enum {
     ORC_IQ4_NL = 20,
     ORC_IQ3_S = 21,
     ORC_IQ4_XS = 23,
+    ORC_Q2_0 = 42,
 };
 
 /* Block geometry: elements and bytes per block (sabah_rt.cu:2155-2184;

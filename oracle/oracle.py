@@ -16,10 +16,10 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsabah_oracle.so")
 
-Q8_0, Q4_K, Q6_K, Q8_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS = 8, 12, 14, 15, 18, 20, 21, 22, 23
+Q8_0, Q4_K, Q6_K, Q8_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0 = 8, 12, 14, 15, 18, 20, 21, 22, 23, 42
 BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292), IQ3_S: (256, 110),
          IQ3_XXS: (256, 98), IQ4_NL: (32, 18), IQ4_XS: (256, 136),
-         IQ2_S: (256, 82)}
+         IQ2_S: (256, 82), Q2_0: (64, 18)}
 
 _lib = None
 

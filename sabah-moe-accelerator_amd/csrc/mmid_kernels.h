@@ -133,7 +133,8 @@ constexpr int kMaxTiles = 64;
 
 // 16-byte loads per lane per pass
 __host__ __device__ constexpr int stage_iters(int qt) {
-    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7 : qt == QT_IQ4_NL ? 5
+    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7
+         : (qt == QT_IQ4_NL || qt == QT_Q2_0) ? 5
          : qt == QT_IQ2_S ? 6 : 9;
 }
 // the same load count spread over nt threads
@@ -170,12 +171,17 @@ __host__ __device__ inline int pass_units(int qt, int n_mat, int unit_bytes) {
     return max(1, (16 * tile_chunk_cap(qt, n_mat) - 30) / unit_bytes);
 }
 
-// Q8_0 and IQ4_NL rows need only be whole 32-element blocks: their last unit
-// may hold 1..3 blocks
-__host__ __device__ inline bool four_block_units(int qt) { return qt == QT_Q8_0 || qt == QT_IQ4_NL; }
-__host__ __device__ inline int units_per_row(int qt, int k) { return four_block_units(qt) ? (k + 127) / 128 : k / 256; }
-// fp32 terms of ggml's row sum: one per block, one per 32-element sub-block for IQ4_XS
-__host__ __device__ inline int contribs_per_row(int qt, int k) { return qt == QT_IQ4_XS ? k / 32 : k / block_elems(qt); }
+// Q8_0, IQ4_NL (32-element blocks) and Q2_0 (64) rows need only be whole
+// blocks: their units are four blocks, the last of a row 1..3
+__host__ __device__ inline bool four_block_units(int qt) { return qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0; }
+__host__ __device__ inline int units_per_row(int qt, int k) {
+    return four_block_units(qt) ? (k + 4 * block_elems(qt) - 1) / (4 * block_elems(qt)) : k / 256;
+}
+// fp32 terms of the row sum: one per block; one per 32 elements for IQ4_XS
+// (its sub-blocks) and Q2_0 (its q8_0 activation blocks)
+__host__ __device__ inline int contribs_per_row(int qt, int k) {
+    return (qt == QT_IQ4_XS || qt == QT_Q2_0) ? k / 32 : k / block_elems(qt);
+}
 __host__ __device__ inline int unit_bytes(int qt) { return four_block_units(qt) ? 4 * (int)block_bytes(qt) : (int)block_bytes(qt); }
 
 // Rows per workgroup: about one unit per lane, with the n_mat tiles staged in
@@ -227,7 +233,8 @@ __host__ inline int launch_lds(int qt, const Plan& P) {
 // bytes of unit us of a row of k elements
 template <int QT>
 __device__ inline int unit_len(int k, int us) {
-    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL) return block_bytes(QT) * min(4, k / 32 - 4 * us);
+    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL || QT == QT_Q2_0)
+        return block_bytes(QT) * min(4, k / block_elems(QT) - 4 * us);
     return UnitFmt<QT>::BYTES;
 }
 
@@ -246,6 +253,12 @@ __device__ inline void unit_into_part(const LdsWindow<QT>& Wn, const uint8_t* ta
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (j < nb) part_row[4 * us + j] = r.c[j];
+    } else if constexpr (QT == QT_Q2_0) {
+        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, act + us * kActChunkStride, dxa + 8 * us, bsa);
+        const int nc = 2 * min(4, k / 64 - 4 * us);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < nc) part_row[8 * us + j] = r.c[j];
     } else if constexpr (QT == QT_IQ4_XS) {
         const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, act + us * kActChunkStride, dxa + us, bsa + 16 * us);
 #pragma unroll

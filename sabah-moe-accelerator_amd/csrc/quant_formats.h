@@ -3,7 +3,7 @@
 // Type codes are ggml's enum values so traces stay comparable with llama.cpp
 // (sabah/runtime/rt.py:20-23; Q6_K = 14 and Q8_K = 15 are the same enum).
 // Geometry follows sabah_rt.cu:2155-2191 for Q8_0/Q4_K/IQ3_S/IQ3_XXS/IQ2_S/
-// IQ4_NL/IQ4_XS and gguf-py quants.py:586-606 for Q6_K (ql[128] qh[64] int8
+// IQ4_NL/IQ4_XS/Q2_0 and gguf-py quants.py:586-606 for Q6_K (ql[128] qh[64] int8
 // scales[16] fp16 d).
 #pragma once
 #include <hip/hip_fp16.h>
@@ -27,10 +27,12 @@ enum : int {
     QT_IQ3_S = 21,
     QT_IQ2_S = 22,
     QT_IQ4_XS = 23,
+    QT_Q2_0 = 42,
 };
 
 __host__ __device__ constexpr int block_elems(int qt) {
     return (qt == QT_Q8_0 || qt == QT_IQ4_NL) ? 32
+         : qt == QT_Q2_0 ? 64
          : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_Q8_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS ||
             qt == QT_IQ4_XS || qt == QT_IQ2_S) ? 256 : 0;
 }
@@ -44,7 +46,8 @@ __host__ __device__ constexpr int block_bytes(int qt) {
          : qt == QT_IQ3_XXS ? 98      // fp16 d, qs[64] grid indices, 8 x u32 (4 x 7-bit signs, 4-bit scale)
          : qt == QT_IQ4_NL ? 18       // fp16 d, 16 bytes of level nibbles
          : qt == QT_IQ2_S ? 82        // fp16 d, qs[32], signs[32], qh[8], scales[8]
-         : qt == QT_IQ4_XS ? 136 : 0; // fp16 d, u16 scales_h, scales_l[4], qs[128]
+         : qt == QT_IQ4_XS ? 136      // fp16 d, u16 scales_h, scales_l[4], qs[128]
+         : qt == QT_Q2_0 ? 18 : 0;    // fp16 d, 16 bytes of 2-bit codes
 }
 
 __host__ __device__ inline size_t row_bytes(int qt, int n) {
@@ -55,16 +58,17 @@ __host__ __device__ inline size_t row_bytes(int qt, int n) {
 
 // The activation format ggml's CPU pairs with each weight type (its
 // vec_dot_type): q8_0 for Q8_0 and IQ4_NL; q8_K for the K-quants, IQ3_S,
-// IQ3_XXS, IQ2_S and IQ4_XS.
+// IQ3_XXS, IQ2_S and IQ4_XS.  Q2_0 takes q8_0, two blocks per weight block
+// (ggml's CPU code for Q2_0 is not in the reference: a choice, see the oracle).
 __host__ __device__ constexpr int act_type(int qt) {
-    return (qt == QT_Q8_0 || qt == QT_IQ4_NL) ? QT_Q8_0
+    return (qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0) ? QT_Q8_0
          : (qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS || qt == QT_IQ4_XS ||
             qt == QT_IQ2_S) ? QT_Q8_K : -1;
 }
 
 __host__ __device__ constexpr bool supported_weight_type(int qt) {
     return qt == QT_Q8_0 || qt == QT_Q4_K || qt == QT_Q6_K || qt == QT_IQ3_S || qt == QT_IQ3_XXS || qt == QT_IQ4_NL ||
-           qt == QT_IQ4_XS || qt == QT_IQ2_S;
+           qt == QT_IQ4_XS || qt == QT_IQ2_S || qt == QT_Q2_0;
 }
 
 // Expanded IQ3_S codebook entry: byte j = 2*level_j + 1.

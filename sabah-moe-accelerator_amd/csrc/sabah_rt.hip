@@ -303,6 +303,7 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
     case QT_IQ3_S: return launch_mmid<QT_IQ3_S>(a, st);
     case QT_IQ3_XXS: return launch_mmid<QT_IQ3_XXS>(a, st);
     case QT_IQ4_NL: return launch_mmid<QT_IQ4_NL>(a, st);
+    case QT_Q2_0: return launch_mmid<QT_Q2_0>(a, st);
     case QT_IQ4_XS: return launch_mmid<QT_IQ4_XS>(a, st);
     case QT_IQ2_S: return launch_mmid<QT_IQ2_S>(a, st);
     }
@@ -335,6 +336,7 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
     case QT_IQ3_S: return launch_gate_up<QT_IQ3_S>(a, n_tokens, st);
     case QT_IQ3_XXS: return launch_gate_up<QT_IQ3_XXS>(a, n_tokens, st);
     case QT_IQ4_NL: return launch_gate_up<QT_IQ4_NL>(a, n_tokens, st);
+    case QT_Q2_0: return launch_gate_up<QT_Q2_0>(a, n_tokens, st);
     case QT_IQ4_XS: return launch_gate_up<QT_IQ4_XS>(a, n_tokens, st);
     case QT_IQ2_S: return launch_gate_up<QT_IQ2_S>(a, n_tokens, st);
     }
@@ -365,6 +367,7 @@ hipError_t dispatch_down(int qt, const DownArgs& a, int n_tokens, hipStream_t st
     case QT_IQ3_S: return launch_down<QT_IQ3_S>(a, n_tokens, st);
     case QT_IQ3_XXS: return launch_down<QT_IQ3_XXS>(a, n_tokens, st);
     case QT_IQ4_NL: return launch_down<QT_IQ4_NL>(a, n_tokens, st);
+    case QT_Q2_0: return launch_down<QT_Q2_0>(a, n_tokens, st);
     case QT_IQ4_XS: return launch_down<QT_IQ4_XS>(a, n_tokens, st);
     case QT_IQ2_S: return launch_down<QT_IQ2_S>(a, n_tokens, st);
     }
@@ -380,7 +383,7 @@ int validate_mmid(const void* source, const void* d_x, const void* d_ids, const 
     if (x_rows <= 0 || (x_rows != 1 && x_rows != n_ids))
         return fail("Sabah MUL_MAT_ID input rows %d must be 1 (broadcast) or n_ids %d", x_rows, n_ids);
     if (!supported_weight_type(qt)) return fail("unsupported quant type %d (supported: 8 Q8_0, 12 Q4_K, 14 Q6_K, 18 IQ3_XXS, 20 IQ4_NL, 21 IQ3_S, "
-                                            "22 IQ2_S, 23 IQ4_XS)", qt);
+                                            "22 IQ2_S, 23 IQ4_XS, 42 Q2_0)", qt);
     if (k % block_elems(qt)) return fail("k=%d is not a whole number of type-%d blocks", k, qt);
     if (row_stride < row_bytes(qt, k)) return fail("row stride %zu is shorter than a row (%zu bytes)", row_stride, row_bytes(qt, k));
     return 0;
@@ -966,6 +969,7 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
     case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ3_XXS: hipLaunchKernelGGL(k_dequant<QT_IQ3_XXS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ4_NL: hipLaunchKernelGGL(k_dequant<QT_IQ4_NL>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_Q2_0: hipLaunchKernelGGL(k_dequant<QT_Q2_0>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ4_XS: hipLaunchKernelGGL(k_dequant<QT_IQ4_XS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ2_S: hipLaunchKernelGGL(k_dequant<QT_IQ2_S>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     }

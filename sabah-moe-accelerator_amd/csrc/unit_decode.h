@@ -1,8 +1,8 @@
 // Register-resident decoding of quantised weights, one "unit" per lane.
 //
 // A unit is one 256-element super-block (Q4_K 144 B, Q6_K 210 B, IQ3_S 110 B,
-// IQ3_XXS 98 B, IQ2_S 82 B, IQ4_XS 136 B) or four 32-element blocks (Q8_0 136 B, IQ4_NL
-// 72 B).  Each lane loads its unit straight
+// IQ3_XXS 98 B, IQ2_S 82 B, IQ4_XS 136 B), four 32-element blocks (Q8_0 136 B, IQ4_NL
+// 72 B) or four 64-element blocks (Q2_0 72 B).  Each lane loads its unit straight
 // from HBM into VGPRs with 8-byte loads that cover exactly the unit's 8-byte
 // granules (so a load never touches a page the unit does not), then
 // re-aligns the bytes so that every field of the format sits at a static
@@ -50,6 +50,7 @@ template <> struct UnitFmt<QT_IQ3_XXS> { static constexpr int BYTES = 98, ELEMS 
 template <> struct UnitFmt<QT_IQ4_XS> { static constexpr int BYTES = 136, ELEMS = 256, ORG = 0, NF = 34, CONTRIB = 8; };
 template <> struct UnitFmt<QT_IQ4_NL> { static constexpr int BYTES = 72, ELEMS = 128, ORG = 2, NF = 18, CONTRIB = 4; };
 template <> struct UnitFmt<QT_IQ2_S> { static constexpr int BYTES = 82, ELEMS = 256, ORG = 2, NF = 20, CONTRIB = 1; };
+template <> struct UnitFmt<QT_Q2_0> { static constexpr int BYTES = 72, ELEMS = 256, ORG = 2, NF = 18, CONTRIB = 8; };
 
 // Window: the unit's granules, loaded from base = (origin - 4) rounded down to
 // 8 bytes; the origin then sits at byte p in [4, 11] of the window.
@@ -503,6 +504,44 @@ __device__ inline void iq4nl_block(const uint32_t (&F)[18], uint32_t Fm1, uint32
     else dbits = F[dob / 4] >> 16;
 }
 
+// ---------------------------------------------------------------------------
+// Q2_0 unit = 4 blocks of 18 B, 64 elements each: the byte layout of an IQ4_NL
+// unit, so block J's d and 16 code bytes come out of iq4nl_block<J>.  Code e
+// of a block sits at bits 2*(e % 4) of byte e / 4; its value is (code - 1) * d
+// (sabah_rt.cu:2411-2419).
+// ---------------------------------------------------------------------------
+// code - 1 as int8, for the codes in the low two bits of each byte of x
+__device__ inline uint32_t q2_0_values(uint32_t x) {
+    return __builtin_amdgcn_perm(0u, 0x020100FFu, x & 0x03030303u);   // selector 0..3 -> -1, 0, 1, 2
+}
+// the 16 codes of code dword w as int8 values in element order: o[g] byte i is
+// element 4g + i (bits 2i of byte g)
+__device__ inline void q2_0_dword(uint32_t w, uint32_t (&o)[4]) {
+    const uint32_t c0 = q2_0_values(w), c1 = q2_0_values(w >> 2), c2 = q2_0_values(w >> 4),
+                   c3 = q2_0_values(w >> 6);
+    // 4 x 4 byte transpose: byte g of c_i becomes byte i of o[g]
+    const uint32_t p0 = __builtin_amdgcn_perm(c1, c0, 0x05010400u);   // c0.b0 c1.b0 c0.b1 c1.b1
+    const uint32_t p1 = __builtin_amdgcn_perm(c1, c0, 0x07030602u);   // c0.b2 c1.b2 c0.b3 c1.b3
+    const uint32_t p2 = __builtin_amdgcn_perm(c3, c2, 0x05010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(c3, c2, 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(p2, p0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(p2, p0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(p3, p1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(p3, p1, 0x07060302u);
+}
+// the integer dot of 32 codes (two code dwords) with 32 activations
+__device__ inline int q2_0_dot32(const uint32_t* qd, const uint32_t* A) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        uint32_t o[4];
+        q2_0_dword(qd[i], o);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) s = sdot4(o[g], A[4 * i + g], s);
+    }
+    return s;
+}
+
 // the integer dot of 16 level bytes (four dwords of nibble pairs) with 32
 // activations: low nibbles against A[0..3], high nibbles against A[4..7]
 __device__ inline int iq4_dot32(const uint32_t* qd, const uint32_t* A) {
@@ -636,6 +675,19 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
         }
         SB_IQ4NL_BLOCK(0) SB_IQ4NL_BLOCK(1) SB_IQ4NL_BLOCK(2) SB_IQ4NL_BLOCK(3)
 #undef SB_IQ4NL_BLOCK
+    } else if constexpr (QT == QT_Q2_0) {    // four blocks, each paired with two q8_0 blocks
+        uint32_t qd[4], A[8], db;
+#define SB_Q20_BLOCK(J)                                                                    \
+        {                                                                                  \
+            iq4nl_block<J>(F, Fm1, qd, db);                                                \
+            const float dw = h2f(db);                                                      \
+            act8(chunk, 2 * J, A);                                                         \
+            r.c[2 * J] = __fmul_rn((float)q2_0_dot32(qd, A), __fmul_rn(dw, dx[2 * J]));   \
+            act8(chunk, 2 * J + 1, A);                                                     \
+            r.c[2 * J + 1] = __fmul_rn((float)q2_0_dot32(qd + 2, A), __fmul_rn(dw, dx[2 * J + 1])); \
+        }
+        SB_Q20_BLOCK(0) SB_Q20_BLOCK(1) SB_Q20_BLOCK(2) SB_Q20_BLOCK(3)
+#undef SB_Q20_BLOCK
     } else {   // Q8_0: four independent blocks
         uint32_t v[8], A[8], db;
 #define SB_Q8_BLOCK(J)                                                              \
@@ -748,6 +800,23 @@ __device__ inline void unit_dequant(const UnitWindow<QT>& Wn, const uint8_t* sme
         }
         SB_IQ4NL_DEQ(0) SB_IQ4NL_DEQ(1) SB_IQ4NL_DEQ(2) SB_IQ4NL_DEQ(3)
 #undef SB_IQ4NL_DEQ
+    } else if constexpr (QT == QT_Q2_0) {
+        uint32_t qd[4], db;
+#define SB_Q20_DEQ(J)                                                                               \
+        {                                                                                           \
+            iq4nl_block<J>(F, Fm1, qd, db);                                                         \
+            const float d = h2f(db);                                                                \
+            if (64 * J < n)                                                                         \
+                for (int i = 0; i < 4; ++i) {                                                       \
+                    uint32_t o[4];                                                                  \
+                    q2_0_dword(qd[i], o);                                                           \
+                    for (int e = 0; e < 16; ++e)                                                    \
+                        out[64 * J + 16 * i + e] =                                                  \
+                            __fmul_rn((float)(int8_t)((o[e >> 2] >> (8 * (e & 3))) & 0xFFu), d);    \
+                }                                                                                   \
+        }
+        SB_Q20_DEQ(0) SB_Q20_DEQ(1) SB_Q20_DEQ(2) SB_Q20_DEQ(3)
+#undef SB_Q20_DEQ
     } else {
         uint32_t v[8], db;
 #define SB_Q8_DEQ(J)                                                                                       \

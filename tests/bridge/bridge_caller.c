@@ -33,6 +33,7 @@ static int type_traits(int type, int64_t *blck, size_t *bytes) {
     case 21: *blck = 256; *bytes = 110; return 0;               /* IQ3_S */
     case 22: *blck = 256; *bytes = 82; return 0;                /* IQ2_S */
     case 23: *blck = 256; *bytes = 136; return 0;               /* IQ4_XS */
+    case 42: *blck = 64; *bytes = 18; return 0;                 /* Q2_0 */
     }
     return -1;
 }

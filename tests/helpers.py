@@ -42,7 +42,7 @@ def f16(x: float) -> bytes:
 def dequant_act(O, qt: int, act: np.ndarray, k: int) -> np.ndarray:
     """float64 values of a quantised activation row (as its vec_dot partner sees them)."""
     act = np.ascontiguousarray(act, np.uint8).reshape(-1)
-    if qt in (O.Q8_0, O.IQ4_NL):                     # q8_0 activations
+    if qt in (O.Q8_0, O.IQ4_NL, O.Q2_0):             # q8_0 activations
         blk = act.reshape(-1, 34)
         d = blk[:, :2].copy().view(np.float16).astype(np.float64)
         return (blk[:, 2:].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
@@ -85,7 +85,7 @@ def random_blocks(rng, qt: int, n_rows: int, k: int) -> np.ndarray:
     def scales(n):
         return (rng.uniform(0.25, 2.0, size=n) * rng.choice([-1, 1], size=n) * 1e-2).astype(np.float16)
 
-    if qt in (8, 18, 20, 21, 22, 23):       # Q8_0, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS: fp16 d at 0
+    if qt in (8, 18, 20, 21, 22, 23, 42):   # Q8_0, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0: fp16 d at 0
         raw[:, :, 0:2] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
     elif qt == 12:                          # Q4_K: d, dmin at 0, 2 (non-negative in real data)
         raw[:, :, 0:2] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)

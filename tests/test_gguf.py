@@ -126,7 +126,7 @@ def test_inspector_refuses(tmp_path, orc, case, needle):
             return gguf.WriterTensor("blk.0.ffn_%s_exps.weight" % role, shape, qt, np.zeros(n, np.uint8))
         ts = [t("gate", 21, (D, F, E)), t("up", 21, (D, F, E))]
         if case == "type":
-            ts.append(t("down", 42, (F, D, E)))             # Q2_0: a GGUF type the kernels do not decode
+            ts.append(t("down", 13, (F, D, E)))             # Q5_K: a GGUF type the kernels do not decode
         elif case == "axis":
             ts.append(t("down", 21, (F, E, D)))             # experts not the slowest axis
         gguf.write_gguf(p, kv, ts)
@@ -135,3 +135,16 @@ def test_inspector_refuses(tmp_path, orc, case, needle):
     assert any(needle in n for n in prof.notes), prof.notes
     with pytest.raises(model.UnsupportedModel):
         model.load_expert_bank(prof, device="cpu")
+
+
+def test_inspector_accepts_q2_0_experts(tmp_path, orc):
+    """The artifact's Q2_0 experts (ggml type 42, 64-element blocks of 18 B)
+    inspect as supported, with their per-expert bytes from the type's geometry."""
+    p = str(tmp_path / "m.gguf")
+    rng = np.random.default_rng(4)
+    E, D, F = 4, 256, 192
+    write_model(p, orc, rng, n_layers=1, E=E, D=D, F=F, layer_types=[(42, 42, 42)])
+    prof = model.inspect_model(p)
+    assert prof.supported, prof.notes
+    assert prof.experts[(0, "gate")].ggml_type == 42
+    assert prof.experts[(0, "down")].per_expert_bytes == D * (F // 64) * 18

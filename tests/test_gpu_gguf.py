@@ -25,9 +25,11 @@ def gguf_model(tmp_path_factory, orc):
     p = str(tmp_path_factory.mktemp("gguf") / "m.gguf")
     rng = np.random.default_rng(41)
     # layer 2: the quant mix of the reference's shipped blocks (IQ3_XXS gate/up, IQ4_NL down);
-    # layer 3: IQ2_S gate/up (another of the artifact's expert types) with IQ4_XS down
-    raws, shared = write_model(p, orc, rng, n_layers=4, E=16, D=1024, F=512, n_used=4,
-                               layer_types=[(21, 21, 21), (12, 12, 14), (18, 18, 20), (22, 22, 23)], Fs=256,
+    # layer 3: IQ2_S gate/up (another of the artifact's expert types) with IQ4_XS down;
+    # layer 4: Q2_0 (ggml type 42), the artifact's last expert type
+    raws, shared = write_model(p, orc, rng, n_layers=5, E=16, D=1024, F=512, n_used=4,
+                               layer_types=[(21, 21, 21), (12, 12, 14), (18, 18, 20), (22, 22, 23), (42, 42, 42)],
+                               Fs=256,
                                gate_inp_shexp=True)
     return p, raws, shared
 
@@ -40,7 +42,7 @@ def test_loaded_bank_is_the_file_and_runs_its_layers(hip_rt, orc, gguf_model):
     assert prof.supported, prof.notes
     bank = model.load_expert_bank(prof, "cuda:0", verify=True)
     rng = np.random.default_rng(42)
-    for l in (0, 1, 2, 3):
+    for l in (0, 1, 2, 3, 4):
         for r in ("gate", "up", "down"):
             assert np.array_equal(bank.tensor(l, r).cpu().numpy().reshape(raws[(l, r)].shape), raws[(l, r)])
         sh = model.load_shared_expert(prof, l)
@@ -67,7 +69,7 @@ def test_drop_in_call_with_the_file_mapping_address(hip_rt, orc, gguf_model):
         rng = np.random.default_rng(43)
         ids, _ = routing.uniform_routing(rng, 3, 16, 4)
         x = rng.standard_normal((3, 1, 1024)).astype(np.float32)
-        for l in (0, 1, 2, 3):
+        for l in (0, 1, 2, 3, 4):
             ref = prof.experts[(l, "gate")]
             key = files[ref.shard].base_address() + ref.data_offset
             via_key = ex.mul_mat_id(l, "gate", T(x), T(ids), source=key)

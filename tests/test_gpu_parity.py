@@ -17,9 +17,9 @@ from helpers import assert_parity, random_blocks, unfused_rounding_row
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS = 8, 12, 14, 18, 20, 21, 22, 23
+Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0 = 8, 12, 14, 18, 20, 21, 22, 23, 42
 # formats whose fp32 steps follow ggml's vec_dot order exactly: results bit-identical to the oracle's
-BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S)
+BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S, Q2_0)
 DEV = torch.device("cuda:0")
 
 
@@ -83,7 +83,8 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
 
 @pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768),
                                   (IQ3_XXS, 2048), (IQ3_XXS, 768), (IQ4_NL, 640), (IQ4_NL, 96), (IQ4_XS, 2048),
-                                  (IQ4_XS, 768), (IQ2_S, 2048), (IQ2_S, 768)])
+                                  (IQ4_XS, 768), (IQ2_S, 2048), (IQ2_S, 768), (Q2_0, 2048), (Q2_0, 192),
+                                  (Q2_0, 64)])
 def test_dequant_is_bit_exact(hip_rt, orc, qt, k):
     rng = np.random.default_rng(qt * 7 + k)
     raw = random_blocks(rng, qt, 37, k)
@@ -113,7 +114,8 @@ def v2(hip_rt, src, expert_stride, row_bytes, x, ids, out, rows, k, E, qt):
 CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), (Q4_K, 768, 64),
          (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104), (Q8_0, 32768, 6),
          (IQ3_XXS, 2048, 48), (IQ3_XXS, 2560, 40), (IQ4_NL, 640, 64), (IQ4_NL, 96, 24), (IQ4_XS, 2048, 48),
-         (IQ4_XS, 768, 72), (IQ2_S, 2048, 48), (IQ2_S, 768, 80)]
+         (IQ4_XS, 768, 72), (IQ2_S, 2048, 48), (IQ2_S, 768, 80), (Q2_0, 2048, 48), (Q2_0, 768, 64),
+         (Q2_0, 192, 40), (Q2_0, 64, 24)]
 
 
 @pytest.mark.parametrize("qt,k,rows", CASES)
@@ -305,7 +307,7 @@ def test_moe_block_single_token_q8_0(hip_rt, orc):
 # iq4nl_down_t3_hq take that path with q8_0 rows (Q8_0 / IQ4_NL down, d_ff 768)
 @pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small", "iq3s_t32",
                                   "iq3xxs_iq4nl_artifact_shape", "iq4xs_small", "iq2s_iq3s_mix", "q8_0_t4_hq",
-                                  "iq4nl_down_t3_hq"])
+                                  "iq4nl_down_t3_hq", "q2_0_decode", "q2_0_down_t3_hq", "q2_0_partial_units"])
 def test_moe_layer_matches_oracle(hip_rt, orc, name):
     from sabah.runtime import routing
     from sabah.runtime.bank import DenseExpert
@@ -336,6 +338,16 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     elif name == "iq4nl_down_t3_hq":
         E, D, F, K, Tn, qts = 24, 2048, 768, 6, 3, (IQ3_XXS, IQ3_XXS, IQ4_NL)
         ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "q2_0_decode":
+        E, D, F, K, Tn, qts = 64, 2048, 768, 10, 1, (Q2_0, Q2_0, Q2_0)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "q2_0_down_t3_hq":
+        E, D, F, K, Tn, qts = 24, 2048, 768, 6, 3, (IQ3_XXS, IQ3_XXS, Q2_0)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "q2_0_partial_units":
+        # d_model 960 = 3 units + 3 blocks, d_ff 576 = 2 units + 1 block
+        E, D, F, K, Tn, qts = 16, 960, 576, 4, 2, (Q2_0, Q2_0, Q2_0)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
     else:
         E, D, F, K, Tn, qts = 64, 2048, 768, 10, 4, (IQ3_S, IQ3_S, IQ3_S)
         ids, w = routing.zipf_routing(rng, Tn, E, K)
@@ -355,6 +367,8 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     sh = None if sh_raw is None else (sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3)
     want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], qts, x, ids, w, shared=sh)
     assert_parity(out.cpu().numpy(), want, name)
+    if name.startswith("q2_0"):
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 def test_mixed_layer_at_512_experts_on_a_synthetic_bank(hip_rt, orc):
