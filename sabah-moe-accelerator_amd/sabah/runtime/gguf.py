@@ -89,6 +89,8 @@ class _Cursor:
         self.buf, self.pos = buf, pos
 
     def take(self, fmt):
+        if self.pos + struct.calcsize(fmt) > len(self.buf):
+            raise GgufError("the header runs past the end of the file at byte %d" % self.pos)
         v = struct.unpack_from(fmt, self.buf, self.pos)[0]
         self.pos += struct.calcsize(fmt)
         return v
@@ -127,8 +129,16 @@ class GgufFile:
         self._f = open(path, "rb")
         size = os.fstat(self._f.fileno()).st_size
         if size < 24:
+            self._f.close()
             raise GgufError("%s: too short for a GGUF header" % path)
         self.mm = mmap.mmap(self._f.fileno(), 0, access=mmap.ACCESS_READ)
+        try:
+            self._parse(path, size)
+        except Exception:
+            self.close()
+            raise
+
+    def _parse(self, path: str, size: int) -> None:
         c = _Cursor(self.mm)
         if bytes(self.mm[:4]) != GGUF_MAGIC:
             raise GgufError("%s: bad magic %r" % (path, bytes(self.mm[:4])))
