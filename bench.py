@@ -28,6 +28,20 @@ sys.path.insert(0, PKG)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "MUL_MAT_ID expert GB/s (% HBM peak) + decode tok/s over 48 MoE layers, 1 GPU"
+ONE_LAYER_CHAIN = 48                   # layer calls per step for a one-layer workload
+
+
+def quant_note(W):
+    from sabah.runtime.rt import QTYPE_NAME
+    names = [QTYPE_NAME[q] for q in (W.qt_gate, W.qt_up, W.qt_down)]
+    return names[0] if len(set(names)) == 1 else "%s gate/up, %s down" % (names[0], names[2])
+
+
+def compute_note(W):
+    from sabah.runtime.rt import QTYPE_NAME
+    acts = sorted({"q8_0" if q in (8, 20, 42) else "q8_K" for q in (W.qt_gate, W.qt_up, W.qt_down)})
+    return ("int8 x int8 -> int32 dot products (%s weights decoded to int8, %s activations), fp32 scales and "
+            "accumulation" % (quant_note(W), " / ".join(acts)))
 
 
 def parse():
@@ -82,8 +96,12 @@ def main() -> int:
 
     rng = np.random.default_rng(args.seed)
     P = args.pool
-    ids_np, w_np = W.route(rng, n_tokens=P)                         # [L, P, k]
-    ids_np = np.ascontiguousarray(ids_np.transpose(1, 0, 2))[:, :, None, :]   # [P, L, 1, k]
+    # a step runs the chain of G layer calls: the model's layers, or for a
+    # one-layer workload G calls of that layer (each with its own ids), so a
+    # ~10 us layer is not measured behind one graph launch per call
+    G = W.n_layers if W.n_layers > 1 else ONE_LAYER_CHAIN
+    ids_np, w_np = W.route(rng, n_tokens=P, n_layers=G)             # [G, P, k]
+    ids_np = np.ascontiguousarray(ids_np.transpose(1, 0, 2))[:, :, None, :]   # [P, G, 1, k]
     w_np = np.ascontiguousarray(w_np.transpose(1, 0, 2))[:, :, None, :]
     x_np = rng.standard_normal((P, 1, W.d_model)).astype(np.float32)
     ids = torch.from_numpy(ids_np).to(dev)
@@ -91,7 +109,10 @@ def main() -> int:
     xs = torch.from_numpy(x_np).to(dev)
     x_buf = torch.empty(1, W.d_model, dtype=torch.float32, device=dev)
     ex = MoEExecutor(bank, max_used=W.top_k)
-    descs = ex.layer_descs()
+    if W.n_layers > 1:
+        descs = ex.layer_descs()
+    else:
+        descs = (rt.MoeLayerDesc * G)(*([bank.layer_desc(0, None)] * G))
     step_bytes = [W.step_expert_bytes(ids_np[p, :, 0][:, None, :]) for p in range(P)]
 
     def eager_step(i):
@@ -131,6 +152,23 @@ def main() -> int:
     nbytes = sum(step_bytes[i % P] for i in range(args.warmup, args.warmup + args.steps))
     gbs = nbytes / (ms_total * 1e6)
 
+    # a layer's launches as the replayed graph runs them: the bare graph (the
+    # last step's inputs in place, no copies in) replayed R times, HIP events
+    # on the stream it replays on; per layer = one fused launch, or the
+    # gate/up and down launches
+    R = max(4, args.steps // 2)
+    cg.replay_static()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(R):
+        cg.replay_static()
+    ev1.record()
+    torch.cuda.synchronize()
+    us_layer_graph = 1000.0 * ev0.elapsed_time(ev1) / (R * G)
+    last = (args.warmup + args.steps - 1) % P
+    layer_bytes_last = step_bytes[last] / G                        # distinct expert bytes per layer call
+
     # per-kernel durations: the same steps run eagerly, each dispatch recording
     # its own start/stop HIP event pair on the stream it runs on
     L = rt.lib()
@@ -144,18 +182,23 @@ def main() -> int:
         ms, n = rt.kernel_timing(kind)
         if n:
             kernels[kind] = {"launches": n, "avg_us": 1000.0 * ms / n, "total_ms": ms}
-    dom = max(kernels, key=lambda k: kernels[k]["total_ms"])
-    # algorithmic bytes of one launch of the dominant kernel
+    # algorithmic bytes of one layer call: its k routed expert matrices (every
+    # slot's, as the kernels read them: distinct ids at one token), x, h
+    # written and read, the weights and the output
     k_used = W.top_k
     per_launch = {
         "gate_up": k_used * (W.matrix_bytes("gate") + W.matrix_bytes("up")) + 4 * W.d_model + 4 * k_used * W.d_ff,
         "down": k_used * W.matrix_bytes("down") + 4 * k_used * W.d_ff + 4 * (2 * W.d_model + k_used),
     }
-    per_launch["layer"] = per_launch["gate_up"] + per_launch["down"]    # the fused launch does both
-    achieved = per_launch[dom] / (kernels[dom]["avg_us"] * 1e3)          # GB/s
+    per_launch["layer"] = per_launch["gate_up"] + per_launch["down"]
+    fused = "layer" in kernels
+    achieved = per_launch["layer"] / (us_layer_graph * 1e3)                  # GB/s
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(W.name, dom),
-                "kernel": dom, "bytes_per_launch": per_launch[dom], "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(W.name, "layer" if fused else None),
+                "kernel": "layer" if fused else "layer (gate_up + down launches)",
+                "bytes_per_launch": per_launch["layer"], "avg_launch_us": round(us_layer_graph, 3),
+                "timing": "replayed graph, %d replays of %d layer calls" % (R, G)}
 
     cpu = None
     parity = None
@@ -166,18 +209,19 @@ def main() -> int:
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8",
-        "compute": "int8 x int8 -> int32 dot products (IQ3_S weights decoded to int8, q8_K activations), fp32 scales and accumulation",
-        "data": "synthetic (N(0,0.02) weights quantised on device; Zipf-biased routing; seeded)",
+        "compute": compute_note(W),
+        "data": "synthetic (N(0,0.02) weights quantised on device; %s routing; seeded)" % W.routing,
         "config": {"workload": W.name, "n_layers": W.n_layers, "n_experts": W.n_experts, "top_k": W.top_k,
-                   "d_model": W.d_model, "d_ff": W.d_ff, "n_tokens": W.n_tokens, "quant": "IQ3_S",
+                   "d_model": W.d_model, "d_ff": W.d_ff, "n_tokens": W.n_tokens, "quant": quant_note(W),
                    "bank_bytes": bank.total_bytes, "expert_bytes_per_step": nbytes // args.steps,
+                   "layer_calls_per_step": G,
                    "mode": ("one fused launch per layer (gate/up+SwiGLU and down+combine workgroups in one grid, h "
-                            "handed over in the kernel), the 48 launches replayed as one HIP graph per token"
-                            if "layer" in kernels else
+                            "handed over in the kernel), the %d launches replayed as one HIP graph per step" % G
+                            if fused else
                             "chain of per-layer kernels (gate/up+SwiGLU, down+combine) replayed as one HIP graph per "
-                            "token")},
-        "tok_s": round(1000.0 / ms_step, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "us_per_layer": round(1000.0 * ms_step / W.n_layers, 3),
+                            "step of %d layer calls" % G)},
+        "tok_s": round(1000.0 * (1 if W.n_layers > 1 else G) / ms_step, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "us_per_layer": round(1000.0 * ms_step / G, 3),
         "kernels": {k: {"launches": v["launches"], "avg_us": round(v["avg_us"], 3)} for k, v in kernels.items()},
         "eager_ms_per_step": round(ms_eager / args.steps, 4),
         "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
@@ -409,6 +453,8 @@ def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid=False):
 def measured_traffic(workload, kind):
     """HBM bytes per launch of `kind` from the committed FETCH_SIZE / WRITE_SIZE
     counter runs (calibrated against a plain copy), or None if not measured."""
+    if kind is None:
+        return None
     path = os.path.join(ROOT, "profiles", "decode_kernels_%s_traffic.json" % workload)
     try:
         with open(path) as f:

@@ -19,7 +19,8 @@
 // The h handoff, per workgroup and without shared counters:
 //   gate/up: h rows stored write-through to memory (agent-scope stores), the
 //     stores waited for, then its flag sync[g] set (an agent-scope store);
-//   down: the codebook table built, the weights loaded and staged in LDS,
+//   down: a head start of d_delay left to the gate/up weight loads, then
+//     the codebook table built, the weights loaded and staged in LDS,
 //     and each lane's half unit decoded to int8 in registers, all while
 //     gate/up runs; then wave 0 waits for the flags, h is read with ordinary
 //     loads, quantised, and dotted with the decoded weights.  Down
@@ -66,6 +67,7 @@ struct LayerArgs {
     uint32_t* sync;             // [kSyncWords] lockstep flags (layout above)
     uint32_t wait_skew;         // 0; a test of the timeout path sets 1: the down workgroups wait for a
                                 // flag value no gate/up workgroup writes, so their bounded wait runs out
+    uint32_t d_delay;           // s_memrealtime ticks (10 ns) the down workgroups wait before their loads
 };
 
 // LDS of the fused kernel: the down role's static layout (IQ3_S table, tile
@@ -179,8 +181,12 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     const float sh0 = d.shared && r0 < nrows ? d.shared[orow] : 0.0f;
     const float rs0 = d.resid && r0 < nrows ? d.resid[orow] : 0.0f;
     const float ac0 = d.accumulate && r0 < nrows ? d.out[orow] : 0.0f;
-    // the codebook table first: this workgroup's weight loads then follow the
-    // gate/up workgroups', whose bytes are needed sooner
+    // wait d_delay, then the codebook table: this workgroup's weight loads
+    // then queue behind the gate/up workgroups', whose bytes are needed sooner
+    if (a.d_delay) {
+        const unsigned long long t0 = wall_ticks();
+        while (wall_ticks() - t0 < a.d_delay) __builtin_amdgcn_s_sleep(8);
+    }
     store_tables<QT, NT>(tabs, load_tables<QT, NT>((int)threadIdx.x), (int)threadIdx.x);
     const uint8_t* e = resolve_slot_word(d.D, d.rt, sw);
     const bool bad = __any(e == nullptr);

@@ -1177,6 +1177,17 @@ static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_
     return ck(dispatch_mmid(L->qt_shared_down, a, st), "shared down launch") ? 0 : -1;
 }
 
+// The fused layer's down workgroups wait this long (10 ns ticks) before their
+// weight loads: the time the gate/up weights take at 7.5 TB/s (75,000 bytes
+// per tick), so the gate/up bytes, needed first, are not shared with them.
+// On the 48-layer decode (13.5 MB of gate/up weights, 180 ticks) the layer
+// measured 11.7 us against 12.7 us without the wait (per-workgroup stamps,
+// same box, interleaved launches); 150-200 ticks were best.
+static uint32_t layer_down_delay(int n_used, int D, int F) {
+    const size_t g_bytes = (size_t)n_used * 2 * F * row_bytes(QT_IQ3_S, D);
+    return (uint32_t)std::min<size_t>(g_bytes / 75000, 1000);
+}
+
 // A one-token IQ3_S layer as one launch (k_layer_decode) when it applies:
 // returns 1 when launched, 0 when the two-kernel form must run, -1 on error.
 static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, const ExpertSrc& DS, const Routing& rt,
@@ -1217,7 +1228,7 @@ static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, cons
         launch_kernel(KK_LAYER, k_clear_sync, dim3(1), dim3(256), 0, st, sync);
         g_sync_reset_pending = false;
     }
-    LayerArgs a{gu, dn, n_g, g_tiles, n_d, sync, g_layer_wait_test ? 1u : 0u};
+    LayerArgs a{gu, dn, n_g, g_tiles, n_d, sync, g_layer_wait_test ? 1u : 0u, layer_down_delay(n_used, D, F)};
     g_layer_wait_test = false;
     launch_kernel(KK_LAYER, k_layer_decode<kLayerThreads>, dim3((unsigned)(n_g + n_d)), dim3(kLayerThreads), dyn, st, a);
     return ck(hipGetLastError(), "fused layer launch") ? 1 : -1;

@@ -181,10 +181,10 @@ class ChainGraph:
     the same scratch while no call has outgrown it."""
 
     def __init__(self, ex: MoEExecutor, n_tokens: int, k: int, descs=None):
-        L = ex.bank.n_layers
         dev = ex.device
         self.ex = ex
         self.descs = ex.layer_descs() if descs is None else descs
+        L = len(self.descs)                   # a chain may apply a layer more than once
         self.x = torch.zeros(n_tokens, ex.d_model, dtype=torch.float32, device=dev)
         self.ids = torch.zeros(L, n_tokens, k, dtype=torch.int32, device=dev)
         self.w = torch.zeros(L, n_tokens, k, dtype=torch.float32, device=dev)
@@ -201,5 +201,10 @@ class ChainGraph:
         self.x.copy_(x)
         self.ids.copy_(ids)
         self.w.copy_(w)
+        self.graph.replay()
+        return self.x
+
+    def replay_static(self) -> torch.Tensor:
+        """Replay on the inputs already in place: the graph's launches only."""
         self.graph.replay()
         return self.x
