@@ -129,9 +129,13 @@ __device__ inline bool wait_flags(const uint32_t* sync, int n, uint32_t target) 
 }
 
 // a whole 128-byte flag line set to v by the first 32 lanes of wave 0 (one
-// store instruction), agent scope
+// ordinary store instruction).  The line stays in this XCD's L2, and the
+// XCD's agent-scope polls (wait_word) see it there at once: an agent-scope
+// load returns a line its L2 holds modified (measured on MI355X: a plain
+// store seen by the sc1 polls of every CU of its XCD before the store's own
+// completion returned to the writer, and by no CU of another XCD).
 __device__ inline void store_flag_line(uint32_t* line, uint32_t v) {
-    if (threadIdx.x < kLine) __hip_atomic_store(line + threadIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < kLine) line[threadIdx.x] = v;
 }
 
 template <int NT>
