@@ -103,36 +103,48 @@ def main() -> int:
     ids_np, w_np = W.route(rng, n_tokens=P, n_layers=G)             # [G, P, k]
     ids_np = np.ascontiguousarray(ids_np.transpose(1, 0, 2))[:, :, None, :]   # [P, G, 1, k]
     w_np = np.ascontiguousarray(w_np.transpose(1, 0, 2))[:, :, None, :]
-    x_np = rng.standard_normal((P, 1, W.d_model)).astype(np.float32)
+    # a model's chain carries x from layer to layer; a one-layer workload's G
+    # calls each get their own input row (the same layer applied G times on
+    # one residual stream grows x without bound: the gated FFN is quadratic)
+    x_np = rng.standard_normal((P, 1 if W.n_layers > 1 else G, W.d_model)).astype(np.float32)
     ids = torch.from_numpy(ids_np).to(dev)
     wts = torch.from_numpy(w_np).to(dev)
     xs = torch.from_numpy(x_np).to(dev)
-    x_buf = torch.empty(1, W.d_model, dtype=torch.float32, device=dev)
     ex = MoEExecutor(bank, max_used=W.top_k)
-    if W.n_layers > 1:
-        descs = ex.layer_descs()
-    else:
-        descs = (rt.MoeLayerDesc * G)(*([bank.layer_desc(0, None)] * G))
     step_bytes = [W.step_expert_bytes(ids_np[p, :, 0][:, None, :]) for p in range(P)]
+    if W.n_layers > 1:
+        x_buf = torch.empty(1, W.d_model, dtype=torch.float32, device=dev)
+        descs = ex.layer_descs()
 
-    def eager_step(i):
-        p = i % P
-        x_buf.copy_(xs[p])
-        ex.run_chain(x_buf, ids[p], wts[p], descs)
+        def eager_step(i):
+            p = i % P
+            x_buf.copy_(xs[p])
+            ex.run_chain(x_buf, ids[p], wts[p], descs)
+            return x_buf
 
-    # the timed steps replay the chain captured as one HIP graph
-    cg = ChainGraph(ex, 1, W.top_k, descs)
+        # the timed steps replay the chain captured as one HIP graph
+        cg = ChainGraph(ex, 1, W.top_k, descs)
+    else:
+        y_buf = torch.empty(G, W.d_model, dtype=torch.float32, device=dev)
+
+        def eager_step(i):
+            p = i % P
+            for g in range(G):
+                ex.run_layer(0, xs[p, g:g + 1], ids[p, g], wts[p, g], out=y_buf[g:g + 1])
+            return y_buf
+
+        cg = LayerCallsGraph(ex, G, W.d_model, W.top_k)
 
     def graph_step(i):
         p = i % P
         cg.replay(xs[p], ids[p], wts[p])
 
-    # the graph computes what the eager chain computes, bit for bit
-    eager_step(0)
+    # the graph computes what the eager calls compute, bit for bit
+    y_eager = eager_step(0).clone()
     graph_step(0)
     torch.cuda.synchronize()
-    if not torch.equal(x_buf, cg.x):
-        print("graph replay differs from the eager chain", file=sys.stderr)
+    if not torch.equal(y_eager, cg.x):
+        print("graph replay differs from the eager calls", file=sys.stderr)
         return 1
 
     def timed(step_fn, steps):
@@ -195,7 +207,7 @@ def main() -> int:
     achieved = per_launch["layer"] / (us_layer_graph * 1e3)                  # GB/s
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(W.name, "layer" if fused else None),
+                "traffic": measured_traffic(W.name, ["layer"] if fused else ["gate_up", "down"]),
                 "kernel": "layer" if fused else "layer (gate_up + down launches)",
                 "bytes_per_launch": per_launch["layer"], "avg_launch_us": round(us_layer_graph, 3),
                 "timing": "replayed graph, %d replays of %d layer calls" % (R, G)}
@@ -203,7 +215,7 @@ def main() -> int:
     cpu = None
     parity = None
     if not args.no_cpu:
-        cpu, parity = cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np, dev)
+        cpu, parity = cpu_baseline(args, W, bank, ex, ids_np, w_np, x_np[:, :1], dev)
 
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -215,11 +227,13 @@ def main() -> int:
                    "d_model": W.d_model, "d_ff": W.d_ff, "n_tokens": W.n_tokens, "quant": quant_note(W),
                    "bank_bytes": bank.total_bytes, "expert_bytes_per_step": nbytes // args.steps,
                    "layer_calls_per_step": G,
-                   "mode": ("one fused launch per layer (gate/up+SwiGLU and down+combine workgroups in one grid, h "
-                            "handed over in the kernel), the %d launches replayed as one HIP graph per step" % G
-                            if fused else
-                            "chain of per-layer kernels (gate/up+SwiGLU, down+combine) replayed as one HIP graph per "
-                            "step of %d layer calls" % G)},
+                   "mode": ("%s; %s" % (
+                       "one fused launch per layer (gate/up+SwiGLU and down+combine workgroups in one grid, h "
+                       "handed over in the kernel)" if fused else
+                       "two launches per layer (gate/up+SwiGLU, down+combine)",
+                       "the %d layers' launches replayed as one HIP graph per step (a residual chain)" % G
+                       if W.n_layers > 1 else
+                       "%d calls of the layer, each on its own input row, replayed as one HIP graph per step" % G))},
         "tok_s": round(1000.0 * (1 if W.n_layers > 1 else G) / ms_step, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "us_per_layer": round(1000.0 * ms_step / G, 3),
         "kernels": {k: {"launches": v["launches"], "avg_us": round(v["avg_us"], 3)} for k, v in kernels.items()},
@@ -227,16 +241,61 @@ def main() -> int:
         "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
     }
     print(json.dumps(line), flush=True)
-    if args.copy_probe_mib:
-        n = args.copy_probe_mib << 18                                   # floats
-        a = torch.ones(n, dtype=torch.float32, device=dev)
-        b = torch.empty_like(a)
-        torch.cuda.synchronize()
-        b.copy_(a)
-        torch.cuda.synchronize()
-        print("copy probe: %d MiB read, %d MiB written" % (args.copy_probe_mib, args.copy_probe_mib),
-              file=sys.stderr, flush=True)
+    copy_probe(args, dev)
     return 0
+
+
+def copy_probe(args, dev):
+    """One device-to-device copy of --copy-probe-mib MiB at the end of the run:
+    a plain copy kernel of known size, to calibrate the FETCH_SIZE / WRITE_SIZE
+    counters of the same run."""
+    if not args.copy_probe_mib:
+        return
+    import torch
+    n = args.copy_probe_mib << 18                                       # floats
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print("copy probe: %d MiB read, %d MiB written" % (args.copy_probe_mib, args.copy_probe_mib),
+          file=sys.stderr, flush=True)
+
+
+class LayerCallsGraph:
+    """G calls of a one-layer workload's layer (sabah_moe_layer), each on its
+    own input row with its own ids and weights, captured as one HIP graph over
+    static buffers; `x` holds the G output rows after a replay."""
+
+    def __init__(self, ex, G, d_model, k):
+        import torch
+        dev = ex.device
+        self.ex, self.G = ex, G
+        self.xin = torch.zeros(G, d_model, dtype=torch.float32, device=dev)
+        self.ids = torch.zeros(G, 1, k, dtype=torch.int32, device=dev)
+        self.w = torch.zeros(G, 1, k, dtype=torch.float32, device=dev)
+        self.x = torch.zeros(G, d_model, dtype=torch.float32, device=dev)
+        self._calls()                                  # eager: sizes the library scratch
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._calls()
+        torch.cuda.synchronize(dev)
+
+    def _calls(self):
+        for g in range(self.G):
+            self.ex.run_layer(0, self.xin[g:g + 1], self.ids[g], self.w[g], out=self.x[g:g + 1])
+
+    def replay(self, x, ids, w):
+        self.xin.copy_(x)
+        self.ids.copy_(ids)
+        self.w.copy_(w)
+        self.graph.replay()
+        return self.x
+
+    def replay_static(self):
+        self.graph.replay()
+        return self.x
 
 
 # kernel symbols of each timing kind, as the traffic summaries name them
@@ -404,12 +463,13 @@ def bench_batch(args, W):
         "token_major_us_per_layer": round(1000.0 * ms_token_major, 2) if ms_token_major else None,
         "kernels": {q: {"launches": v["launches"], "avg_us": v["avg_us"]} for q, v in kernels.items()},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(W.name, [dom]), "kernel": dom,
                      "bytes_per_launch": int(per_launch), "avg_launch_us": kernels[dom]["avg_us"]},
         "cpu_baseline": None if args.no_cpu else cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid),
         "parity": parity,
     }
     print(json.dumps(line), flush=True)
+    copy_probe(args, dev)
     return 0
 
 
@@ -450,21 +510,36 @@ def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid=False):
             "host": host_info(threads)}
 
 
-def measured_traffic(workload, kind):
-    """HBM bytes per launch of `kind` from the committed FETCH_SIZE / WRITE_SIZE
-    counter runs (calibrated against a plain copy), or None if not measured."""
-    if kind is None:
+# the committed profiles' name of each workload's summaries
+PROFILE_PREFIX = {"iq3s_48x512_top10": "decode_kernels_iq3s_48x512_top10",
+                  "q8_0_e8_top2": "decode_kernels_q8_0_e8_top2",
+                  "q4k_e128_top8": "decode_kernels_q4k_e128_top8",
+                  "iq3s_prefill_t512": "prefill_layer_iq3s_t512_e512_top10",
+                  "iq3s_mmid_t512": "mul_mat_id_iq3s_t512_e512_top10",
+                  "mixed_t32_q4k_q6k_shared": "mixed_layer_q4k_q6k_shared_t32"}
+
+
+def measured_traffic(workload, kinds):
+    """HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter
+    runs (calibrated against a plain copy), summed over the kernel kinds
+    `kinds` (a layer's launches) and averaged over the kernels of one kind (a
+    kind's routed and shared-expert launches); None if one was not measured."""
+    if not kinds or workload not in PROFILE_PREFIX:
         return None
-    path = os.path.join(ROOT, "profiles", "decode_kernels_%s_traffic.json" % workload)
+    path = os.path.join(ROOT, "profiles", "%s_traffic.json" % PROFILE_PREFIX[workload])
     try:
         with open(path) as f:
             kernels = json.load(f)["kernels"]
     except (OSError, KeyError, ValueError):
         return None
-    for sym in KERNEL_SYMBOL[kind]:
-        if sym in kernels:
-            return kernels[sym]["traffic_bytes"]
-    return None
+    total = 0
+    for kind in kinds:
+        hit = [v["traffic_bytes"] for name, v in kernels.items()
+               if any(name == sym or name.startswith(sym + "<") for sym in KERNEL_SYMBOL[kind])]
+        if not hit:
+            return None
+        total += sum(hit) / len(hit)                # a kind's launches of one step, on average
+    return int(total)
 
 
 def cpu_threads(args):
