@@ -148,31 +148,46 @@ __global__ __launch_bounds__(kThreads) void k_quant_rows(const float* __restrict
 // result's lane l holds column l % 16 and rows 4 (l / 16) .. +3.
 // ---------------------------------------------------------------------------
 
-// IQ3_S A operand: the eight weights of row `unit`'s sub-block `sub` that lane
-// quarter q holds (grid groups 2q, 2q + 1), from the staged unit bytes and the
-// signed codebook table
-__device__ inline long iq3s_a_operand(const uint8_t* unit, const uint8_t* tabs, int sub, int q) {
-    const uint32_t qs = unit[2 + 8 * sub + 2 * q] | (uint32_t)unit[3 + 8 * sub + 2 * q] << 8;   // any alignment
-    const uint32_t qh = unit[66 + sub] >> (2 * q);
-    const uint32_t sg = unit[74 + 4 * sub + q];
-    const uint32_t i0 = (qs & 0xFFu) + 256u * ((sg & 15u) + 16u * (qh & 1u));
-    const uint32_t i1 = (qs >> 8) + 256u * ((sg >> 4) + 16u * ((qh >> 1) & 1u));
+// The weights are the B operand (columns = the tile's 16 rows, lane l holding
+// row l % 16's eight k-values 8 (l / 16) .. +7 of a sub-block), the pairs'
+// activations the A operand; so the int32 result's lane l holds row l % 16
+// for pairs 4 (l / 16) .. +3, and the row's sub-block scales and d are the
+// lane's own.
+//
+// What lane quarter q of a staged IQ3_S unit needs for each of the unit's
+// eight sub-blocks s: the qs bytes 8s + 2q, 8s + 2q + 1 (grid groups 2q and
+// 2q + 1), their ninth index bits (bits 2q, 2q + 1 of qh[s]) and sign
+// nibbles (byte 4s + q of the signs); and the unit's sub-block scales and d.
+// Read once per block (the unit starts at an even byte).
+struct Iq3sQuarter {
+    uint32_t qs[4];               // halfword s of qs[s >> 1]: the lane's two qs bytes of sub-block s
+    uint32_t qh[2];               // qh bytes 0..7
+    uint32_t sg[2];               // byte s of sg[s >> 2]: the lane's sign byte of sub-block s
+    uint32_t sc;                  // the four scale bytes (nibble s: sub-block s)
+    uint32_t d;                   // fp16 d (low half)
+};
+__device__ inline void iq3s_quarter_fields(const uint8_t* unit, int q, Iq3sQuarter& F) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(unit);
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+        F.qs[p] = (uint32_t)h[1 + 8 * p + q] | (uint32_t)h[5 + 8 * p + q] << 16;   // bytes 2 + 8s + 2q, s = 2p, 2p + 1
+    F.qh[0] = (uint32_t)h[33] | (uint32_t)h[34] << 16;
+    F.qh[1] = (uint32_t)h[35] | (uint32_t)h[36] << 16;
+    const uint8_t* sg = unit + 74 + q;
+    F.sg[0] = (uint32_t)sg[0] | (uint32_t)sg[4] << 8 | (uint32_t)sg[8] << 16 | (uint32_t)sg[12] << 24;
+    F.sg[1] = (uint32_t)sg[16] | (uint32_t)sg[20] << 8 | (uint32_t)sg[24] << 16 | (uint32_t)sg[28] << 24;
+    F.sc = (uint32_t)h[53] | (uint32_t)h[54] << 16;
+    F.d = h[0];
+}
+// the lane's eight weights of sub-block s (B operand) from the signed codebook table
+__device__ inline long iq3s_quarter_operand(const Iq3sQuarter& F, const uint8_t* tabs, int s, int q) {
+    const uint32_t qs2 = (F.qs[s >> 1] >> (16 * (s & 1))) & 0xFFFFu;
+    const uint32_t qh2 = (F.qh[s >> 2] >> (8 * (s & 3) + 2 * q)) & 3u;
+    const uint32_t sgb = (F.sg[s >> 2] >> (8 * (s & 3))) & 0xFFu;
+    const uint32_t i0 = (qs2 & 0xFFu) + 256u * ((sgb & 15u) + 16u * (qh2 & 1u));
+    const uint32_t i1 = (qs2 >> 8) + 256u * ((sgb >> 4) + 16u * (qh2 >> 1));
     const uint32_t g0 = lds_u32(tabs, kLdsGrid + 4u * i0), g1 = lds_u32(tabs, kLdsGrid + 4u * i1);
     return (long)(((uint64_t)g1 << 32) | g0);
-}
-
-// per (matrix, sub-block, row) scale 2 * nibble + 1 and per (matrix, block, row) d of
-// the staged IQ3_S tiles: unit u = (m * nrows + r) * nb + b
-__device__ inline void iq3s_scale_tables(const uint8_t* stage, int cpt, const int* leads, int n_mat, int nrows,
-                                         int nb, size_t rb, uint8_t* ls_tab, float* dw_tab) {
-    for (int u = threadIdx.x; u < n_mat * nrows * nb; u += blockDim.x) {
-        const int b = u % nb, mr = u / nb, r = mr % nrows, m = mr / nrows;
-        const uint8_t* unit = stage + 16 * cpt * m + leads[m] + (size_t)r * rb + 110 * b;
-        dw_tab[(m * nb + b) * nrows + r] = h2f(unit[0] | (uint32_t)unit[1] << 8);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            ls_tab[((m * nb + b) * 8 + j) * nrows + r] = (uint8_t)(2 * ((unit[106 + j / 2] >> (4 * (j & 1))) & 15) + 1);
-    }
 }
 
 // the staged tiles' loads only (no decode): tiles_begin issued them
@@ -182,8 +197,8 @@ __device__ inline void tiles_stage(TileRun<QT>& S, uint8_t* stage, int* leads) {
 }
 
 // One pair's activation words for blocks [b0, b1) of a row (this lane's MFMA
-// column and k-quarter q), and the blocks' scales.  Loaded ahead of the
-// MFMAs that use them, so their latency is paid once.
+// row and k-quarter q), and the blocks' scales.  Loaded ahead of the MFMAs
+// that use them, so their latency is paid once.
 template <int NBMAX>
 struct XRegs {
     long X[NBMAX][8];
@@ -203,33 +218,33 @@ __device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const float*
 
 // 16 rows x 16 pairs over blocks [b0, b1) of a row: per block, the exact int32
 // block sum sum_sub ls * (W_sub . x_sub), then c = (d_w * d_x) * bsum.  rowp is
-// the lane's staged weight row (decoded into the A operand as it is used);
+// the lane's staged weight row (decoded into the B operand as it is used);
 // lanes of a pair past the tile (valid false) multiply zeros.  c[blk][i] is
-// for the lane's rows 4q + i.
+// for the lane's row and pair 4q + i.
 template <int NBMAX>
 __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int b0, int b1, const XRegs<NBMAX>& R,
-                                   bool valid, const uint8_t* ls_tab, const float* dw_tab, int nrows, int rbase, int q,
-                                   float (&c)[NBMAX][4]) {
+                                   bool valid, int q, float (&c)[NBMAX][4]) {
 #pragma unroll
     for (int j = 0; j < NBMAX; ++j) {
         const int b = b0 + j;
         if (b >= b1) break;
+        Iq3sQuarter F;
+        iq3s_quarter_fields(rowp + 110 * b, q, F);
         int bs[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int sub = 0; sub < 8; ++sub) {
             v4i32 z = {0, 0, 0, 0};
-            const long A = iq3s_a_operand(rowp + 110 * b, tabs, sub, q);
-            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, valid ? R.X[j][sub] : 0, z, 0, 0, 0);
-            const uint32_t ls4 = *reinterpret_cast<const uint32_t*>(ls_tab + (b * 8 + sub) * nrows + rbase + 4 * q);
+            const long B = iq3s_quarter_operand(F, tabs, sub, q);
+            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(valid ? R.X[j][sub] : 0, B, z, 0, 0, 0);
+            const int ls = 2 * (int)((F.sc >> (4 * sub)) & 15u) + 1;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bs[i] += __mul24((int)((ls4 >> (8 * i)) & 0xFFu), d[i]);
+            for (int i = 0; i < 4; ++i) bs[i] += __mul24(ls, d[i]);
         }
+        // d_x of the output pairs 4q .. 4q + 3: lanes 4q + i hold them (lane l loads pair l % 16)
         const float dxv = valid ? R.dx[j] : 0.0f;
-        const float4 dw = *reinterpret_cast<const float4*>(dw_tab + b * nrows + rbase + 4 * q);
-        c[j][0] = __fmul_rn(__fmul_rn(dw.x, dxv), (float)bs[0]);
-        c[j][1] = __fmul_rn(__fmul_rn(dw.y, dxv), (float)bs[1]);
-        c[j][2] = __fmul_rn(__fmul_rn(dw.z, dxv), (float)bs[2]);
-        c[j][3] = __fmul_rn(__fmul_rn(dw.w, dxv), (float)bs[3]);
+        const float dw = h2f(F.d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c[j][i] = __fmul_rn(__fmul_rn(dw, __shfl(dxv, 4 * q + i)), (float)bs[i]);
     }
 }
 
@@ -270,8 +285,6 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
     const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
     if (n_e == 0) return;                                  // uniform: the whole workgroup leaves
     SABAH_STATIC_LDS(QT)
-    __shared__ __align__(16) uint8_t ls_tab[2 * 8 * kGuBlocksPerWave * 2 * kGuRows];
-    __shared__ __align__(16) float dw_tab[2 * kGuBlocksPerWave * 2 * kGuRows];
     __shared__ __align__(16) float part[2][kGuBlocksPerWave][kGuRows][kPairTile];
     __shared__ __align__(16) float gu[2][kGuRows][kPairTile];
     const int row0 = blockIdx.x * (MMID ? 2 * kGuRows : kGuRows);
@@ -295,25 +308,21 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
     };
     store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     tiles_stage(S, stage, leads);
-    __syncthreads();
-    iq3s_scale_tables(stage, S.cpt, leads, 2, kGuRows, nb, rb, ls_tab, dw_tab);
+    __syncthreads();                                        // staged rows and table written
     XRegs<kGuBlocksPerWave> XR;
     const uint8_t* rowp = stage + 16 * S.cpt * m + leads[m] + (size_t)r * rb;
-    __syncthreads();                                        // scale tables written
-    const uint8_t* lsm = ls_tab + m * (nb * 8 * kGuRows);
-    const float* dwm = dw_tab + m * (nb * kGuRows);
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
         pair_x(pt, XR);
         float c[kGuBlocksPerWave][4];
-        mfma_blocks<kGuBlocksPerWave>(rowp, tabs, b0, b1, XR, valid, lsm, dwm, kGuRows, 0, q, c);
+        mfma_blocks<kGuBlocksPerWave>(rowp, tabs, b0, b1, XR, valid, q, c);
         if (half) {
 #pragma unroll
             for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
                 if (b0 + jj < b1)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) part[m][jj][4 * q + i][j] = c[jj][i];
+                    for (int i = 0; i < 4; ++i) part[m][jj][r][4 * q + i] = c[jj][i];
         }
         __syncthreads();
         if (!half) {
@@ -323,8 +332,8 @@ __global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs 
 #pragma unroll
                 for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
                     if (jj < b1 - b0) acc = __fadd_rn(acc, c[jj][i]);
-                for (int jj = 0; jj < nb - nb0; ++jj) acc = __fadd_rn(acc, part[m][jj][4 * q + i][j]);
-                gu[m][4 * q + i][j] = acc;
+                for (int jj = 0; jj < nb - nb0; ++jj) acc = __fadd_rn(acc, part[m][jj][r][4 * q + i]);
+                gu[m][r][4 * q + i] = acc;
             }
         }
         __syncthreads();
@@ -370,8 +379,6 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
     const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
     if (n_e == 0) return;
     SABAH_STATIC_LDS(QT)
-    __shared__ __align__(16) uint8_t ls_tab[8 * kDownBlocks * kDownRows];
-    __shared__ __align__(16) float dw_tab[kDownBlocks * kDownRows];
     const int row0 = blockIdx.x * kDownRows;
     const int nb = a.d_ff / 256;
     const size_t rb = row_bytes(QT, a.d_ff);
@@ -391,29 +398,27 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
     };
     store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
     tiles_stage(S, stage, leads);
-    __syncthreads();
-    iq3s_scale_tables(stage, S.cpt, leads, 1, kDownRows, nb, rb, ls_tab, dw_tab);
+    __syncthreads();                                        // staged rows and table written
     const uint8_t* rowp = stage + leads[0] + (size_t)(rbase + r) * rb;
-    __syncthreads();
     XRegs<kDownBlocks> XR;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
-        const int pos = g0 + pt + min(j, cnt - 1);
         pair_x(pt, XR);
         float c[kDownBlocks][4];
-        mfma_blocks<kDownBlocks>(rowp, tabs, 0, nb, XR, valid, ls_tab, dw_tab, kDownRows, rbase, q, c);
-        if (valid) {
-            float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, a.pair_of[pos])
-                              : a.y + (size_t)pos * a.d_model;
+        mfma_blocks<kDownBlocks>(rowp, tabs, 0, nb, XR, valid, q, c);
+        // the lane's row for pairs 4q .. 4q + 3
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float acc = 0.0f;
+        for (int i = 0; i < 4; ++i) {
+            if (4 * q + i >= cnt) break;
+            float acc = 0.0f;
 #pragma unroll
-                for (int jj = 0; jj < kDownBlocks; ++jj)
-                    if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
-                out[row0 + rbase + 4 * q + i] = acc;
-            }
+            for (int jj = 0; jj < kDownBlocks; ++jj)
+                if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
+            const int pi = g0 + pt + 4 * q + i;
+            float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, a.pair_of[pi])
+                              : a.y + (size_t)pi * a.d_model;
+            out[row0 + rbase + r] = acc;
         }
     }
 }
