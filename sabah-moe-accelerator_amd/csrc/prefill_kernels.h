@@ -129,16 +129,22 @@ __global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
 // ---------------------------------------------------------------------------
 // q8 rows in the kernels' activation layout (ActLayout), n_rows rows of k
 // floats.  Each workgroup quantises 16 chunk-rows (one per 16-lane row).
+// With `gather`, output row r is input row gather[r] / gdiv, for the rows
+// below *count (the grouped pairs: the rows come out in group order).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void k_quant_rows(const float* __restrict__ x, int n_rows, int k, int at,
-                                                         uint8_t* __restrict__ out, int out_stride) {
+                                                         uint8_t* __restrict__ out, int out_stride,
+                                                         const int* __restrict__ gather, int gdiv,
+                                                         const int* __restrict__ count) {
     const int nch = k / 256;
     const int q = blockIdx.x * (kThreads / 16) + (int)(threadIdx.x >> 4);
     if (q >= n_rows * nch) return;                       // whole 16-lane rows leave together
     const int r = q / nch, c = q - r * nch;
+    if (count && r >= *count) return;
+    const int src = gather ? gather[r] / gdiv : r;
     const ActBatch B{x, (size_t)k, n_rows, k, at, out, out_stride};
     Act16 v;
-    load16(x + (size_t)r * k, c * 256 + 16 * (int)(threadIdx.x & 15u), k, act_vec(B), v);
+    load16(x + (size_t)src * k, c * 256 + 16 * (int)(threadIdx.x & 15u), k, act_vec(B), v);
     quant_chunk(B, v, q);
 }
 
@@ -249,25 +255,32 @@ __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int
 }
 
 // ---------------------------------------------------------------------------
-// Grouped gate/up + SwiGLU.  grid = (d_ff / 16, n_experts), 256 threads.
-// Wave w: matrix w >> 1 (gate, up), blocks of k [nb0, nb) for w & 1, else
-// [0, nb0).  Each wave runs its 16 rows x blocks against every 16-pair tile
-// of the expert, decoding the staged rows into MFMA operands as it goes; the
-// two halves meet in LDS, in block order, before SwiGLU.
+// Grouped gate/up + SwiGLU.  grid = (d_ff / 16, n_experts), 512 threads.
+// Wave w: matrix w >> 2 (gate, up), blocks [b0, b1) of k for quarter w & 3.
+// Each wave runs its 16 rows x blocks against every 16-pair tile of the
+// expert, decoding the staged rows into MFMA operands as it goes; the
+// quarters' block results meet in LDS and are summed in block order before
+// SwiGLU.  The activation rows are the pairs' rows in group order (k_quant_rows
+// with the grouping as its gather), so a pair tile's activations load from
+// the group offset alone, at the start.
 // ---------------------------------------------------------------------------
+constexpr int kGuThreads = 512;
+constexpr int kGuWaveBlocks = 2;              // 256-blocks of k per wave (four waves per matrix)
+constexpr int kGuMaxBlocks = 4 * kGuWaveBlocks;
+// weight staging: both matrices' 16 rows at k <= 2048, each at any lead
+constexpr int kGuStageBytes = 2 * 16 * (kGuRows * kGuMaxBlocks * 110 / 16 + 2);
+
 struct GroupedGateUpArgs {
     const uint8_t *gate, *up;     // bank bases [n_experts][d_ff][row bytes]
     size_t expert_stride;
     const int* off;
     const int* pair_of;
-    int k;                        // slots per token: pair p is token p / k
-    const uint8_t* xq;            // q8_K rows per token, xq_stride bytes apart
+    int k;                        // slots per token (MMID: n_ids)
+    const uint8_t* xq;            // q8_K rows of the pairs in group order, xq_stride bytes apart
     int xq_stride;
     float* h;                     // [pairs in group order][d_ff]
     int d_model, d_ff;
-    // MMID: x row of pair p = p / x_div (1: a row per slot, k: a row per token);
-    // rows 32 b .. 32 b + 31 of the one matrix at gate; out = dst[t][s]
-    int x_div;
+    // MMID: rows 32 b .. 32 b + 31 of the one matrix at gate; out = dst[t][s]
     float* dst;
     size_t dst_nb1, dst_nb2;
 };
@@ -279,75 +292,68 @@ __device__ inline float* pair_dst(float* dst, size_t nb1, size_t nb2, int n_ids,
 }
 
 template <bool MMID = false>
-__global__ __launch_bounds__(kThreads) void k_grouped_gate_up(GroupedGateUpArgs a) {
-    constexpr int QT = QT_IQ3_S;
+__global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUpArgs a) {
+    constexpr int QT = QT_IQ3_S, NT = kGuThreads;
     const int e = blockIdx.y;
     const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
     if (n_e == 0) return;                                  // uniform: the whole workgroup leaves
-    SABAH_STATIC_LDS(QT)
-    __shared__ __align__(16) float part[2][kGuBlocksPerWave][kGuRows][kPairTile];
-    __shared__ __align__(16) float gu[2][kGuRows][kPairTile];
+    __shared__ __align__(16) uint8_t tabs[kLdsTables];
+    __shared__ int leads[2];
+    __shared__ __align__(16) uint8_t stage_mem[16 + kGuStageBytes + 16];   // guards: the decoder reads past a unit's ends
+    __shared__ __align__(16) float part[2][kGuMaxBlocks][kGuRows][kPairTile];
+    uint8_t* const stage = stage_mem + 16;
     const int row0 = blockIdx.x * (MMID ? 2 * kGuRows : kGuRows);
-    const int nb = a.d_model / 256, nb0 = nb / 2;
+    const int nb = a.d_model / 256, bpw = (nb + 3) / 4;
     const size_t rb = row_bytes(QT, a.d_model);
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
-    const int m = wave >> 1, half = wave & 1, r = lane & 15, q = lane >> 4, j = lane & 15;
-    const int b0 = half ? nb0 : 0, b1 = half ? nb : nb0;
+    const int m = wave >> 2, r = lane & 15, q = lane >> 4, j = lane & 15;
+    const int b0 = min(nb, (wave & 3) * bpw), b1 = min(nb, b0 + bpw);
+    const int xb0 = min(b0, nb - 1), xb1 = max(b1, xb0 + 1);      // the blocks this wave's X covers (valid ones)
     const ActLayout XL(a.d_model, QT_Q8_K);
-    GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    GridRegs<NT> gr = load_grid_regs<NT>((int)threadIdx.x);
     const uint8_t* wg = a.gate + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     const uint8_t* wu = MMID ? wg + (size_t)kGuRows * rb : a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     auto tile_ptr = [&](int mm) { return mm ? wu : wg; };
-    TileRun<QT> S{TileWalk<QT>(2, kGuRows, rb, a.d_model)};
+    TileRun<QT, NT> S{TileWalk<QT, NT>(2, kGuRows, rb, a.d_model)};
     tiles_begin(S, tile_ptr);
-    auto pair_x = [&](int pt, XRegs<kGuBlocksPerWave>& R) {
+    auto pair_x = [&](int pt, XRegs<kGuWaveBlocks>& R) {
         const int cnt = min(kPairTile, n_e - pt);
-        const int t = a.pair_of[g0 + pt + min(j, cnt - 1)] / (MMID ? a.x_div : a.k);
-        const uint8_t* xrow = a.xq + (size_t)t * a.xq_stride;
-        load_x(R, xrow, reinterpret_cast<const float*>(xrow + XL.off_d), b0, b1, q);
+        const uint8_t* xrow = a.xq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.xq_stride;
+        load_x(R, xrow, reinterpret_cast<const float*>(xrow + XL.off_d), xb0, xb1, q);
     };
-    store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
-    tiles_stage(S, stage, leads);
+    XRegs<kGuWaveBlocks> XR;
+    pair_x(0, XR);                                          // with the weights
+    store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
+    pass_store(S, stage, leads);
     __syncthreads();                                        // staged rows and table written
-    XRegs<kGuBlocksPerWave> XR;
     const uint8_t* rowp = stage + 16 * S.cpt * m + leads[m] + (size_t)r * rb;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
-        pair_x(pt, XR);
-        float c[kGuBlocksPerWave][4];
-        mfma_blocks<kGuBlocksPerWave>(rowp, tabs, b0, b1, XR, valid, q, c);
-        if (half) {
+        if (pt) pair_x(pt, XR);
+        float c[kGuWaveBlocks][4];
+        mfma_blocks<kGuWaveBlocks>(rowp, tabs, b0, b1, XR, valid, q, c);
 #pragma unroll
-            for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
-                if (b0 + jj < b1)
+        for (int jj = 0; jj < kGuWaveBlocks; ++jj)
+            if (b0 + jj < b1)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) part[m][jj][r][4 * q + i] = c[jj][i];
-        }
+                for (int i = 0; i < 4; ++i) part[m][b0 + jj][r][4 * q + i] = c[jj][i];
         __syncthreads();
-        if (!half) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int jj = 0; jj < kGuBlocksPerWave; ++jj)
-                    if (jj < b1 - b0) acc = __fadd_rn(acc, c[jj][i]);
-                for (int jj = 0; jj < nb - nb0; ++jj) acc = __fadd_rn(acc, part[m][jj][r][4 * q + i]);
-                gu[m][r][4 * q + i] = acc;
+        // thread (pair jp, row rr), rows fastest: both matrices' block sums in block order
+        const int t = (int)threadIdx.x, rr = t & 15, jp = (t >> 4) & 15;
+        if (t < 256 && jp < cnt) {
+            float g = 0.0f, u = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                g = __fadd_rn(g, part[0][b][rr][jp]);
+                u = __fadd_rn(u, part[1][b][rr][jp]);
             }
-        }
-        __syncthreads();
-        if constexpr (MMID) {
-            const int rr = (int)threadIdx.x >> 4, jj = (int)threadIdx.x & 15;
-            if (jj < cnt) {
-                float* d = pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.k, a.pair_of[g0 + pt + jj]);
-                d[row0 + rr] = gu[0][rr][jj];
-                d[row0 + kGuRows + rr] = gu[1][rr][jj];
+            if constexpr (MMID) {
+                float* d = pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.k, a.pair_of[g0 + pt + jp]);
+                d[row0 + rr] = g;
+                d[row0 + kGuRows + rr] = u;
+            } else {
+                a.h[(size_t)(g0 + pt + jp) * a.d_ff + row0 + rr] = __fmul_rn(silu_f32(g), u);
             }
-        } else {
-            const int rr = (int)threadIdx.x >> 4, jj = (int)threadIdx.x & 15;
-            if (jj < cnt)
-                a.h[(size_t)(g0 + pt + jj) * a.d_ff + row0 + rr] = __fmul_rn(silu_f32(gu[0][rr][jj]), gu[1][rr][jj]);
         }
         __syncthreads();
     }
@@ -365,9 +371,9 @@ struct GroupedDownArgs {
     int hq_stride;
     float* y;                     // [pairs in group order][d_model]
     int d_model, d_ff;
-    // MMID: input row of pair p = hq + (p / x_div) * hq_stride; out = dst[t][s]
+    // MMID: the q8 rows are the pairs' input rows in group order; out = dst[t][s]
     const int* pair_of;
-    int n_ids, x_div;
+    int n_ids;
     float* dst;
     size_t dst_nb1, dst_nb2;
 };
@@ -393,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
     auto pair_x = [&](int pt, XRegs<kDownBlocks>& R) {
         const int cnt = min(kPairTile, n_e - pt);
         const int pos = g0 + pt + min(j, cnt - 1);
-        const uint8_t* hrow = a.hq + (size_t)(MMID ? a.pair_of[pos] / a.x_div : pos) * a.hq_stride;
+        const uint8_t* hrow = a.hq + (size_t)pos * a.hq_stride;
         load_x(R, hrow, reinterpret_cast<const float*>(hrow + HL.off_d), 0, nb, q);
     };
     store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);

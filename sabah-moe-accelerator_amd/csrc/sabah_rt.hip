@@ -768,7 +768,7 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
     const int xq_stride = (int)XL.bytes;
     int* off = static_cast<int*>(grow_scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
     int* pair_of = static_cast<int*>(grow_scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
-    uint8_t* xq = static_cast<uint8_t*>(grow_scratch(g_scratch_gxq, (size_t)xq_stride * nx, st));
+    uint8_t* xq = static_cast<uint8_t*>(grow_scratch(g_scratch_gxq, (size_t)xq_stride * P, st));
     if (!off || !pair_of || !xq) return -1;
     int* pos_of = pair_of + P;
     GroupArgs ga{d_ids, n_tokens, n_ids, E, off, pair_of, pos_of, g_err_dev, d_dst, dst_id_stride, dst_token_stride, rows};
@@ -776,10 +776,12 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
     // (KK_MMID), so a call's kernel time covers all three of its launches
     launch_kernel(KK_MMID, k_group_pairs, dim3(1), dim3(kGroupThreads), (int)sizeof(int) * (2 * E + kGroupThreads), st,
                   ga);
-    const int xq_rows = nx * (k / 256);
-    launch_kernel(KK_MMID, k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, nx, k,
-                  (int)QT_Q8_K, xq, xq_stride);
-    const int x_div = x_rows == 1 ? n_ids : 1;      // pair p = t * n_ids + s reads x row p / x_div
+    // the pairs' x rows, quantised in group order (pair p = t * n_ids + s reads x row p / x_div)
+    const int x_div = x_rows == 1 ? n_ids : 1;
+    const size_t xq_rows = P * (size_t)(k / 256);
+    launch_kernel(KK_MMID, k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, (int)P, k,
+                  (int)QT_Q8_K, xq, xq_stride, (const int*)pair_of, x_div, (const int*)(off + E));
+    (void)nx;
     if (form == 1) {
         GroupedDownArgs dn{};
         dn.down = bank;
@@ -791,7 +793,6 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
         dn.d_ff = k;
         dn.pair_of = pair_of;
         dn.n_ids = n_ids;
-        dn.x_div = x_div;
         dn.dst = d_dst;
         dn.dst_nb1 = dst_id_stride;
         dn.dst_nb2 = dst_token_stride;
@@ -807,12 +808,11 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
         gu.xq_stride = xq_stride;
         gu.d_model = k;
         gu.d_ff = rows;
-        gu.x_div = x_div;
         gu.dst = d_dst;
         gu.dst_nb1 = dst_id_stride;
         gu.dst_nb2 = dst_token_stride;
         launch_kernel(KK_MMID, k_grouped_gate_up<true>, dim3((unsigned)(rows / (2 * kGuRows)), (unsigned)E),
-                      dim3(kThreads), 0, st, gu);
+                      dim3(kGuThreads), 0, st, gu);
     }
     return ck(hipGetLastError(), "grouped MUL_MAT_ID launch") ? 0 : -1;
 }
@@ -1039,7 +1039,7 @@ static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D,
         const int n_rows = n_tokens * n_slots;
         const int chunk_rows = n_rows * (d_ff / 256);
         launch_kernel(KK_DOWN, k_quant_rows, dim3((unsigned)((chunk_rows + 15) / 16)), dim3(kThreads), 0, st, gu.h,
-                      n_rows, d_ff, act_type(qtd), hq, hb);
+                      n_rows, d_ff, act_type(qtd), hq, hb, (const int*)nullptr, 1, (const int*)nullptr);
         if (!ck(hipGetLastError(), "h quantisation launch")) return -1;
         a.hq = hq;
     }
@@ -1362,7 +1362,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     const int xq_stride = (int)XL.bytes, hq_stride = (int)HL.bytes;
     int* off = static_cast<int*>(grow_scratch(g_scratch_goff, sizeof(int) * (size_t)(E + 1), st));
     int* pair_of = static_cast<int*>(grow_scratch(g_scratch_gpair, 2 * sizeof(int) * P, st));
-    uint8_t* xq = static_cast<uint8_t*>(grow_scratch(g_scratch_gxq, (size_t)xq_stride * n_tokens, st));
+    uint8_t* xq = static_cast<uint8_t*>(grow_scratch(g_scratch_gxq, (size_t)xq_stride * P, st));
     float* h = static_cast<float*>(grow_scratch(g_scratch_gh, sizeof(float) * P * F, st));
     uint8_t* hq = static_cast<uint8_t*>(grow_scratch(g_scratch_ghq, (size_t)hq_stride * P, st));
     float* y = static_cast<float*>(grow_scratch(g_scratch_gy, sizeof(float) * P * D, st));
@@ -1378,9 +1378,10 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
 
     GroupArgs ga{d_ids, n_tokens, n_used, E, off, pair_of, pos_of, g_err_dev, nullptr, 0, 0, 0};
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);
-    const int xq_rows = n_tokens * (D / 256);
-    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, n_tokens, D,
-                       (int)QT_Q8_K, xq, xq_stride);
+    // the pairs' x rows in group order (pair p is token p / n_used)
+    const size_t xq_rows = P * (size_t)(D / 256);
+    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, (int)P, D,
+                       (int)QT_Q8_K, xq, xq_stride, (const int*)pair_of, n_used, (const int*)(off + E));
     GroupedGateUpArgs gu{};
     gu.gate = static_cast<const uint8_t*>(L->gate);
     gu.up = static_cast<const uint8_t*>(L->up);
@@ -1393,10 +1394,11 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     gu.h = h;
     gu.d_model = D;
     gu.d_ff = F;
-    launch_kernel(KK_GGATE_UP, k_grouped_gate_up<false>, dim3((unsigned)(F / kGuRows), (unsigned)E), dim3(kThreads), 0, st, gu);
+    launch_kernel(KK_GGATE_UP, k_grouped_gate_up<false>, dim3((unsigned)(F / kGuRows), (unsigned)E), dim3(kGuThreads), 0,
+                  st, gu);
     const size_t hq_rows = P * (size_t)(F / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((hq_rows + 15) / 16)), dim3(kThreads), 0, st, h, (int)P, F,
-                       (int)QT_Q8_K, hq, hq_stride);
+                       (int)QT_Q8_K, hq, hq_stride, (const int*)nullptr, 1, (const int*)(off + E));
     GroupedDownArgs dn{};
     dn.down = static_cast<const uint8_t*>(L->down);
     dn.expert_stride = row_bytes(QT_IQ3_S, F) * (size_t)D;

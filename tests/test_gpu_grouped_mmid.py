@@ -195,7 +195,7 @@ def test_scratch_growth_inside_a_capture_fails_and_says_why(hip_rt, orc, groupin
     rng = np.random.default_rng(15)
     raw = orc.quantize_weights(IQ3_S, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
     bank, rb = T(raw), raw.shape[-1]
-    big_t = 800                                             # x: 800 x 6 rows, larger than any call before
+    big_t = 1000                                            # 6000 pairs: more than any call before (5120)
     bid = T(np.stack([rng.choice(E - 1, K, replace=False) for _ in range(big_t)]).astype(np.int32))
     bx = T(rng.standard_normal((big_t, K, k)).astype(np.float32))
     out = torch.empty((big_t, K, rows), dtype=torch.float32, device=DEV)
