@@ -58,6 +58,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layer-fusion", type=int, default=1, choices=(0, 1),
                     help="1 (the library's default): one fused launch per layer; 0: gate/up then down + combine")
+    ap.add_argument("--grouping", default="auto", choices=("auto", "off"),
+                    help="batch workloads: auto runs the group-major layer when it takes the workload's types "
+                         "(gate/up of one type, each of IQ3_S, Q4_K, Q6_K) and there are at least 2 "
+                         "(token, slot) pairs per expert; off runs token-major")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="finish with one device-to-device copy of this many MiB (a plain copy kernel of known "
                          "size, to calibrate the FETCH_SIZE / WRITE_SIZE counters)")
@@ -308,9 +312,10 @@ INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
 def bench_batch(args, W):
     """One MoE layer over a batch of tokens (prefill / small-batch decode).
 
-    IQ3_S layers run group-major (sabah_moe_prefill_layer: pairs grouped by
-    expert, each expert read once, int8 MFMA); other formats run token-major
-    (sabah_moe_layer).  The bank holds 8 layers of the workload's shape and
+    Layers of IQ3_S, Q4_K and Q6_K with at least 2 (token, slot) pairs per
+    expert run group-major (sabah_moe_prefill_layer: pairs grouped by expert,
+    each expert read once, int8 MFMA); other layers, and every layer under
+    --grouping off, run token-major (sabah_moe_layer).  The bank holds 8 layers of the workload's shape and
     the steps rotate through them, so a step never finds the previous step's
     experts in the 256 MB last-level cache.  `value` is the step's algorithmic
     bytes / wall time: every distinct routed expert matrix once, the shared
@@ -343,7 +348,11 @@ def bench_batch(args, W):
     x = torch.from_numpy(x_np).to(dev)
     out = torch.empty_like(x)
     ex = MoEExecutor(bank, max_used=W.top_k, max_tokens=W.n_tokens, shared=shared)
-    grouped = W.qt_gate == W.qt_up == W.qt_down == rt.QTYPE["IQ3_S"]
+    grouped_types = {rt.QTYPE["IQ3_S"], rt.QTYPE["Q4_K"], rt.QTYPE["Q6_K"]}
+    # group-major from 2 (token, slot) pairs per expert on average: measured at top-10 of
+    # 512 (2048 / 768), the token-major layer is faster below that for every format
+    grouped = (args.grouping == "auto" and W.qt_gate == W.qt_up and W.qt_gate in grouped_types
+               and W.qt_down in grouped_types and W.n_tokens * W.top_k >= 2 * W.n_experts)
     T, k = W.n_tokens, W.top_k
     mmid = W.op == "mul_mat_id"
     if mmid:
@@ -446,7 +455,7 @@ def bench_batch(args, W):
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms / steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8",
-        "compute": ("int8 MFMA (v_mfma_i32_16x16x32_i8) on IQ3_S weights decoded to int8 x q8_K activations, "
+        "compute": ("int8 MFMA (v_mfma_i32_16x16x32_i8) on weights decoded to int8 x q8_K activations, "
                     "fp32 scales and accumulation" if grouped else
                     "int8 x int8 -> int32 dot products, fp32 scales and accumulation"),
         "data": "synthetic (N(0,0.02) weights quantised on device; seeded routing)",

@@ -15,17 +15,18 @@
 //
 // Kernels of one layer, in stream order:
 //   k_group_pairs     ids -> per-expert offsets and the pairs in group order
-//   k_quant_rows      x -> q8_K rows (ActLayout), one per token
+//   k_quant_rows      x -> q8_K rows (ActLayout), one per pair in group order
 //   k_grouped_gate_up h[pos] = silu(Wg[e] . q8(x[t])) * (Wu[e] . q8(x[t]))
 //   k_quant_rows      h -> q8_K rows, one per grouped pair
 //   k_grouped_down    y[pos] = Wd[e] . q8(h[pos])
 //   k_combine         out[t] = [resid +] ((y0 w0 + y1 w1) + ...) [+ shared]
-// Supported: IQ3_S gate, up and down; d_model / 256 even and <= 8; d_ff / 256 <= 4.
+// Supported: gate and up of one type, down of any, each IQ3_S, Q4_K or Q6_K;
+// d_model / 256 even and <= 8; d_ff / 256 <= 4.
 //
 // The same kernels, instantiated with MMID = true, run a grouped MUL_MAT_ID
 // (sabah_rt_mul_mat_id_v2 over many tokens): k_group_pairs, k_quant_rows on
-// x, then k_grouped_down<true> (k <= 1024, 64-row tiles) or
-// k_grouped_gate_up<true> (k <= 2048, two 16-row groups of one matrix in the
+// x, then k_grouped_down<QT, true> (k <= 1024, 64-row tiles) or
+// k_grouped_gate_up<QT, true> (k <= 2048, two 16-row groups of one matrix in the
 // places of gate and up, no SwiGLU), each reading x through the pair's token
 // (or its own row when x has one row per slot) and writing dst[t][slot].
 #pragma once
@@ -37,7 +38,6 @@ constexpr int kGroupThreads = 1024;
 constexpr int kPairTile = 16;                 // pairs per MFMA column tile
 constexpr int kGuRows = 16;                   // gate/up rows per workgroup (one MFMA row tile)
 constexpr int kDownRows = 64;                 // down rows per workgroup (four MFMA row tiles)
-constexpr int kGuBlocksPerWave = 4;           // 256-blocks of k per gate/up wave (two waves per matrix)
 constexpr int kDownBlocks = 4;                // 256-blocks of k per down wave (one wave per row tile)
 
 typedef int v4i32 __attribute__((ext_vector_type(4)));
@@ -196,22 +196,96 @@ __device__ inline long iq3s_quarter_operand(const Iq3sQuarter& F, const uint8_t*
     return (long)(((uint64_t)g1 << 32) | g0);
 }
 
-// the staged tiles' loads only (no decode): tiles_begin issued them
-template <int QT>
-__device__ inline void tiles_stage(TileRun<QT>& S, uint8_t* stage, int* leads) {
-    pass_store(S, stage, leads);
+// A dword of a staged unit at any even address (two 16-bit LDS reads)
+__device__ inline uint32_t lds_u32_even(const uint8_t* p) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    return (uint32_t)h[0] | (uint32_t)h[1] << 16;
+}
+
+// Q4_K: lane quarter q's eight elements of item j (elements 32j .. 32j + 31)
+// are nibbles (low for even j, high for odd) of qs bytes 32 (j / 2) + 8q ..
+// +7; the item's 6-bit scale and min (get_scale_min_k4) and the unit's d,
+// dmin are the row's.  Unit: d, dmin (4 B), scales (12 B), qs (128 B).
+struct Q4kQuarter {
+    uint32_t qs[8];               // qs bytes 32p + 8q .. +7 for p = 0..3, two dwords each
+    uint32_t sc[3];               // the 12 packed scale/min bytes
+    uint32_t dd;                  // fp16 d | fp16 dmin << 16
+};
+__device__ inline void q4k_quarter_fields(const uint8_t* unit, int q, Q4kQuarter& F) {
+    F.dd = lds_u32_even(unit);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) F.sc[i] = lds_u32_even(unit + 4 + 4 * i);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        F.qs[2 * p] = lds_u32_even(unit + 16 + 32 * p + 8 * q);
+        F.qs[2 * p + 1] = lds_u32_even(unit + 20 + 32 * p + 8 * q);
+    }
+}
+__device__ inline long q4k_quarter_operand(const Q4kQuarter& F, int j) {
+    const uint64_t w = (uint64_t)F.qs[2 * (j >> 1)] | (uint64_t)F.qs[2 * (j >> 1) + 1] << 32;
+    return (long)((w >> (4 * (j & 1))) & 0x0F0F0F0F0F0F0F0Full);
+}
+// get_scale_min_k4 (ggml) on the 12 scale bytes
+__device__ inline void q4k_quarter_scale_min(const Q4kQuarter& F, int j, int& sc, int& mn) {
+    if (j < 4) {
+        sc = (int)(byte_of(F.sc, j) & 63u);
+        mn = (int)(byte_of(F.sc, j + 4) & 63u);
+    } else {
+        sc = (int)((byte_of(F.sc, j + 4) & 0xFu) | ((byte_of(F.sc, j - 4) >> 6) << 4));
+        mn = (int)((byte_of(F.sc, j + 4) >> 4) | ((byte_of(F.sc, j) >> 6) << 4));
+    }
+}
+
+// Q6_K: item j = half h = j / 4, quarter t = j % 4: the low 4 bits of lane
+// quarter q's eight elements are nibbles t / 2 of ql bytes 64h + 32 (t & 1)
+// + 8q .. +7, the high 2 bits bits 2t of qh bytes 32h + 8q .. +7; value q6 -
+// 32.  The int8 scales (one per 16 elements) and d are the row's.  Unit: ql
+// (128 B), qh (64 B), scales (16 B), d (2 B).  The bits are read one half
+// at a time (fewer live registers).
+struct Q6kQuarter {
+    uint32_t sc[4];               // the 16 int8 scales
+    uint32_t d;                   // fp16 d (low half)
+};
+__device__ inline void q6k_quarter_fields(const uint8_t* unit, Q6kQuarter& F) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) F.sc[i] = lds_u32_even(unit + 192 + 4 * i);
+    F.d = reinterpret_cast<const uint16_t*>(unit + 208)[0];
+}
+// half h's bits for lane quarter q: ql bytes 64h + 32u + 8q .. +7 (u = 0, 1), qh bytes 32h + 8q .. +7
+struct Q6kHalf {
+    uint64_t ql[2], qh;
+};
+__device__ inline void q6k_half_fields(const uint8_t* unit, int h, int q, Q6kHalf& H) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        H.ql[u] = (uint64_t)lds_u32_even(unit + 64 * h + 32 * u + 8 * q) |
+                  (uint64_t)lds_u32_even(unit + 64 * h + 32 * u + 8 * q + 4) << 32;
+    H.qh = (uint64_t)lds_u32_even(unit + 128 + 32 * h + 8 * q) | (uint64_t)lds_u32_even(unit + 132 + 32 * h + 8 * q) << 32;
+}
+// item 4h + t
+__device__ inline long q6k_half_operand(const Q6kHalf& H, int t) {
+    const uint64_t lo = H.ql[t & 1] >> (4 * (t >> 1)), hi = H.qh >> (2 * t);
+    return (long)((lo & 0x0F0F0F0F0F0F0F0Full) | ((hi & 0x0303030303030303ull) << 4));
+}
+__device__ inline int q6k_quarter_scale(const Q6kQuarter& F, int s16) {
+    return (int)(int8_t)((F.sc[s16 >> 2] >> (8 * (s16 & 3))) & 0xFFu);
 }
 
 // One pair's activation words for blocks [b0, b1) of a row (this lane's MFMA
-// row and k-quarter q), and the blocks' scales.  Loaded ahead of the MFMAs
-// that use them, so their latency is paid once.
+// row and k-quarter q), the blocks' scales and, for the K formats, the q8_K
+// block sums the lane feeds the side products: Q4_K the two 32-element sums
+// of items q and q + 4, Q6_K the 16-element sums q, q + 4, q + 8, q + 12.
+// Loaded ahead of the MFMAs that use them, so their latency is paid once.
 template <int NBMAX>
 struct XRegs {
     long X[NBMAX][8];
     float dx[NBMAX];
+    float bsv[NBMAX][4];
 };
-template <int NBMAX>
-__device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const float* dxrow, int b0, int b1, int q) {
+template <int QT, int NBMAX>
+__device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const ActLayout& XL, int b0, int b1, int q) {
+    const float* dxrow = reinterpret_cast<const float*>(xrow + XL.off_d);
+    const int16_t* bsrow = reinterpret_cast<const int16_t*>(xrow + XL.off_bsum);
 #pragma unroll
     for (int j = 0; j < NBMAX; ++j) {
         const int b = min(b0 + j, b1 - 1);                 // blocks past b1 re-read the last one (unused)
@@ -219,40 +293,177 @@ __device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const float*
         for (int sub = 0; sub < 8; ++sub)
             R.X[j][sub] = *reinterpret_cast<const long*>(xrow + b * kActChunkStride + 32 * sub + 8 * q);
         R.dx[j] = dxrow[b];
+        if constexpr (QT == QT_Q4_K) {
+            R.bsv[j][0] = (float)((int)bsrow[16 * b + 2 * q] + (int)bsrow[16 * b + 2 * q + 1]);
+            R.bsv[j][1] = (float)((int)bsrow[16 * b + 2 * q + 8] + (int)bsrow[16 * b + 2 * q + 9]);
+        } else if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) R.bsv[j][t] = (float)bsrow[16 * b + q + 4 * t];
+        }
     }
 }
 
-// 16 rows x 16 pairs over blocks [b0, b1) of a row: per block, the exact int32
-// block sum sum_sub ls * (W_sub . x_sub), then c = (d_w * d_x) * bsum.  rowp is
-// the lane's staged weight row (decoded into the B operand as it is used);
-// lanes of a pair past the tile (valid false) multiply zeros.  c[blk][i] is
-// for the lane's row and pair 4q + i.
-template <int NBMAX>
+typedef float v4f32 __attribute__((ext_vector_type(4)));
+
+// 16 rows x 16 pairs over blocks [b0, b1) of a row: per block the row's exact
+// integer block sum(s) against the pair, as the token-major unit dot forms
+// them, then the same fp32 steps:
+//   IQ3_S: bsum = sum_sub ls * (W_sub . x_sub);            c = (d_w d_x) bsum
+//   Q4_K:  isum = sum_j sc_j (q_j . x_j), msum = sum_j mn_j bs_j;
+//          c = (d_w d_x) isum - (dmin_w d_x) msum
+//   Q6_K:  isum = sum_h sc_h (q_h . x_h) - 32 sum_h sc_h bs_h;   c = (d_w d_x) isum
+// The weight terms run on int8 MFMA (Q6_K: one per 16-element half, the other
+// half's activations zero); the bsum side terms on fp32 MFMA, exact because
+// every product and partial sum is an integer below 2^24.  rowp is the
+// lane's staged weight row; lanes of a pair past the tile (valid false)
+// multiply zeros.  c[blk][i] is for the lane's row and pair 4q + i.  PIN
+// (IQ3_S): form the block sum's first half before the second half's MFMAs
+// issue, so at most four MFMA results are live (a kernel at 128 VGPRs keeps
+// four waves per SIMD without spilling; with more registers to spare, the
+// unpinned order overlaps more MFMAs and is faster).
+template <int QT, int NBMAX, bool PIN = false>
 __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int b0, int b1, const XRegs<NBMAX>& R,
                                    bool valid, int q, float (&c)[NBMAX][4]) {
+    constexpr int UB = UnitFmt<QT>::BYTES;
 #pragma unroll
     for (int j = 0; j < NBMAX; ++j) {
         const int b = b0 + j;
         if (b >= b1) break;
-        Iq3sQuarter F;
-        iq3s_quarter_fields(rowp + 110 * b, q, F);
-        int bs[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int sub = 0; sub < 8; ++sub) {
-            v4i32 z = {0, 0, 0, 0};
-            const long B = iq3s_quarter_operand(F, tabs, sub, q);
-            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(valid ? R.X[j][sub] : 0, B, z, 0, 0, 0);
-            const int ls = 2 * (int)((F.sc >> (4 * sub)) & 15u) + 1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bs[i] += __mul24(ls, d[i]);
-        }
+        const uint8_t* unit = rowp + UB * b;
+        const v4i32 z = {0, 0, 0, 0};
         // d_x of the output pairs 4q .. 4q + 3: lanes 4q + i hold them (lane l loads pair l % 16)
         const float dxv = valid ? R.dx[j] : 0.0f;
-        const float dw = h2f(F.d);
+        auto dx_of = [&](int i) { return __shfl(dxv, 4 * q + i); };
+        if constexpr (QT == QT_IQ3_S) {
+            Iq3sQuarter F;
+            iq3s_quarter_fields(unit, q, F);
+            int bs[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) c[j][i] = __fmul_rn(__fmul_rn(dw, __shfl(dxv, 4 * q + i)), (float)bs[i]);
+            for (int sub = 0; sub < 8; ++sub) {
+                const long B = iq3s_quarter_operand(F, tabs, sub, q);
+                const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(valid ? R.X[j][sub] : 0, B, z, 0, 0, 0);
+                const int ls = 2 * (int)((F.sc >> (4 * sub)) & 15u) + 1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bs[i] += __mul24(ls, d[i]);
+                if (PIN && sub == 3)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(bs[i]));
+            }
+            const float dw = h2f(F.d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[j][i] = __fmul_rn(__fmul_rn(dw, dx_of(i)), (float)bs[i]);
+        } else if constexpr (QT == QT_Q4_K) {
+            Q4kQuarter F;
+            q4k_quarter_fields(unit, q, F);
+            int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(valid ? R.X[j][it] : 0, q4k_quarter_operand(F, it),
+                                                                       z, 0, 0, 0);
+                int sc, mn;
+                q4k_quarter_scale_min(F, it, sc, mn);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) isum[i] += __mul24(sc, d[i]);
+            }
+            // msum: pairs' item sums (k = the lane's item q, q + 4) x the row's mins
+            int sc0, mn0, sc1, mn1;
+            q4k_quarter_scale_min(F, q, sc0, mn0);
+            q4k_quarter_scale_min(F, q + 4, sc1, mn1);
+            v4f32 ms = {0.0f, 0.0f, 0.0f, 0.0f};
+            ms = __builtin_amdgcn_mfma_f32_16x16x4f32(valid ? R.bsv[j][0] : 0.0f, (float)mn0, ms, 0, 0, 0);
+            ms = __builtin_amdgcn_mfma_f32_16x16x4f32(valid ? R.bsv[j][1] : 0.0f, (float)mn1, ms, 0, 0, 0);
+            const float dw = h2f(F.dd), dmin = h2f(F.dd >> 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float dxi = dx_of(i);
+                c[j][i] = __fsub_rn(__fmul_rn(__fmul_rn(dw, dxi), (float)isum[i]), __fmul_rn(__fmul_rn(dmin, dxi), ms[i]));
+            }
+        } else {
+            static_assert(QT == QT_Q6_K, "grouped formats: IQ3_S, Q4_K, Q6_K");
+            Q6kQuarter F;
+            q6k_quarter_fields(unit, F);
+            const long lo_half = q < 2 ? -1L : 0L;         // the lane's k-values are in the item's first half
+            int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                Q6kHalf H;
+                q6k_half_fields(unit, h, q, H);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int it = 4 * h + t;
+                    const long B = q6k_half_operand(H, t);
+                    const long X = valid ? R.X[j][it] : 0;
+                    const v4i32 da = __builtin_amdgcn_mfma_i32_16x16x32_i8(X & lo_half, B, z, 0, 0, 0);
+                    const v4i32 db = __builtin_amdgcn_mfma_i32_16x16x32_i8(X & ~lo_half, B, z, 0, 0, 0);
+                    const int sa = q6k_quarter_scale(F, 2 * it), sb = q6k_quarter_scale(F, 2 * it + 1);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) isum[i] += __mul24(sa, da[i]) + __mul24(sb, db[i]);
+                }
+                // the half's sums are formed here, so only its MFMA results are live at a time
+                // (otherwise the sums are reassociated past the block's 16 MFMAs, whose
+                // results then spill)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(isum[i]));
+            }
+            // sum_h sc_h bs_h: pairs' 16-element sums (h = q + 4t) x the row's scales
+            v4f32 tb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                tb = __builtin_amdgcn_mfma_f32_16x16x4f32(valid ? R.bsv[j][t] : 0.0f, (float)q6k_quarter_scale(F, q + 4 * t),
+                                                         tb, 0, 0, 0);
+            const float dw = h2f(F.d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[j][i] = __fmul_rn(__fmul_rn(dw, dx_of(i)), (float)(isum[i] - 32 * (int)tb[i]));
+        }
     }
 }
+
+// Staging of a grouped workgroup's weights: n_reg regions (matrices) of
+// `bytes` contiguous bytes each, loaded as aligned 16-byte chunks by the NT
+// threads (NL loads each; loads past the last chunk repeat it) and stored in
+// LDS at reg * cap + chunk offset; the region's first byte lands at
+// lead[reg] (its address mod 16).  A repeat stores the same bytes to the same
+// place, so every store is unconditional (a store under a condition lets the
+// compiler sink its load past the table set-up, a whole memory latency late).
+template <int NL>
+struct GroupStage {
+    u32x4 d[NL];
+    int off[NL];                  // LDS offset of each load
+};
+template <int NT, int NL, int NREG>
+__device__ inline void group_stage_issue(GroupStage<NL>& G, const uint8_t* const (&src)[NREG], int bytes, int cap,
+                                         int* leads) {
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    int nch[NREG];
+    const uint8_t* base[NREG];
+#pragma unroll
+    for (int m = 0; m < NREG; ++m) {
+        const int lead = (int)(reinterpret_cast<uintptr_t>(src[m]) & 15);
+        base[m] = src[m] - lead;
+        nch[m] = (lead + bytes + 15) >> 4;
+        if (threadIdx.x == 0) leads[m] = lead;
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        int c = (int)threadIdx.x + NT * i, m = 0;
+#pragma unroll
+        for (int mm = 0; mm + 1 < NREG; ++mm)
+            if (m == mm && c >= nch[mm]) {
+                c -= nch[mm];
+                m = mm + 1;
+            }
+        const int cc = min(c, nch[m] - 1);
+        G.d[i] = *(g_u32x4*)(base[m] + 16 * cc);
+        G.off[i] = m * cap + 16 * cc;
+    }
+}
+template <int NL>
+__device__ inline void group_stage_store(const GroupStage<NL>& G, uint8_t* stage) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) *reinterpret_cast<u32x4*>(stage + G.off[i]) = G.d[i];
+}
+// staging bytes of one region of rows rows x rb bytes, room for its lead
+__host__ __device__ constexpr int group_cap(int rows, int rb) { return (rows * rb + 31) & ~15; }
 
 // ---------------------------------------------------------------------------
 // Grouped gate/up + SwiGLU.  grid = (d_ff / 16, n_experts), 512 threads.
@@ -267,8 +478,12 @@ __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int
 constexpr int kGuThreads = 512;
 constexpr int kGuWaveBlocks = 2;              // 256-blocks of k per wave (four waves per matrix)
 constexpr int kGuMaxBlocks = 4 * kGuWaveBlocks;
-// weight staging: both matrices' 16 rows at k <= 2048, each at any lead
-constexpr int kGuStageBytes = 2 * 16 * (kGuRows * kGuMaxBlocks * 110 / 16 + 2);
+// one workgroup's gate and up rows at k <= 2048, and the 16-byte loads per thread that stage them
+template <int QT>
+struct GuStage {
+    static constexpr int CAP = group_cap(kGuRows, kGuMaxBlocks * UnitFmt<QT>::BYTES);
+    static constexpr int LOADS = (2 * (CAP / 16) + kGuThreads - 1) / kGuThreads;
+};
 
 struct GroupedGateUpArgs {
     const uint8_t *gate, *up;     // bank bases [n_experts][d_ff][row bytes]
@@ -291,15 +506,15 @@ __device__ inline float* pair_dst(float* dst, size_t nb1, size_t nb2, int n_ids,
                                     (size_t)(p % n_ids) * nb1);
 }
 
-template <bool MMID = false>
+template <int QT, bool MMID = false>
 __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUpArgs a) {
-    constexpr int QT = QT_IQ3_S, NT = kGuThreads;
+    constexpr int NT = kGuThreads;
     const int e = blockIdx.y;
     const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
     if (n_e == 0) return;                                  // uniform: the whole workgroup leaves
-    __shared__ __align__(16) uint8_t tabs[kLdsTables];
+    __shared__ __align__(16) uint8_t tabs[QT == QT_IQ3_S ? kLdsTables : 16];
     __shared__ int leads[2];
-    __shared__ __align__(16) uint8_t stage_mem[16 + kGuStageBytes + 16];   // guards: the decoder reads past a unit's ends
+    __shared__ __align__(16) uint8_t stage_mem[16 + 2 * GuStage<QT>::CAP + 16];   // guards: reads past a unit's ends
     __shared__ __align__(16) float part[2][kGuMaxBlocks][kGuRows][kPairTile];
     uint8_t* const stage = stage_mem + 16;
     const int row0 = blockIdx.x * (MMID ? 2 * kGuRows : kGuRows);
@@ -310,29 +525,30 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
     const int b0 = min(nb, (wave & 3) * bpw), b1 = min(nb, b0 + bpw);
     const int xb0 = min(b0, nb - 1), xb1 = max(b1, xb0 + 1);      // the blocks this wave's X covers (valid ones)
     const ActLayout XL(a.d_model, QT_Q8_K);
-    GridRegs<NT> gr = load_grid_regs<NT>((int)threadIdx.x);
     const uint8_t* wg = a.gate + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     const uint8_t* wu = MMID ? wg + (size_t)kGuRows * rb : a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
-    auto tile_ptr = [&](int mm) { return mm ? wu : wg; };
-    TileRun<QT, NT> S{TileWalk<QT, NT>(2, kGuRows, rb, a.d_model)};
-    tiles_begin(S, tile_ptr);
+    GridRegs<NT> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
+    GroupStage<GuStage<QT>::LOADS> G;
+    const uint8_t* const src[2] = {wg, wu};
+    group_stage_issue<NT, GuStage<QT>::LOADS, 2>(G, src, kGuRows * (int)rb, GuStage<QT>::CAP, leads);
     auto pair_x = [&](int pt, XRegs<kGuWaveBlocks>& R) {
         const int cnt = min(kPairTile, n_e - pt);
         const uint8_t* xrow = a.xq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.xq_stride;
-        load_x(R, xrow, reinterpret_cast<const float*>(xrow + XL.off_d), xb0, xb1, q);
+        load_x<QT>(R, xrow, XL, xb0, xb1, q);
     };
     XRegs<kGuWaveBlocks> XR;
     pair_x(0, XR);                                          // with the weights
-    store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
-    pass_store(S, stage, leads);
-    __syncthreads();                                        // staged rows and table written
-    const uint8_t* rowp = stage + 16 * S.cpt * m + leads[m] + (size_t)r * rb;
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
+    group_stage_store(G, stage);
+    __syncthreads();                                        // staged rows, leads and table written
+    const uint8_t* rowp = stage + GuStage<QT>::CAP * m + leads[m] + (size_t)r * rb;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
         if (pt) pair_x(pt, XR);
         float c[kGuWaveBlocks][4];
-        mfma_blocks<kGuWaveBlocks>(rowp, tabs, b0, b1, XR, valid, q, c);
+        mfma_blocks<QT, kGuWaveBlocks, true>(rowp, tabs, b0, b1, XR, valid, q, c);
 #pragma unroll
         for (int jj = 0; jj < kGuWaveBlocks; ++jj)
             if (b0 + jj < b1)
@@ -363,6 +579,12 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
 // Grouped down.  grid = (d_model / 64, n_experts), 256 threads; wave w owns
 // rows 16 w .. 16 w + 15 of the workgroup's 64, over the whole of k.
 // ---------------------------------------------------------------------------
+template <int QT>
+struct DownStage {
+    static constexpr int CAP = group_cap(kDownRows, kDownBlocks * UnitFmt<QT>::BYTES);
+    static constexpr int LOADS = (CAP / 16 + kThreads - 1) / kThreads;
+};
+
 struct GroupedDownArgs {
     const uint8_t* down;          // bank base [n_experts][d_model][row bytes]
     size_t expert_stride;
@@ -378,33 +600,34 @@ struct GroupedDownArgs {
     size_t dst_nb1, dst_nb2;
 };
 
-template <bool MMID = false>
-__global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
-    constexpr int QT = QT_IQ3_S;
+template <int QT, bool MMID = false>
+__global__ __launch_bounds__(kThreads, 2) void k_grouped_down(GroupedDownArgs a) {
     const int e = blockIdx.y;
     const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
     if (n_e == 0) return;
-    SABAH_STATIC_LDS(QT)
+    __shared__ __align__(16) uint8_t tabs[QT == QT_IQ3_S ? kLdsTables : 16];
+    __shared__ int leads[1];
+    __shared__ __align__(16) uint8_t stage_mem[16 + DownStage<QT>::CAP + 16];
+    uint8_t* const stage = stage_mem + 16;
     const int row0 = blockIdx.x * kDownRows;
     const int nb = a.d_ff / 256;
     const size_t rb = row_bytes(QT, a.d_ff);
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
     const int r = lane & 15, q = lane >> 4, rbase = 16 * wave, j = lane & 15;
     const ActLayout HL(a.d_ff, QT_Q8_K);
-    GridRegs<kThreads> gr = load_grid_regs<kThreads>((int)threadIdx.x);
-    const uint8_t* wd = a.down + (size_t)e * a.expert_stride + (size_t)row0 * rb;
-    auto tile_ptr = [&](int) { return wd; };
-    TileRun<QT> S{TileWalk<QT>(1, kDownRows, rb, a.d_ff)};
-    tiles_begin(S, tile_ptr);
+    GridRegs<kThreads> gr;
+    if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
+    GroupStage<DownStage<QT>::LOADS> G;
+    const uint8_t* const src[1] = {a.down + (size_t)e * a.expert_stride + (size_t)row0 * rb};
+    group_stage_issue<kThreads, DownStage<QT>::LOADS, 1>(G, src, kDownRows * (int)rb, DownStage<QT>::CAP, leads);
     auto pair_x = [&](int pt, XRegs<kDownBlocks>& R) {
         const int cnt = min(kPairTile, n_e - pt);
-        const int pos = g0 + pt + min(j, cnt - 1);
-        const uint8_t* hrow = a.hq + (size_t)pos * a.hq_stride;
-        load_x(R, hrow, reinterpret_cast<const float*>(hrow + HL.off_d), 0, nb, q);
+        const uint8_t* hrow = a.hq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.hq_stride;
+        load_x<QT>(R, hrow, HL, 0, nb, q);
     };
-    store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
-    tiles_stage(S, stage, leads);
-    __syncthreads();                                        // staged rows and table written
+    if constexpr (QT == QT_IQ3_S) store_iq3s_tables<kThreads>(tabs, gr, (int)threadIdx.x);
+    group_stage_store(G, stage);
+    __syncthreads();                                        // staged rows, lead and table written
     const uint8_t* rowp = stage + leads[0] + (size_t)(rbase + r) * rb;
     XRegs<kDownBlocks> XR;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
@@ -412,7 +635,7 @@ __global__ __launch_bounds__(kThreads) void k_grouped_down(GroupedDownArgs a) {
         const bool valid = j < cnt;
         pair_x(pt, XR);
         float c[kDownBlocks][4];
-        mfma_blocks<kDownBlocks>(rowp, tabs, 0, nb, XR, valid, q, c);
+        mfma_blocks<QT, kDownBlocks>(rowp, tabs, 0, nb, XR, valid, q, c);
         // the lane's row for pairs 4q .. 4q + 3
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

@@ -726,18 +726,24 @@ SABAH_API int sabah_rt_unregister_bank(const void* source_key) {
 // MUL_MAT_ID
 // ===========================================================================
 // ---------------------------------------------------------------------------
-// Grouped MUL_MAT_ID (IQ3_S, many tokens): the (token, slot) pairs are grouped
+// Grouped MUL_MAT_ID (IQ3_S, Q4_K, Q6_K, many tokens): the (token, slot) pairs are grouped
 // by expert on the device and each expert's rows are read once per call, with
 // int8 MFMA over up to 16 pairs at a time.  The integer block sums and every
 // fp32 step are the token-major kernel's, so the results are bit-identical to
 // it; the choice between the two paths changes no value.
 //   mode 0 (default): grouped when eligible and the call has at least
-//     kGroupedMinPairs[form] pairs per expert on average;
+//     grouped_min_pairs(form, qt) pairs per expert on average;
 //   mode 1: never; mode 2: whenever eligible.
 // ---------------------------------------------------------------------------
-// measured on IQ3_S top-10 of 512: the down-shaped form (k <= 1024) wins from
-// 64 tokens (1.25 pairs per expert), the gate/up-shaped form from 128 (2.5)
-constexpr int kGroupedMinPairs[3] = {0, 1, 2};
+// measured at top-10 of 512 (2048 -> 768 and 768 -> 2048): the down-shaped
+// form (k <= 1024) wins from 64 tokens (1.25 pairs per expert) for IQ3_S and
+// Q6_K and from 128 (2.5) for Q4_K; the gate/up-shaped form from 128 tokens
+// for IQ3_S and Q4_K and from 64 for Q6_K
+static int grouped_min_pairs(int form, int qt) {
+    if (qt == QT_Q4_K) return 2;
+    if (qt == QT_Q6_K) return 1;
+    return form == 1 ? 1 : 2;
+}
 std::atomic<int> g_mmid_grouping{0};
 
 SABAH_API int sabah_rt_set_mmid_grouping(int mode) {
@@ -746,20 +752,41 @@ SABAH_API int sabah_rt_set_mmid_grouping(int mode) {
     return 0;
 }
 
+// the grouped kernels for the weight type qt (one of grouped_type_ok's)
+static bool grouped_type_ok(int qt) { return qt == QT_IQ3_S || qt == QT_Q4_K || qt == QT_Q6_K; }
+
+template <bool MMID>
+static void launch_grouped_gate_up(int qt, int kind, dim3 grid, hipStream_t st, const GroupedGateUpArgs& a) {
+    switch (qt) {
+    case QT_Q4_K: launch_kernel(kind, k_grouped_gate_up<QT_Q4_K, MMID>, grid, dim3(kGuThreads), 0, st, a); break;
+    case QT_Q6_K: launch_kernel(kind, k_grouped_gate_up<QT_Q6_K, MMID>, grid, dim3(kGuThreads), 0, st, a); break;
+    default: launch_kernel(kind, k_grouped_gate_up<QT_IQ3_S, MMID>, grid, dim3(kGuThreads), 0, st, a); break;
+    }
+}
+
+template <bool MMID>
+static void launch_grouped_down(int qt, int kind, dim3 grid, hipStream_t st, const GroupedDownArgs& a) {
+    switch (qt) {
+    case QT_Q4_K: launch_kernel(kind, k_grouped_down<QT_Q4_K, MMID>, grid, dim3(kThreads), 0, st, a); break;
+    case QT_Q6_K: launch_kernel(kind, k_grouped_down<QT_Q6_K, MMID>, grid, dim3(kThreads), 0, st, a); break;
+    default: launch_kernel(kind, k_grouped_down<QT_IQ3_S, MMID>, grid, dim3(kThreads), 0, st, a); break;
+    }
+}
+
 // 0: not eligible; 1: down-shaped kernel (64-row tiles, k <= 1024); 2: gate/up-shaped (32-row tiles)
 static int grouped_mmid_form(int qt, bool packed, size_t ids_id_stride, size_t ids_token_stride, size_t x_id_stride,
                              size_t x_token_stride, int x_rows, int n_ids, int n_tokens, int rows, int k,
                              int n_experts) {
-    if (qt != QT_IQ3_S || !packed || n_experts > 4096) return 0;
+    if (!grouped_type_ok(qt) || !packed || n_experts > 4096) return 0;
     if (ids_id_stride != 4 || ids_token_stride != 4 * (size_t)n_ids) return 0;
     if (x_id_stride != 4 * (size_t)k || x_token_stride != 4 * (size_t)k * x_rows) return 0;
     if ((size_t)n_tokens * n_ids > (size_t)1 << 24) return 0;
     if (k % 256 == 0 && k / 256 <= kDownBlocks && rows % kDownRows == 0) return 1;
-    if (k % 512 == 0 && k / 256 <= 2 * kGuBlocksPerWave && rows % (2 * kGuRows) == 0) return 2;
+    if (k % 512 == 0 && k / 256 <= kGuMaxBlocks && rows % (2 * kGuRows) == 0) return 2;
     return 0;
 }
 
-static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, const float* d_x, int x_rows,
+static int mmid_grouped(int form, int qt, const uint8_t* bank, size_t expert_stride, const float* d_x, int x_rows,
                         const int32_t* d_ids, int n_ids, int n_tokens, float* d_dst, size_t dst_id_stride,
                         size_t dst_token_stride, int rows, int k, int n_experts, hipStream_t st) {
     const size_t P = (size_t)n_tokens * n_ids;
@@ -796,7 +823,7 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
         dn.dst = d_dst;
         dn.dst_nb1 = dst_id_stride;
         dn.dst_nb2 = dst_token_stride;
-        launch_kernel(KK_MMID, k_grouped_down<true>, dim3((unsigned)(rows / kDownRows), (unsigned)E), dim3(kThreads), 0, st, dn);
+        launch_grouped_down<true>(qt, KK_MMID, dim3((unsigned)(rows / kDownRows), (unsigned)E), st, dn);
     } else {
         GroupedGateUpArgs gu{};
         gu.gate = bank;
@@ -811,8 +838,7 @@ static int mmid_grouped(int form, const uint8_t* bank, size_t expert_stride, con
         gu.dst = d_dst;
         gu.dst_nb1 = dst_id_stride;
         gu.dst_nb2 = dst_token_stride;
-        launch_kernel(KK_MMID, k_grouped_gate_up<true>, dim3((unsigned)(rows / (2 * kGuRows)), (unsigned)E),
-                      dim3(kGuThreads), 0, st, gu);
+        launch_grouped_gate_up<true>(qt, KK_MMID, dim3((unsigned)(rows / (2 * kGuRows)), (unsigned)E), st, gu);
     }
     return ck(hipGetLastError(), "grouped MUL_MAT_ID launch") ? 0 : -1;
 }
@@ -855,8 +881,8 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
     const int form = mode == 1 ? 0
                    : grouped_mmid_form(qt, packed, ids_id_stride, ids_token_stride, x_id_stride, x_token_stride,
                                        x_rows, n_ids, n_tokens, rows, k, n_experts);
-    if (form && (mode == 2 || (long long)n_tokens * n_ids >= (long long)kGroupedMinPairs[form] * n_experts)) {
-        if (mmid_grouped(form, bank, expert_stride, static_cast<const float*>(d_x), x_rows,
+    if (form && (mode == 2 || (long long)n_tokens * n_ids >= (long long)grouped_min_pairs(form, qt) * n_experts)) {
+        if (mmid_grouped(form, qt, bank, expert_stride, static_cast<const float*>(d_x), x_rows,
                          static_cast<const int32_t*>(d_ids), n_ids, n_tokens, d_dst, dst_id_stride, dst_token_stride,
                          rows, k, n_experts, st))
             return -1;
@@ -1349,8 +1375,8 @@ SABAH_API int sabah_moe_chain(const sabah_moe_layer_desc* layers, int n_layers, 
 // ===========================================================================
 static bool grouped_shape_ok(const sabah_moe_layer_desc* L) {
     const int D = L->d_model, F = L->d_ff;
-    return L->qt_gate == QT_IQ3_S && L->qt_up == QT_IQ3_S && L->qt_down == QT_IQ3_S && D % 512 == 0 &&
-           D / 256 <= 2 * kGuBlocksPerWave && F % 256 == 0 && F / 256 <= kDownBlocks && D % kDownRows == 0 &&
+    return grouped_type_ok(L->qt_gate) && L->qt_up == L->qt_gate && grouped_type_ok(L->qt_down) && D % 512 == 0 &&
+           D / 256 <= kGuMaxBlocks && F % 256 == 0 && F / 256 <= kDownBlocks && D % kDownRows == 0 &&
            L->n_experts <= 4096;
 }
 
@@ -1385,7 +1411,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     GroupedGateUpArgs gu{};
     gu.gate = static_cast<const uint8_t*>(L->gate);
     gu.up = static_cast<const uint8_t*>(L->up);
-    gu.expert_stride = row_bytes(QT_IQ3_S, D) * (size_t)F;
+    gu.expert_stride = row_bytes(L->qt_gate, D) * (size_t)F;
     gu.off = off;
     gu.pair_of = pair_of;
     gu.k = n_used;
@@ -1394,21 +1420,20 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     gu.h = h;
     gu.d_model = D;
     gu.d_ff = F;
-    launch_kernel(KK_GGATE_UP, k_grouped_gate_up<false>, dim3((unsigned)(F / kGuRows), (unsigned)E), dim3(kGuThreads), 0,
-                  st, gu);
+    launch_grouped_gate_up<false>(L->qt_gate, KK_GGATE_UP, dim3((unsigned)(F / kGuRows), (unsigned)E), st, gu);
     const size_t hq_rows = P * (size_t)(F / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((hq_rows + 15) / 16)), dim3(kThreads), 0, st, h, (int)P, F,
                        (int)QT_Q8_K, hq, hq_stride, (const int*)nullptr, 1, (const int*)(off + E));
     GroupedDownArgs dn{};
     dn.down = static_cast<const uint8_t*>(L->down);
-    dn.expert_stride = row_bytes(QT_IQ3_S, F) * (size_t)D;
+    dn.expert_stride = row_bytes(L->qt_down, F) * (size_t)D;
     dn.off = off;
     dn.hq = hq;
     dn.hq_stride = hq_stride;
     dn.y = y;
     dn.d_model = D;
     dn.d_ff = F;
-    launch_kernel(KK_GDOWN, k_grouped_down<false>, dim3((unsigned)(D / kDownRows), (unsigned)E), dim3(kThreads), 0, st, dn);
+    launch_grouped_down<false>(L->qt_down, KK_GDOWN, dim3((unsigned)(D / kDownRows), (unsigned)E), st, dn);
     CombineArgs cb{y, pos_of, d_w, shared, d_resid, d_out, n_used, D};
     hipLaunchKernelGGL(k_combine, dim3((unsigned)((D + kThreads - 1) / kThreads), (unsigned)n_tokens), dim3(kThreads), 0,
                        st, cb);
@@ -1421,9 +1446,10 @@ SABAH_API int sabah_moe_prefill_layer(const sabah_moe_layer_desc* layer, const f
     if (check_layer_desc(layer)) return -1;
     if (!d_x || !d_ids || !d_w || !d_out || n_used <= 0 || n_tokens < 0) return fail("invalid MoE layer arguments");
     if (!grouped_shape_ok(layer))
-        return fail("grouped MoE layer: needs IQ3_S gate/up/down, d_model a multiple of 512 up to %d, d_ff a "
-                    "multiple of 256 up to %d, n_experts <= 4096 (got types %d/%d/%d, d_model=%d d_ff=%d E=%d)",
-                    512 * kGuBlocksPerWave, 256 * kDownBlocks, layer->qt_gate, layer->qt_up, layer->qt_down,
+        return fail("grouped MoE layer: needs gate/up of one type and down each IQ3_S, Q4_K or Q6_K, d_model a "
+                    "multiple of 512 up to %d, d_ff a multiple of 256 up to %d, n_experts <= 4096 (got types "
+                    "%d/%d/%d, d_model=%d d_ff=%d E=%d)",
+                    256 * kGuMaxBlocks, 256 * kDownBlocks, layer->qt_gate, layer->qt_up, layer->qt_down,
                     layer->d_model, layer->d_ff, layer->n_experts);
     if ((size_t)n_tokens * n_used > (size_t)1 << 24) return fail("grouped MoE layer: too many (token, slot) pairs");
     if (g_device < 0) return fail("sabah_rt_init has not been called");

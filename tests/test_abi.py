@@ -112,12 +112,13 @@ def _desc(qt_gate=21, qt_up=21, qt_down=21, d_model=2048, d_ff=768, n_experts=51
     return d
 
 
-@pytest.mark.parametrize("kw", [dict(qt_gate=12, qt_up=12, qt_down=14), dict(d_model=2560), dict(d_model=4096),
+@pytest.mark.parametrize("kw", [dict(qt_gate=12, qt_up=14, qt_down=14), dict(qt_gate=8, qt_up=8, qt_down=8),
+                                dict(qt_down=8), dict(d_model=2560), dict(d_model=4096),
                                 dict(d_ff=1280), dict(n_experts=8192)])
 def test_prefill_layer_rejects_shapes_it_does_not_group_without_a_device(kw):
-    """The grouped layer takes IQ3_S, d_model a multiple of 512 up to 2048, d_ff a
-    multiple of 256 up to 1024 and n_experts <= 4096; anything else is refused
-    before the device is touched."""
+    """The grouped layer takes gate/up of one type and down, each IQ3_S, Q4_K or
+    Q6_K, d_model a multiple of 512 up to 2048, d_ff a multiple of 256 up to 1024
+    and n_experts <= 4096; anything else is refused before the device is touched."""
     from sabah.runtime import rt
     L = rt.lib()
     d = _desc(**kw)

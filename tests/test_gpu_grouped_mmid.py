@@ -1,10 +1,12 @@
-"""Grouped MUL_MAT_ID (IQ3_S over many tokens) through sabah_rt_mul_mat_id_v2.
+"""Grouped MUL_MAT_ID (IQ3_S, Q4_K, Q6_K over many tokens) through sabah_rt_mul_mat_id_v2.
 
 The grouped path groups the (token, slot) pairs by expert on the device and
 reads each expert once per call (int8 MFMA over up to 16 pairs at a time).
 Its integer block sums are exact and its fp32 steps are the token-major
-kernel's, so the bar is bit-identity with both the token-major path and the
-oracle (ggml's CPU MUL_MAT_ID).
+kernel's, so the bar is bit-identity with the token-major path; for IQ3_S
+also with the oracle (ggml's CPU MUL_MAT_ID), whose fp32 order for IQ3_S is
+the same, and for the K formats (ggml sums their blocks in another fp32
+order) the oracle within max_rel <= 1e-3, cosine >= 0.99999.
 """
 from __future__ import annotations
 
@@ -18,7 +20,7 @@ from helpers import assert_parity
 
 pytestmark = pytest.mark.gpu
 
-IQ3_S = 21
+Q4_K, Q6_K, IQ3_S = 12, 14, 21
 DEV = torch.device("cuda:0")
 AUTO, NEVER, ALWAYS = 0, 1, 2
 
@@ -42,12 +44,12 @@ def grouping(hip_rt):
     set_mode(AUTO)
 
 
-def v2(hip_rt, bank, rb, rows, k, E, x, ids, out):
+def v2(hip_rt, bank, rb, rows, k, E, x, ids, out, qt=IQ3_S):
     return hip_rt.lib().sabah_rt_mul_mat_id_v2(
         vp(bank), ctypes.c_size_t(rows * rb), ctypes.c_size_t(rb),
         vp(x), ctypes.c_size_t(x.stride(1) * 4), x.shape[1], ctypes.c_size_t(x.stride(0) * 4),
         vp(ids), ctypes.c_size_t(4), ctypes.c_size_t(ids.stride(0) * 4), ids.shape[1], ids.shape[0],
-        vp(out), ctypes.c_size_t(out.stride(1) * 4), ctypes.c_size_t(out.stride(0) * 4), rows, k, E, IQ3_S,
+        vp(out), ctypes.c_size_t(out.stride(1) * 4), ctypes.c_size_t(out.stride(0) * 4), rows, k, E, qt,
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), None)
 
 
@@ -55,23 +57,23 @@ def grouped_calls(hip_rt):
     return hip_rt.snapshot()["grouped_calls"]
 
 
-def run(hip_rt, bank, rb, rows, k, E, x, ids, grouped=None):
+def run(hip_rt, bank, rb, rows, k, E, x, ids, grouped=None, qt=IQ3_S):
     """One v2 call; `grouped` (if given) is whether it must take the grouped path."""
     out = torch.full((ids.shape[0], ids.shape[1], rows), float("nan"), dtype=torch.float32, device=DEV)
     before = grouped_calls(hip_rt)
-    hip_rt.check(v2(hip_rt, bank, rb, rows, k, E, x, ids, out), "v2")
+    hip_rt.check(v2(hip_rt, bank, rb, rows, k, E, x, ids, out, qt), "v2")
     torch.cuda.synchronize()
     if grouped is not None:
         assert grouped_calls(hip_rt) == before + int(grouped)
     return out.cpu().numpy()
 
 
-def case(orc, seed, E, rows, k, Tn, K, x_rows):
+def case(orc, seed, E, rows, k, Tn, K, x_rows, qt=IQ3_S):
     """E experts (the last one never selected), Tn tokens x K distinct ids, a
     duplicate id in token 3; about Tn * K / (E - 1) pairs per expert, so most
     experts take several 16-pair tiles."""
     rng = np.random.default_rng(seed)
-    raw = orc.quantize_weights(IQ3_S, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
     ids = np.stack([rng.choice(E - 1, K, replace=False) for _ in range(Tn)]).astype(np.int32)
     ids[3, K - 1] = ids[3, 0]
     x = rng.standard_normal((Tn, x_rows, k)).astype(np.float32)
@@ -85,18 +87,20 @@ SHAPES = [(768, 2048), (1024, 128), (256, 64), (2048, 768), (1536, 64)]
 
 @pytest.mark.parametrize("k,rows", SHAPES)
 @pytest.mark.parametrize("x_rows_is_n_ids", [False, True])
-def test_grouped_mul_mat_id_is_bit_identical(hip_rt, orc, grouping, k, rows, x_rows_is_n_ids):
+@pytest.mark.parametrize("qt", [IQ3_S, Q4_K, Q6_K])
+def test_grouped_mul_mat_id_is_bit_identical(hip_rt, orc, grouping, qt, k, rows, x_rows_is_n_ids):
     E, Tn, K = 12, 40, 6
-    raw, ids, x = case(orc, k + rows + x_rows_is_n_ids, E, rows, k, Tn, K, K if x_rows_is_n_ids else 1)
+    raw, ids, x = case(orc, k + rows + x_rows_is_n_ids + qt, E, rows, k, Tn, K, K if x_rows_is_n_ids else 1, qt)
     bank, rb = T(raw), raw.shape[-1]
     xd, idd = T(x), T(ids)
     grouping(ALWAYS)
-    got = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=True)
+    got = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=True, qt=qt)
     grouping(NEVER)
-    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=False)
-    want = orc.mul_mat_id(raw, x, ids, rows, k, IQ3_S)
-    assert_parity(got, want, "grouped k=%d rows=%d" % (k, rows))
-    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=False, qt=qt)
+    want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    assert_parity(got, want, "grouped qt=%d k=%d rows=%d" % (qt, k, rows))
+    if qt == IQ3_S:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
     if not x_rows_is_n_ids:
         assert np.array_equal(got[3, K - 1], got[3, 0])
