@@ -253,9 +253,10 @@ int sabah_moe_chain(const sabah_moe_layer_desc *layers, int n_layers, float *d_x
  * are read once and applied to all of its pairs with int8 MFMA.  No
  * reference counterpart: the reference's kernel re-reads an expert per
  * (token, slot) (sabah_rt.cu:2791-2839); the grouping follows upstream
- * ggml's sorted MUL_MAT_ID fallback (ggml-cuda.cu:1985-2082).  Needs IQ3_S
- * gate/up/down, d_model a multiple of 512 up to 2048, d_ff a multiple of 256
- * up to 1024, n_experts <= 4096; returns -1 otherwise.  An out-of-range id
+ * ggml's sorted MUL_MAT_ID fallback (ggml-cuda.cu:1985-2082).  Needs gate and
+ * up of one type and down of any, each IQ3_S, Q4_K or Q6_K, d_model a multiple
+ * of 512 up to 2048, d_ff a multiple of 256 up to 1024, n_experts <= 4096;
+ * returns -1 otherwise.  An out-of-range id
  * makes its token's output NaN and fails the next call, as in sabah_moe_layer. */
 int sabah_moe_prefill_layer(const sabah_moe_layer_desc *layer, const float *d_x, const int32_t *d_ids,
                             const float *d_w, int n_used, int n_tokens, float *d_out, const float *d_resid,
@@ -275,14 +276,15 @@ int sabah_moe_prefill_layer(const sabah_moe_layer_desc *layer, const float *d_x,
 int sabah_moe_route(const float *d_logits, int n_tokens, int n_experts, int n_used, int norm_w,
                     float w_scale, int32_t *d_ids, float *d_w, void *stream);
 
-/* How sabah_rt_mul_mat_id_v2 runs IQ3_S calls over many tokens.  No reference
+/* How sabah_rt_mul_mat_id_v2 runs IQ3_S, Q4_K and Q6_K calls over many tokens.  No reference
  * counterpart: the reference's kernel re-reads an expert per (token, slot)
  * (sabah_rt.cu:2791-2839).  Grouped, the (token, slot) pairs are grouped by
  * expert on the device and each expert is read once per call (int8 MFMA);
  * eligible calls have packed rows, dense ids and x, n_experts <= 4096, and
  * k <= 1024 with rows % 64 == 0, or k % 512 == 0, k <= 2048, rows % 32 == 0.
- * mode 0 (default): grouped when eligible with at least 1 (k <= 1024) or 2
- * (larger k) pairs per expert on average; 1: never; 2: whenever eligible.
+ * mode 0 (default): grouped when eligible with at least 1 (IQ3_S with
+ * k <= 1024, and Q6_K) or 2 (otherwise) pairs per expert on average; 1: never;
+ * 2: whenever eligible.
  * The results are bit-identical either way.  Grouped calls use library
  * scratch (pair lists, q8 rows) shared by every stream: calls that may
  * overlap on different streams need mode 1 (the token-major kernel uses no
