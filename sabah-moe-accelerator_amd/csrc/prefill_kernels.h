@@ -164,11 +164,13 @@ __global__ __launch_bounds__(kThreads) void k_quant_rows(const float* __restrict
 // eight sub-blocks s: the qs bytes 8s + 2q, 8s + 2q + 1 (grid groups 2q and
 // 2q + 1), their ninth index bits (bits 2q, 2q + 1 of qh[s]) and sign
 // nibbles (byte 4s + q of the signs); and the unit's sub-block scales and d.
-// Read once per block (the unit starts at an even byte).
+// Read once per block (the unit starts at an even byte).  A group's table
+// index is the 16-bit value [qs, h] with h = sign nibble | ninth bit << 4
+// (the codebook table's layout), so the fields are packed as the bytes one
+// v_perm turns into both indices of a sub-block.
 struct Iq3sQuarter {
-    uint32_t qs[4];               // halfword s of qs[s >> 1]: the lane's two qs bytes of sub-block s
-    uint32_t qh[2];               // qh bytes 0..7
-    uint32_t sg[2];               // byte s of sg[s >> 2]: the lane's sign byte of sub-block s
+    uint32_t qs[4];               // halfword s & 1 of qs[s >> 1]: [qs_2q, qs_2q+1] of sub-block s
+    uint32_t lh[4];               // halfword s & 1 of lh[s >> 1]: [h_2q, h_2q+1] of sub-block s
     uint32_t sc;                  // the four scale bytes (nibble s: sub-block s)
     uint32_t d;                   // fp16 d (low half)
 };
@@ -177,22 +179,32 @@ __device__ inline void iq3s_quarter_fields(const uint8_t* unit, int q, Iq3sQuart
 #pragma unroll
     for (int p = 0; p < 4; ++p)
         F.qs[p] = (uint32_t)h[1 + 8 * p + q] | (uint32_t)h[5 + 8 * p + q] << 16;   // bytes 2 + 8s + 2q, s = 2p, 2p + 1
-    F.qh[0] = (uint32_t)h[33] | (uint32_t)h[34] << 16;
-    F.qh[1] = (uint32_t)h[35] | (uint32_t)h[36] << 16;
+    const uint32_t qh[2] = {(uint32_t)h[33] | (uint32_t)h[34] << 16, (uint32_t)h[35] | (uint32_t)h[36] << 16};
     const uint8_t* sg = unit + 74 + q;
-    F.sg[0] = (uint32_t)sg[0] | (uint32_t)sg[4] << 8 | (uint32_t)sg[8] << 16 | (uint32_t)sg[12] << 24;
-    F.sg[1] = (uint32_t)sg[16] | (uint32_t)sg[20] << 8 | (uint32_t)sg[24] << 16 | (uint32_t)sg[28] << 24;
+    const uint32_t sw[2] = {(uint32_t)sg[0] | (uint32_t)sg[4] << 8 | (uint32_t)sg[8] << 16 | (uint32_t)sg[12] << 24,
+                            (uint32_t)sg[16] | (uint32_t)sg[20] << 8 | (uint32_t)sg[24] << 16 | (uint32_t)sg[28] << 24};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        // byte j (sub-block 4k + j): h of group 2q in lo, of group 2q + 1 in hi
+        const uint32_t b0 = ((qh[k] >> (2 * q)) << 4) & 0x10101010u;
+        const uint32_t b1 = ((qh[k] >> (2 * q + 1)) << 4) & 0x10101010u;
+        const uint32_t lo = (sw[k] & 0x0F0F0F0Fu) | b0;
+        const uint32_t hi = ((sw[k] >> 4) & 0x0F0F0F0Fu) | b1;
+        F.lh[2 * k] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);       // [lo.b0, hi.b0, lo.b1, hi.b1]
+        F.lh[2 * k + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);   // [lo.b2, hi.b2, lo.b3, hi.b3]
+    }
     F.sc = (uint32_t)h[53] | (uint32_t)h[54] << 16;
     F.d = h[0];
 }
 // the lane's eight weights of sub-block s (B operand) from the signed codebook table
 __device__ inline long iq3s_quarter_operand(const Iq3sQuarter& F, const uint8_t* tabs, int s, int q) {
-    const uint32_t qs2 = (F.qs[s >> 1] >> (16 * (s & 1))) & 0xFFFFu;
-    const uint32_t qh2 = (F.qh[s >> 2] >> (8 * (s & 3) + 2 * q)) & 3u;
-    const uint32_t sgb = (F.sg[s >> 2] >> (8 * (s & 3))) & 0xFFu;
-    const uint32_t i0 = (qs2 & 0xFFu) + 256u * ((sgb & 15u) + 16u * (qh2 & 1u));
-    const uint32_t i1 = (qs2 >> 8) + 256u * ((sgb >> 4) + 16u * (qh2 >> 1));
-    const uint32_t g0 = lds_u32(tabs, kLdsGrid + 4u * i0), g1 = lds_u32(tabs, kLdsGrid + 4u * i1);
+    (void)q;
+    const uint32_t p = 2u * (uint32_t)(s & 1);
+    // [qs_2q, h_2q, qs_2q+1, h_2q+1]: the two 16-bit table indices
+    const uint32_t sel = (4u + p) | (p << 8) | ((5u + p) << 16) | ((p + 1u) << 24);
+    const uint32_t W = __builtin_amdgcn_perm(F.qs[s >> 1], F.lh[s >> 1], sel);
+    const uint32_t g0 = lds_u32(tabs, kLdsGrid + ((W & 0xFFFFu) << 2));
+    const uint32_t g1 = lds_u32(tabs, kLdsGrid + (W >> 14));      // h < 32: bits 14, 15 of W are 0
     return (long)(((uint64_t)g1 << 32) | g0);
 }
 
