@@ -479,17 +479,18 @@ __host__ __device__ constexpr int group_cap(int rows, int rb) { return (rows * r
 
 // ---------------------------------------------------------------------------
 // Grouped gate/up + SwiGLU.  grid = (d_ff / 16, n_experts), 512 threads.
-// Wave w: matrix w >> 2 (gate, up), blocks [b0, b1) of k for quarter w & 3.
-// Each wave runs its 16 rows x blocks against every 16-pair tile of the
-// expert, decoding the staged rows into MFMA operands as it goes; the
-// quarters' block results meet in LDS and are summed in block order before
-// SwiGLU.  The activation rows are the pairs' rows in group order (k_quant_rows
+// Above four 256-blocks of k, wave w takes block w of both matrices, so a
+// pair tile's activations for a block are loaded by one wave, once (the
+// loads of 16 rows x 8 bytes each are what a workgroup's start waits on);
+// up to four blocks, wave w takes block w & 3 of matrix w >> 2.  Each wave
+// runs its rows against every 16-pair tile of the expert, decoding the
+// staged rows into MFMA operands as it goes; the block results meet in LDS
+// and are summed in block order before SwiGLU.  The activation rows are the pairs' rows in group order (k_quant_rows
 // with the grouping as its gather), so a pair tile's activations load from
 // the group offset alone, at the start.
 // ---------------------------------------------------------------------------
 constexpr int kGuThreads = 512;
-constexpr int kGuWaveBlocks = 2;              // 256-blocks of k per wave (four waves per matrix)
-constexpr int kGuMaxBlocks = 4 * kGuWaveBlocks;
+constexpr int kGuMaxBlocks = 8;               // 256-blocks of k: one per wave
 // one workgroup's gate and up rows at k <= 2048, and the 16-byte loads per thread that stage them
 template <int QT>
 struct GuStage {
@@ -530,12 +531,13 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
     __shared__ __align__(16) float part[2][kGuMaxBlocks][kGuRows][kPairTile];
     uint8_t* const stage = stage_mem + 16;
     const int row0 = blockIdx.x * (MMID ? 2 * kGuRows : kGuRows);
-    const int nb = a.d_model / 256, bpw = (nb + 3) / 4;
+    const int nb = a.d_model / 256;
     const size_t rb = row_bytes(QT, a.d_model);
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
-    const int m = wave >> 2, r = lane & 15, q = lane >> 4, j = lane & 15;
-    const int b0 = min(nb, (wave & 3) * bpw), b1 = min(nb, b0 + bpw);
-    const int xb0 = min(b0, nb - 1), xb1 = max(b1, xb0 + 1);      // the blocks this wave's X covers (valid ones)
+    const bool both = nb > 4;                              // the wave's block of both matrices
+    const int m = both ? 0 : wave >> 2, b = both ? wave : wave & 3;
+    const int r = lane & 15, q = lane >> 4, j = lane & 15;
+    const int xb = min(b, nb - 1);                         // the block this wave's X covers (a valid one)
     const ActLayout XL(a.d_model, QT_Q8_K);
     const uint8_t* wg = a.gate + (size_t)e * a.expert_stride + (size_t)row0 * rb;
     const uint8_t* wu = MMID ? wg + (size_t)kGuRows * rb : a.up + (size_t)e * a.expert_stride + (size_t)row0 * rb;
@@ -544,28 +546,33 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
     GroupStage<GuStage<QT>::LOADS> G;
     const uint8_t* const src[2] = {wg, wu};
     group_stage_issue<NT, GuStage<QT>::LOADS, 2>(G, src, kGuRows * (int)rb, GuStage<QT>::CAP, leads);
-    auto pair_x = [&](int pt, XRegs<kGuWaveBlocks>& R) {
+    auto pair_x = [&](int pt, XRegs<1>& R) {
         const int cnt = min(kPairTile, n_e - pt);
         const uint8_t* xrow = a.xq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.xq_stride;
-        load_x<QT>(R, xrow, XL, xb0, xb1, q);
+        load_x<QT>(R, xrow, XL, xb, xb + 1, q);
     };
-    XRegs<kGuWaveBlocks> XR;
+    XRegs<1> XR;
     pair_x(0, XR);                                          // with the weights
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
     group_stage_store(G, stage);
     __syncthreads();                                        // staged rows, leads and table written
     const uint8_t* rowp = stage + GuStage<QT>::CAP * m + leads[m] + (size_t)r * rb;
+    const uint8_t* rowp1 = stage + GuStage<QT>::CAP + leads[1] + (size_t)r * rb;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
         if (pt) pair_x(pt, XR);
-        float c[kGuWaveBlocks][4];
-        mfma_blocks<QT, kGuWaveBlocks, true>(rowp, tabs, b0, b1, XR, valid, q, c);
+        if (b < nb) {
+            float c[1][4];
+            mfma_blocks<QT, 1, true>(rowp, tabs, b, b + 1, XR, valid, q, c);
 #pragma unroll
-        for (int jj = 0; jj < kGuWaveBlocks; ++jj)
-            if (b0 + jj < b1)
+            for (int i = 0; i < 4; ++i) part[m][b][r][4 * q + i] = c[0][i];
+            if (both) {
+                mfma_blocks<QT, 1, true>(rowp1, tabs, b, b + 1, XR, valid, q, c);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) part[m][b0 + jj][r][4 * q + i] = c[jj][i];
+                for (int i = 0; i < 4; ++i) part[1][b][r][4 * q + i] = c[0][i];
+            }
+        }
         __syncthreads();
         // thread (pair jp, row rr), rows fastest: both matrices' block sums in block order
         const int t = (int)threadIdx.x, rr = t & 15, jp = (t >> 4) & 15;
