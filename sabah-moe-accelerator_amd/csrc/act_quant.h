@@ -92,7 +92,11 @@ __device__ inline uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32
 // whichever of the chunk's maximum and minimum reaches amax; only a chunk
 // holding both looks for the first one by index.  |iscale * x| <= 127 (1 + 2^-22)
 // rounds to at most 127, so ggml's clamp at 127 never applies.
-__device__ inline void row16_quant_q8K(const Act16& a, int c, uint8_t* act, const ActLayout& L) {
+// mfma_order: the chunk's 256 bytes in the grouped kernels' operand order, in
+// which the element k = 32 s + 8 q + i (sub-block s, quarter q, i < 8) sits
+// at byte 64 (s / 2) + 16 q + 8 (s % 2) + i, so one 16-byte load gives an
+// MFMA lane its eight elements of two sub-blocks (bsums and d unchanged).
+__device__ inline void row16_quant_q8K(const Act16& a, int c, uint8_t* act, const ActLayout& L, bool mfma_order = false) {
     const uint32_t l = threadIdx.x & 15u;
     float mx_l = a.v[0], mn_l = a.v[0];
 #pragma unroll
@@ -127,7 +131,14 @@ __device__ inline void row16_quant_q8K(const Act16& a, int c, uint8_t* act, cons
     packed.y = low_bytes4(b[4], b[5], b[6], b[7]);
     packed.z = low_bytes4(b[8], b[9], b[10], b[11]);
     packed.w = low_bytes4(b[12], b[13], b[14], b[15]);
-    reinterpret_cast<uint4*>(act + c * kActChunkStride)[l] = packed;
+    if (mfma_order) {
+        // elements 16 l .. 16 l + 7 and 16 l + 8 .. + 15: quarters 2 (l & 1) and 2 (l & 1) + 1 of sub-block l / 2
+        uint8_t* o = act + c * kActChunkStride + 64 * (l >> 2) + 32 * (l & 1u) + 8 * ((l >> 1) & 1u);
+        *reinterpret_cast<uint2*>(o) = make_uint2(packed.x, packed.y);
+        *reinterpret_cast<uint2*>(o + 16) = make_uint2(packed.z, packed.w);
+    } else {
+        reinterpret_cast<uint4*>(act + c * kActChunkStride)[l] = packed;
+    }
     // bsum = sum of the sixteen int8 values
     int s = 0;
     s = sdot4_i8(packed.x, 0x01010101u, s);
@@ -220,7 +231,7 @@ __device__ inline void act_prefetch(const ActBatch& B, ActRegs<ROUNDS>& R, int w
     }
 }
 
-__device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q) {
+__device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q, bool mfma_order = false) {
     const int nch = (B.k + 255) / 256;
     const int r = div_small(q, __builtin_amdgcn_rcpf((float)nch)), c = q - r * nch;
     const ActLayout L(B.k, B.at);
@@ -228,7 +239,7 @@ __device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q) 
     Act16 a;
 #pragma unroll
     for (int j = 0; j < 16; ++j) a.v[j] = in ? a_in.v[j] : 0.0f;
-    if (B.at == QT_Q8_K) row16_quant_q8K(a, c, B.act + r * B.act_stride, L);
+    if (B.at == QT_Q8_K) row16_quant_q8K(a, c, B.act + r * B.act_stride, L, mfma_order);
     else row16_quant_q8_0(a, c, B.act + r * B.act_stride, L);
 }
 

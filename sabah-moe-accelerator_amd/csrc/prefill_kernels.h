@@ -130,12 +130,14 @@ __global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
 // q8 rows in the kernels' activation layout (ActLayout), n_rows rows of k
 // floats.  Each workgroup quantises 16 chunk-rows (one per 16-lane row).
 // With `gather`, output row r is input row gather[r] / gdiv, for the rows
-// below *count (the grouped pairs: the rows come out in group order).
+// below *count (the grouped pairs: the rows come out in group order).  With
+// mfma_order (q8_K only), each chunk's bytes are in the grouped kernels'
+// operand order (row16_quant_q8K).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void k_quant_rows(const float* __restrict__ x, int n_rows, int k, int at,
                                                          uint8_t* __restrict__ out, int out_stride,
                                                          const int* __restrict__ gather, int gdiv,
-                                                         const int* __restrict__ count) {
+                                                         const int* __restrict__ count, int mfma_order) {
     const int nch = k / 256;
     const int q = blockIdx.x * (kThreads / 16) + (int)(threadIdx.x >> 4);
     if (q >= n_rows * nch) return;                       // whole 16-lane rows leave together
@@ -145,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void k_quant_rows(const float* __restrict
     const ActBatch B{x, (size_t)k, n_rows, k, at, out, out_stride};
     Act16 v;
     load16(x + (size_t)src * k, c * 256 + 16 * (int)(threadIdx.x & 15u), k, act_vec(B), v);
-    quant_chunk(B, v, q);
+    quant_chunk(B, v, q, mfma_order != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -294,6 +296,8 @@ struct XRegs {
     float dx[NBMAX];
     float bsv[NBMAX][4];
 };
+// The rows are in MFMA operand order (k_quant_rows with mfma_order): the
+// lane's eight bytes of sub-blocks 2 t and 2 t + 1 are one 16-byte load.
 template <int QT, int NBMAX>
 __device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const ActLayout& XL, int b0, int b1, int q) {
     const float* dxrow = reinterpret_cast<const float*>(xrow + XL.off_d);
@@ -302,8 +306,11 @@ __device__ inline void load_x(XRegs<NBMAX>& R, const uint8_t* xrow, const ActLay
     for (int j = 0; j < NBMAX; ++j) {
         const int b = min(b0 + j, b1 - 1);                 // blocks past b1 re-read the last one (unused)
 #pragma unroll
-        for (int sub = 0; sub < 8; ++sub)
-            R.X[j][sub] = *reinterpret_cast<const long*>(xrow + b * kActChunkStride + 32 * sub + 8 * q);
+        for (int t = 0; t < 4; ++t) {
+            const uint4 v = *reinterpret_cast<const uint4*>(xrow + b * kActChunkStride + 64 * t + 16 * q);
+            R.X[j][2 * t] = (long)((uint64_t)v.y << 32 | v.x);
+            R.X[j][2 * t + 1] = (long)((uint64_t)v.w << 32 | v.z);
+        }
         R.dx[j] = dxrow[b];
         if constexpr (QT == QT_Q4_K) {
             R.bsv[j][0] = (float)((int)bsrow[16 * b + 2 * q] + (int)bsrow[16 * b + 2 * q + 1]);
@@ -333,10 +340,11 @@ typedef float v4f32 __attribute__((ext_vector_type(4)));
 // issue, so at most four MFMA results are live (a kernel at 128 VGPRs keeps
 // four waves per SIMD without spilling; with more registers to spare, the
 // unpinned order overlaps more MFMAs and is faster).
-template <int QT, int NBMAX, bool PIN = false>
+template <int QT, int NBMAX, bool PIN = false, bool MASK = true>
 __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int b0, int b1, const XRegs<NBMAX>& R,
-                                   bool valid, int q, float (&c)[NBMAX][4]) {
+                                   bool valid_in, int q, float (&c)[NBMAX][4]) {
     constexpr int UB = UnitFmt<QT>::BYTES;
+    const bool valid = valid_in || !MASK;
 #pragma unroll
     for (int j = 0; j < NBMAX; ++j) {
         const int b = b0 + j;
@@ -564,11 +572,11 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
         if (pt) pair_x(pt, XR);
         if (b < nb) {
             float c[1][4];
-            mfma_blocks<QT, 1, true>(rowp, tabs, b, b + 1, XR, valid, q, c);
+            mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
 #pragma unroll
             for (int i = 0; i < 4; ++i) part[m][b][r][4 * q + i] = c[0][i];
             if (both) {
-                mfma_blocks<QT, 1, true>(rowp1, tabs, b, b + 1, XR, valid, q, c);
+                mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) part[1][b][r][4 * q + i] = c[0][i];
             }

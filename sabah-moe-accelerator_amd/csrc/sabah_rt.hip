@@ -807,7 +807,7 @@ static int mmid_grouped(int form, int qt, const uint8_t* bank, size_t expert_str
     const int x_div = x_rows == 1 ? n_ids : 1;
     const size_t xq_rows = P * (size_t)(k / 256);
     launch_kernel(KK_MMID, k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, (int)P, k,
-                  (int)QT_Q8_K, xq, xq_stride, (const int*)pair_of, x_div, (const int*)(off + E));
+                  (int)QT_Q8_K, xq, xq_stride, (const int*)pair_of, x_div, (const int*)(off + E), 1);
     (void)nx;
     if (form == 1) {
         GroupedDownArgs dn{};
@@ -1065,7 +1065,7 @@ static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D,
         const int n_rows = n_tokens * n_slots;
         const int chunk_rows = n_rows * (d_ff / 256);
         launch_kernel(KK_DOWN, k_quant_rows, dim3((unsigned)((chunk_rows + 15) / 16)), dim3(kThreads), 0, st, gu.h,
-                      n_rows, d_ff, act_type(qtd), hq, hb, (const int*)nullptr, 1, (const int*)nullptr);
+                      n_rows, d_ff, act_type(qtd), hq, hb, (const int*)nullptr, 1, (const int*)nullptr, 0);
         if (!ck(hipGetLastError(), "h quantisation launch")) return -1;
         a.hq = hq;
     }
@@ -1407,7 +1407,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     // the pairs' x rows in group order (pair p is token p / n_used)
     const size_t xq_rows = P * (size_t)(D / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((xq_rows + 15) / 16)), dim3(kThreads), 0, st, d_x, (int)P, D,
-                       (int)QT_Q8_K, xq, xq_stride, (const int*)pair_of, n_used, (const int*)(off + E));
+                       (int)QT_Q8_K, xq, xq_stride, (const int*)pair_of, n_used, (const int*)(off + E), 1);
     GroupedGateUpArgs gu{};
     gu.gate = static_cast<const uint8_t*>(L->gate);
     gu.up = static_cast<const uint8_t*>(L->up);
@@ -1423,7 +1423,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     launch_grouped_gate_up<false>(L->qt_gate, KK_GGATE_UP, dim3((unsigned)(F / kGuRows), (unsigned)E), st, gu);
     const size_t hq_rows = P * (size_t)(F / 256);
     hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((hq_rows + 15) / 16)), dim3(kThreads), 0, st, h, (int)P, F,
-                       (int)QT_Q8_K, hq, hq_stride, (const int*)nullptr, 1, (const int*)(off + E));
+                       (int)QT_Q8_K, hq, hq_stride, (const int*)nullptr, 1, (const int*)(off + E), 1);
     GroupedDownArgs dn{};
     dn.down = static_cast<const uint8_t*>(L->down);
     dn.expert_stride = row_bytes(L->qt_down, F) * (size_t)D;
