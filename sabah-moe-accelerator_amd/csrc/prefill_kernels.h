@@ -445,6 +445,13 @@ __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int
 // lead[reg] (its address mod 16).  A repeat stores the same bytes to the same
 // place, so every store is unconditional (a store under a condition lets the
 // compiler sink its load past the table set-up, a whole memory latency late).
+// With row_bytes (a multiple of 16) and a region that starts 16-aligned, each
+// row lands kRowPad bytes after the last (stage_row_stride): rows 16 B-aligned
+// would put rows r and r + 8 of an MFMA operand on the same LDS banks (2-way
+// conflicts on the unit field reads for 880-byte IQ3_S rows, 16-way for
+// 1152-byte Q4_K rows).  Padded chunks are stored as two 8-byte halves.
+constexpr int kRowPad = 8;
+__device__ inline int stage_row_stride(int rb, int lead) { return rb + ((rb & 15) == 0 && lead == 0 ? kRowPad : 0); }
 template <int NL>
 struct GroupStage {
     u32x4 d[NL];
@@ -452,15 +459,18 @@ struct GroupStage {
 };
 template <int NT, int NL, int NREG>
 __device__ inline void group_stage_issue(GroupStage<NL>& G, const uint8_t* const (&src)[NREG], int bytes, int cap,
-                                         int* leads) {
+                                         int* leads, int row_bytes = 0) {
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
-    int nch[NREG];
+    int nch[NREG], rch[NREG];
+    float rrcp[NREG];
     const uint8_t* base[NREG];
 #pragma unroll
     for (int m = 0; m < NREG; ++m) {
         const int lead = (int)(reinterpret_cast<uintptr_t>(src[m]) & 15);
         base[m] = src[m] - lead;
         nch[m] = (lead + bytes + 15) >> 4;
+        rch[m] = row_bytes && stage_row_stride(row_bytes, lead) != row_bytes ? row_bytes >> 4 : 0;   // chunks per padded row
+        rrcp[m] = __builtin_amdgcn_rcpf((float)max(rch[m], 1));
         if (threadIdx.x == 0) leads[m] = lead;
     }
 #pragma unroll
@@ -474,13 +484,20 @@ __device__ inline void group_stage_issue(GroupStage<NL>& G, const uint8_t* const
             }
         const int cc = min(c, nch[m] - 1);
         G.d[i] = *(g_u32x4*)(base[m] + 16 * cc);
-        G.off[i] = m * cap + 16 * cc;
+        G.off[i] = m * cap + 16 * cc + (rch[m] ? kRowPad * div_small(cc, rrcp[m]) : 0);
     }
 }
-template <int NL>
+template <int NL, bool PADDED = false>
 __device__ inline void group_stage_store(const GroupStage<NL>& G, uint8_t* stage) {
 #pragma unroll
-    for (int i = 0; i < NL; ++i) *reinterpret_cast<u32x4*>(stage + G.off[i]) = G.d[i];
+    for (int i = 0; i < NL; ++i) {
+        if constexpr (PADDED) {                             // 8-byte aligned
+            *reinterpret_cast<uint2*>(stage + G.off[i]) = make_uint2(G.d[i].x, G.d[i].y);
+            *reinterpret_cast<uint2*>(stage + G.off[i] + 8) = make_uint2(G.d[i].z, G.d[i].w);
+        } else {
+            *reinterpret_cast<u32x4*>(stage + G.off[i]) = G.d[i];
+        }
+    }
 }
 // staging bytes of one region of rows rows x rb bytes, room for its lead
 __host__ __device__ constexpr int group_cap(int rows, int rb) { return (rows * rb + 31) & ~15; }
@@ -502,7 +519,10 @@ constexpr int kGuMaxBlocks = 8;               // 256-blocks of k: one per wave
 // one workgroup's gate and up rows at k <= 2048, and the 16-byte loads per thread that stage them
 template <int QT>
 struct GuStage {
-    static constexpr int CAP = group_cap(kGuRows, kGuMaxBlocks * UnitFmt<QT>::BYTES);
+    // padded rows (measured: IQ3_S gate/up 332 against 346 us, Q4_K 132 against
+    // 172 us per 512-token call; Q6_K 235 against 231 us, so not padded)
+    static constexpr bool PAD = QT != QT_Q6_K;
+    static constexpr int CAP = group_cap(kGuRows, kGuMaxBlocks * UnitFmt<QT>::BYTES + (PAD ? kRowPad : 0));
     static constexpr int LOADS = (2 * (CAP / 16) + kGuThreads - 1) / kGuThreads;
 };
 
@@ -553,7 +573,8 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
     if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
     GroupStage<GuStage<QT>::LOADS> G;
     const uint8_t* const src[2] = {wg, wu};
-    group_stage_issue<NT, GuStage<QT>::LOADS, 2>(G, src, kGuRows * (int)rb, GuStage<QT>::CAP, leads);
+    group_stage_issue<NT, GuStage<QT>::LOADS, 2>(G, src, kGuRows * (int)rb, GuStage<QT>::CAP, leads,
+                                                  GuStage<QT>::PAD ? (int)rb : 0);
     auto pair_x = [&](int pt, XRegs<1>& R) {
         const int cnt = min(kPairTile, n_e - pt);
         const uint8_t* xrow = a.xq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.xq_stride;
@@ -562,10 +583,11 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
     XRegs<1> XR;
     pair_x(0, XR);                                          // with the weights
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
-    group_stage_store(G, stage);
+    group_stage_store<GuStage<QT>::LOADS, GuStage<QT>::PAD>(G, stage);
     __syncthreads();                                        // staged rows, leads and table written
-    const uint8_t* rowp = stage + GuStage<QT>::CAP * m + leads[m] + (size_t)r * rb;
-    const uint8_t* rowp1 = stage + GuStage<QT>::CAP + leads[1] + (size_t)r * rb;
+    auto rstride = [&](int lead) { return GuStage<QT>::PAD ? stage_row_stride((int)rb, lead) : (int)rb; };
+    const uint8_t* rowp = stage + GuStage<QT>::CAP * m + leads[m] + r * rstride(leads[m]);
+    const uint8_t* rowp1 = stage + GuStage<QT>::CAP + leads[1] + r * rstride(leads[1]);
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
