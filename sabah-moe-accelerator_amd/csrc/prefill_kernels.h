@@ -547,6 +547,12 @@ __device__ inline float* pair_dst(float* dst, size_t nb1, size_t nb2, int n_ids,
                                     (size_t)(p % n_ids) * nb1);
 }
 
+// Column of pair p in row r of a block's partial sums: the row's four 4-pair
+// groups in the order g ^ ((r >> 1) & 3), so a wave's 16-byte stores (one row,
+// four pairs per lane) and the epilogue's reads (sixteen pairs of two rows
+// per half-wave) each fall on distinct LDS banks.
+__device__ inline int part_col(int r, int p) { return 4 * ((p >> 2) ^ ((r >> 1) & 3)) + (p & 3); }
+
 template <int QT, bool MMID = false>
 __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUpArgs a) {
     constexpr int NT = kGuThreads;
@@ -595,22 +601,22 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
         if (b < nb) {
             float c[1][4];
             mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) part[m][b][r][4 * q + i] = c[0][i];
+            *reinterpret_cast<float4*>(&part[m][b][r][part_col(r, 4 * q)]) = make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
             if (both) {
                 mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) part[1][b][r][4 * q + i] = c[0][i];
+                *reinterpret_cast<float4*>(&part[1][b][r][part_col(r, 4 * q)]) =
+                    make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
             }
         }
         __syncthreads();
-        // thread (pair jp, row rr), rows fastest: both matrices' block sums in block order
-        const int t = (int)threadIdx.x, rr = t & 15, jp = (t >> 4) & 15;
+        // thread (row rr, pair jp), pairs fastest: both matrices' block sums in block order
+        const int t = (int)threadIdx.x, jp = t & 15, rr = (t >> 4) & 15;
         if (t < 256 && jp < cnt) {
             float g = 0.0f, u = 0.0f;
+            const int col = part_col(rr, jp);
             for (int b = 0; b < nb; ++b) {
-                g = __fadd_rn(g, part[0][b][rr][jp]);
-                u = __fadd_rn(u, part[1][b][rr][jp]);
+                g = __fadd_rn(g, part[0][b][rr][col]);
+                u = __fadd_rn(u, part[1][b][rr][col]);
             }
             if constexpr (MMID) {
                 float* d = pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.k, a.pair_of[g0 + pt + jp]);
