@@ -61,40 +61,68 @@ struct GroupArgs {
     int poison_rows;
 };
 
-// exclusive scan of one int per thread over the workgroup; tmp holds blockDim.x ints
+// exclusive scan of one int per thread over the workgroup (a multiple of 64
+// threads, at most 1024): a shuffle scan per wave, then the wave totals;
+// tmp holds 16 ints
 __device__ inline int block_exclusive_scan(int v, int* tmp, int& total) {
-    const int i = (int)threadIdx.x, n = (int)blockDim.x;
-    tmp[i] = v;
-    __syncthreads();
-    for (int o = 1; o < n; o <<= 1) {
-        const int x = i >= o ? tmp[i - o] : 0;
-        __syncthreads();
-        tmp[i] += x;
-        __syncthreads();
+    const int lane = (int)(threadIdx.x & 63u), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
     }
-    total = tmp[n - 1];
-    const int r = tmp[i] - v;
+    if (lane == 63) tmp[wave] = x;
     __syncthreads();
-    return r;
+    int before = 0;
+    total = 0;
+    for (int w = 0; w < nw; ++w) {
+        const int t = tmp[w];
+        before += w < wave ? t : 0;
+        total += t;
+    }
+    __syncthreads();
+    return before + x - v;
 }
+
+// ids a thread keeps in registers between the histogram and the scatter
+// (n_tokens * k up to 8 x 1024); larger batches re-read them
+constexpr int kGroupIdRegs = 8;
 
 // one workgroup of kGroupThreads; dynamic LDS: 2 * n_experts + kGroupThreads ints
 __global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
     extern __shared__ int glds[];
-    const int E = a.n_experts, P = a.n_tokens * a.k;
+    const int E = a.n_experts, P = a.n_tokens * a.k, NT = (int)blockDim.x, tid = (int)threadIdx.x;
     int* cnt = glds;
     int* fill = glds + E;
     int* tmp = glds + 2 * E;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
-    __syncthreads();
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-        const int e = a.ids[p];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    // every id load is issued before any is used (one memory latency, not one per pair)
+    const bool in_regs = P <= kGroupIdRegs * NT;
+    int idv[kGroupIdRegs];
+#pragma unroll
+    for (int i = 0; i < kGroupIdRegs; ++i) {
+        const int p = tid + NT * i;
+        idv[i] = in_regs && p < P ? a.ids[p] : -1;
     }
+    for (int e = tid; e < E; e += NT) cnt[e] = 0;
+    __syncthreads();
+    // f(p, e) for each of the thread's pairs
+    auto each_pair = [&](auto&& f) {
+        if (in_regs) {
+#pragma unroll
+            for (int i = 0; i < kGroupIdRegs; ++i)
+                if (tid + NT * i < P) f(tid + NT * i, idv[i]);
+        } else {
+            for (int p = tid; p < P; p += NT) f(p, a.ids[p]);
+        }
+    };
+    each_pair([&](int, int e) {
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    });
     __syncthreads();
     // each thread scans a contiguous run of seg experts
-    const int seg = (E + (int)blockDim.x - 1) / (int)blockDim.x;
-    const int e0 = min(E, (int)threadIdx.x * seg), e1 = min(E, e0 + seg);
+    const int seg = (E + NT - 1) / NT;
+    const int e0 = min(E, tid * seg), e1 = min(E, e0 + seg);
     int s = 0;
     for (int e = e0; e < e1; ++e) s += cnt[e];
     int total;
@@ -104,11 +132,10 @@ __global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
         a.off[e] = run;
         run += cnt[e];
     }
-    if (threadIdx.x == 0) a.off[E] = total;
+    if (tid == 0) a.off[E] = total;
     __syncthreads();
     bool bad = false;
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-        const int e = a.ids[p];
+    each_pair([&](int p, int e) {
         if (e >= 0 && e < E) {
             const int pos = atomicAdd(&fill[e], 1);
             a.pair_of[pos] = p;
@@ -122,7 +149,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group_pairs(GroupArgs a) {
                 for (int r = 0; r < a.poison_rows; ++r) d[r] = __builtin_nanf("");
             }
         }
-    }
+    });
     if (bad) *reinterpret_cast<volatile unsigned int*>(a.err) = 1u;
 }
 
@@ -710,7 +737,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_down(GroupedDownArgs a)
 // ---------------------------------------------------------------------------
 // Combine in slot order, as k_down_combine does:
 //   out[t][i] = [resid[t][i] +] ((y(t,0)[i] w0 + y(t,1)[i] w1) + ...) [+ shared[t][i]]
-// grid = (ceil(d_model / 256), n_tokens); a token with an invalid id gets NaN.
+// grid = (ceil(d_model / (256 VW)), n_tokens); a token with an invalid id gets NaN.
 // ---------------------------------------------------------------------------
 struct CombineArgs {
     const float* y;               // [pairs in group order][d_model]
@@ -722,23 +749,70 @@ struct CombineArgs {
     int k, d_model;
 };
 
+// VW elements per thread (4 when d_model % 4 == 0 and out, resid, shared
+// are 16-byte aligned, else 1); up to kCombineSlots slots' rows are all
+// loaded before the first is added (one memory latency per thread, not one
+// per slot); more slots take a loop.
+constexpr int kCombineSlots = 16;
+template <int VW>
+struct CombineVec {
+    float v[VW];
+};
+template <int VW>
+__device__ inline CombineVec<VW> combine_load(const float* p) {
+    CombineVec<VW> r;
+    if constexpr (VW == 4) {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        r.v[0] = x.x; r.v[1] = x.y; r.v[2] = x.z; r.v[3] = x.w;
+    } else {
+        r.v[0] = *p;
+    }
+    return r;
+}
+template <int VW>
 __global__ __launch_bounds__(kThreads) void k_combine(CombineArgs a) {
-    const int t = blockIdx.y, i = blockIdx.x * kThreads + (int)threadIdx.x;
+    const int t = blockIdx.y, i = VW * (blockIdx.x * kThreads + (int)threadIdx.x);
     if (i >= a.d_model) return;
     const int* pos = a.pos_of + (size_t)t * a.k;
     const float* wt = a.w + (size_t)t * a.k;
     bool bad = false;
     for (int s = 0; s < a.k; ++s) bad |= pos[s] < 0;
-    float* o = a.out + (size_t)t * a.d_model + i;
+    CombineVec<VW> acc;
     if (bad) {
-        *o = __builtin_nanf("");
-        return;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) acc.v[e] = __builtin_nanf("");
+    } else {
+        auto yrow = [&](int s) { return combine_load<VW>(a.y + (size_t)pos[s] * a.d_model + i); };
+        auto add = [&](int s, const CombineVec<VW>& y) {
+            const float w = wt[s];
+#pragma unroll
+            for (int e = 0; e < VW; ++e) acc.v[e] = s == 0 ? __fmul_rn(y.v[e], w) : __fadd_rn(acc.v[e], __fmul_rn(y.v[e], w));
+        };
+        if (a.k <= kCombineSlots) {
+            CombineVec<VW> y[kCombineSlots];
+#pragma unroll
+            for (int s = 0; s < kCombineSlots; ++s)
+                if (s < a.k) y[s] = yrow(s);
+#pragma unroll
+            for (int s = 0; s < kCombineSlots; ++s)
+                if (s < a.k) add(s, y[s]);
+        } else {
+            for (int s = 0; s < a.k; ++s) add(s, yrow(s));
+        }
+        if (a.shared) {
+            const CombineVec<VW> sh = combine_load<VW>(a.shared + (size_t)t * a.d_model + i);
+#pragma unroll
+            for (int e = 0; e < VW; ++e) acc.v[e] = __fadd_rn(acc.v[e], sh.v[e]);
+        }
+        if (a.resid) {
+            const CombineVec<VW> r = combine_load<VW>(a.resid + (size_t)t * a.d_model + i);
+#pragma unroll
+            for (int e = 0; e < VW; ++e) acc.v[e] = __fadd_rn(r.v[e], acc.v[e]);
+        }
     }
-    float acc = __fmul_rn(a.y[(size_t)pos[0] * a.d_model + i], wt[0]);
-    for (int s = 1; s < a.k; ++s) acc = __fadd_rn(acc, __fmul_rn(a.y[(size_t)pos[s] * a.d_model + i], wt[s]));
-    if (a.shared) acc = __fadd_rn(acc, a.shared[(size_t)t * a.d_model + i]);
-    if (a.resid) acc = __fadd_rn(a.resid[(size_t)t * a.d_model + i], acc);
-    *o = acc;
+    float* o = a.out + (size_t)t * a.d_model + i;
+    if constexpr (VW == 4) *reinterpret_cast<float4*>(o) = make_float4(acc.v[0], acc.v[1], acc.v[2], acc.v[3]);
+    else *o = acc.v[0];
 }
 
 }  // namespace sabah

@@ -1435,8 +1435,14 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     dn.d_ff = F;
     launch_grouped_down<false>(L->qt_down, KK_GDOWN, dim3((unsigned)(D / kDownRows), (unsigned)E), st, dn);
     CombineArgs cb{y, pos_of, d_w, shared, d_resid, d_out, n_used, D};
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((D + kThreads - 1) / kThreads), (unsigned)n_tokens), dim3(kThreads), 0,
-                       st, cb);
+    const bool v4 = D % 4 == 0 && ((reinterpret_cast<uintptr_t>(d_out) | reinterpret_cast<uintptr_t>(d_resid) |
+                                    reinterpret_cast<uintptr_t>(shared)) & 15) == 0;
+    if (v4)
+        hipLaunchKernelGGL(k_combine<4>, dim3((unsigned)((D + 4 * kThreads - 1) / (4 * kThreads)), (unsigned)n_tokens),
+                           dim3(kThreads), 0, st, cb);
+    else
+        hipLaunchKernelGGL(k_combine<1>, dim3((unsigned)((D + kThreads - 1) / kThreads), (unsigned)n_tokens),
+                           dim3(kThreads), 0, st, cb);
     return ck(hipGetLastError(), "grouped layer launch") ? 0 : -1;
 }
 
