@@ -122,6 +122,27 @@ struct LdsWindow {
     // the address stays derived from the LDS pointer (no integer round trip),
     // so the reads are LDS instructions, not flat ones
     __device__ inline void load(const uint8_t* unit_lds) {
+        if constexpr (UnitFmt<QT>::BYTES % 16 == 0 && ORG == 0 && NF % 4 == 0) {
+            // 16-byte aligned units (Q4_K rows from a 16-aligned bank): 16-byte
+            // reads.  Lanes on consecutive units are 144 bytes apart, so dword
+            // reads of 32 lanes fall on 8 banks (4-way conflicts); 16-byte
+            // reads of 8 lanes cover all 32
+            if ((reinterpret_cast<uintptr_t>(unit_lds) & 15) == 0) {
+                const uint4* g = reinterpret_cast<const uint4*>(unit_lds);
+#pragma unroll
+                for (int c = 0; c < NF / 4; ++c) {
+                    const uint4 v = g[c];
+                    W[1 + 4 * c] = v.x;
+                    W[2 + 4 * c] = v.y;
+                    W[3 + 4 * c] = v.z;
+                    W[4 + 4 * c] = v.w;
+                }
+                W[0] = 0;                                 // the dword before the unit (not used by these formats)
+                W[NF + 1] = 0;
+                sh = 0;
+                return;
+            }
+        }
         const uint8_t* o = unit_lds + ORG - 4;
         sh = (uint32_t)(reinterpret_cast<uintptr_t>(o) & 3);
         const uint32_t* g = reinterpret_cast<const uint32_t*>(o - sh);
