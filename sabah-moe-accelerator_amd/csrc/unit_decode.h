@@ -122,24 +122,38 @@ struct LdsWindow {
     // the address stays derived from the LDS pointer (no integer round trip),
     // so the reads are LDS instructions, not flat ones
     __device__ inline void load(const uint8_t* unit_lds) {
-        if constexpr (UnitFmt<QT>::BYTES % 16 == 0 && ORG == 0 && NF % 4 == 0) {
-            // 16-byte aligned units (Q4_K rows from a 16-aligned bank): 16-byte
-            // reads.  Lanes on consecutive units are 144 bytes apart, so dword
-            // reads of 32 lanes fall on 8 banks (4-way conflicts); 16-byte
-            // reads of 8 lanes cover all 32
-            if ((reinterpret_cast<uintptr_t>(unit_lds) & 15) == 0) {
-                const uint4* g = reinterpret_cast<const uint4*>(unit_lds);
+        // A unit whose NF dwords are exactly its bytes, at an A-aligned address
+        // (A = 16 or 8, units an odd number of A-byte words apart: Q4_K 9 x 16,
+        // Q8_0 / IQ4_XS 17 x 8, IQ4_NL 9 x 8 bytes), is read as A-byte words:
+        // lanes on consecutive units then cover every bank, where dword reads
+        // put 32 lanes on 8 (Q4_K) or 16 banks.  W[0] and W[NF + 1] hold only
+        // bytes outside the unit, which no field uses.
+        constexpr int UB = UnitFmt<QT>::BYTES;
+        constexpr int A = UB % 16 == 0 && (UB / 16) % 2 == 1 ? 16 : UB % 8 == 0 && (UB / 8) % 2 == 1 ? 8 : 0;
+        if constexpr (A != 0 && 4 * NF == UB) {
+            if ((reinterpret_cast<uintptr_t>(unit_lds) & (A - 1)) == 0) {
+                if constexpr (A == 16) {
+                    const uint4* g = reinterpret_cast<const uint4*>(unit_lds);
 #pragma unroll
-                for (int c = 0; c < NF / 4; ++c) {
-                    const uint4 v = g[c];
-                    W[1 + 4 * c] = v.x;
-                    W[2 + 4 * c] = v.y;
-                    W[3 + 4 * c] = v.z;
-                    W[4 + 4 * c] = v.w;
+                    for (int c = 0; c < NF / 4; ++c) {
+                        const uint4 v = g[c];
+                        W[1 + 4 * c] = v.x;
+                        W[2 + 4 * c] = v.y;
+                        W[3 + 4 * c] = v.z;
+                        W[4 + 4 * c] = v.w;
+                    }
+                } else {
+                    const uint2* g = reinterpret_cast<const uint2*>(unit_lds);
+#pragma unroll
+                    for (int c = 0; c < NF / 2; ++c) {
+                        const uint2 v = g[c];
+                        W[1 + 2 * c] = v.x;
+                        W[2 + 2 * c] = v.y;
+                    }
                 }
-                W[0] = 0;                                 // the dword before the unit (not used by these formats)
+                W[0] = 0;
                 W[NF + 1] = 0;
-                sh = 0;
+                sh = ORG & 3;
                 return;
             }
         }
