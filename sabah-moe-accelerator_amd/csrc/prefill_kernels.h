@@ -232,7 +232,7 @@ __device__ inline long iq3s_quarter_operand(const Iq3sQuarter& F, const uint8_t*
     // [qs_2q, h_2q, qs_2q+1, h_2q+1]: the two 16-bit table indices
     const uint32_t sel = (4u + p) | (p << 8) | ((5u + p) << 16) | ((p + 1u) << 24);
     const uint32_t W = __builtin_amdgcn_perm(F.qs[s >> 1], F.lh[s >> 1], sel);
-    const uint32_t g0 = lds_u32(tabs, kLdsGrid + ((W & 0xFFFFu) << 2));
+    const uint32_t g0 = lds_u32(tabs, kLdsGrid + lo16_x4(W));
     const uint32_t g1 = lds_u32(tabs, kLdsGrid + (W >> 14));      // h < 32: bits 14, 15 of W are 0
     return (long)(((uint64_t)g1 << 32) | g0);
 }

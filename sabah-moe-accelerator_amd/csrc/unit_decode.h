@@ -187,6 +187,17 @@ constexpr int kLdsTables = 8192 * 4;
 
 __device__ inline uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
 
+// (w & 0xFFFF) << 2, the byte address of the table index in w's low half, in
+// one instruction: the SDWA operand select reads the low 16 bits of w (the
+// compiler otherwise shifts and masks in two)
+__device__ inline uint32_t lo16_x4(uint32_t w) {
+    uint32_t a;
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+        : "=v"(a)
+        : "v"(w));
+    return a;
+}
+
 // v_perm selector that negates byte j of a codebook word g where bit j of n
 // is set, taking that byte from g ^ 0xFEFEFEFE (source 0) instead of g
 // (source 1): for odd g, -g = g ^ 0xFE (two's complement ~(g - 1), and
@@ -336,7 +347,7 @@ __device__ inline int iq3s_item(const uint32_t (&F)[27], int ib, const uint8_t* 
         // [qs_g, h_g, qs_g+1, h_g+1] for g = 2l: two 16-bit table indices
         const uint32_t sel = (4u + pp) | (pp << 8) | ((5u + pp) << 16) | ((pp + 1u) << 24);
         const uint32_t D = __builtin_amdgcn_perm(Q, H[l >> 1], sel);
-        v[2 * l] = lds_u32(smem, kLdsGrid + ((D & 0xFFFFu) << 2));
+        v[2 * l] = lds_u32(smem, kLdsGrid + lo16_x4(D));
         v[2 * l + 1] = lds_u32(smem, kLdsGrid + (D >> 14));      // h < 32: bits 14, 15 of D are 0
     }
     return 2 * (int)((F[26] >> (4 * ib)) & 15u) + 1;
