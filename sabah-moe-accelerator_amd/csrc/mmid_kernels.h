@@ -743,7 +743,10 @@ __device__ inline void gate_up_rounds_tile(const GateUpArgs& a, int t, int s, in
     __syncthreads();                                        // activations and tables ready
     uint8_t* region = stage + 16 * WCH * wave;
     const float rcp_nus = __builtin_amdgcn_rcpf((float)NUS);
-    const int j = lane / PER, half = lane & (PER - 1);      // the lane's unit in the round and its half
+    // the lane's unit in the round and its half: with two lanes per unit, the
+    // halves sit 32 lanes apart, so a half-wave's field reads come from 32
+    // units (110 bytes apart) rather than 16 units twice, on fewer shared banks
+    const int j = PER == 2 ? lane & 31 : lane, half = PER == 2 ? lane >> 5 : 0;
     // a lane's unit column is the same in every round (a wave's rounds are
     // 128 units apart and NUS divides 128), so its activation half is read once
     uint32_t A[4][8];
@@ -768,7 +771,7 @@ __device__ inline void gate_up_rounds_tile(const GateUpArgs& a, int t, int s, in
                 uint32_t G[UnitFmt<QT>::NF], dbits;
                 iq3s_half_fields(unit, half, G, dbits);
                 int bs = iq3s_half_bsum(G, tabs, A);
-                bs += (int)dpp<kDppXor1>((uint32_t)bs);
+                bs += __shfl_xor(bs, 32);                  // the partner lane's half
                 if (half == 0)
                     prow[us] = __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(act + AL.off_d)[us]),
                                          (float)bs);
