@@ -393,8 +393,12 @@ __device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs
     constexpr int PER = SPLIT ? 2 : 1;                  // lanes per unit
     const int n = S.T.n_mat * S.nv;
     const float rcp_nv = __builtin_amdgcn_rcpf((float)S.nv);
-    const int half = SPLIT ? (int)(threadIdx.x & 1u) : 0;
-    for (int u = (int)threadIdx.x / PER; u < n; u += NT / PER) {     // both lanes of a pair iterate together
+    // with two lanes per unit the halves sit 32 lanes apart (a half-wave's
+    // field reads span 32 units): lane l of wave w takes unit 32 w + l % 32
+    const int tid = (int)threadIdx.x;
+    const int half = SPLIT ? (tid >> 5) & 1 : 0;
+    const int u0 = SPLIT ? 32 * (tid >> 6) + (tid & 31) : tid;
+    for (int u = u0; u < n; u += NT / PER) {           // both lanes of a pair iterate together
         const int t = div_small(u, rcp_nv);
         const int v = S.v0 + (u - t * S.nv);             // tile-relative unit (row-major over the rows)
         const int r = div_small(v, S.T.rcp_nus), us = v - r * S.T.NUS;
@@ -407,7 +411,7 @@ __device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs
             iq3s_half_fields(unit, half, G, dbits);
             act_half(act + us * kActChunkStride, half, A);
             int bs = iq3s_half_bsum(G, tabs, A);
-            bs += (int)dpp<kDppXor1>((uint32_t)bs);       // the partner lane's half
+            bs += __shfl_xor(bs, 32);                    // the partner lane's half
             if (half == 0)
                 prow[us] = __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(act + AL.off_d)[us]), (float)bs);
         } else {
