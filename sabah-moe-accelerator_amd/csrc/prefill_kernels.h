@@ -661,9 +661,14 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
 // Grouped down.  grid = (d_model / 64, n_experts), 256 threads; wave w owns
 // rows 16 w .. 16 w + 15 of the workgroup's 64, over the whole of k.
 // ---------------------------------------------------------------------------
-template <int QT>
+// ROWS = 128 (k <= 768): each wave takes two 16-row groups against the same
+// activation registers, so a pair tile's activations are loaded once per 32
+// rows and the table built once per 128.
+template <int QT, int ROWS = kDownRows>
 struct DownStage {
-    static constexpr int CAP = group_cap(kDownRows, kDownBlocks * UnitFmt<QT>::BYTES);
+    static constexpr int NB = ROWS == kDownRows ? kDownBlocks : 3;       // 256-blocks of k held
+    static constexpr int RG = ROWS / (4 * 16);                           // 16-row groups per wave
+    static constexpr int CAP = group_cap(ROWS, NB * UnitFmt<QT>::BYTES);
     static constexpr int LOADS = (CAP / 16 + kThreads - 1) / kThreads;
 };
 
@@ -682,27 +687,28 @@ struct GroupedDownArgs {
     size_t dst_nb1, dst_nb2;
 };
 
-template <int QT, bool MMID = false>
+template <int QT, bool MMID = false, int ROWS = kDownRows>
 __global__ __launch_bounds__(kThreads, 2) void k_grouped_down(GroupedDownArgs a) {
+    using DS = DownStage<QT, ROWS>;
     const int e = blockIdx.y;
     const int g0 = a.off[e], n_e = a.off[e + 1] - g0;
     if (n_e == 0) return;
     __shared__ __align__(16) uint8_t tabs[QT == QT_IQ3_S ? kLdsTables : 16];
     __shared__ int leads[1];
-    __shared__ __align__(16) uint8_t stage_mem[16 + DownStage<QT>::CAP + 16];
+    __shared__ __align__(16) uint8_t stage_mem[16 + DS::CAP + 16];
     uint8_t* const stage = stage_mem + 16;
-    const int row0 = blockIdx.x * kDownRows;
+    const int row0 = blockIdx.x * ROWS;
     const int nb = a.d_ff / 256;
     const size_t rb = row_bytes(QT, a.d_ff);
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
-    const int r = lane & 15, q = lane >> 4, rbase = 16 * wave, j = lane & 15;
+    const int r = lane & 15, q = lane >> 4, rbase = 16 * DS::RG * wave, j = lane & 15;
     const ActLayout HL(a.d_ff, QT_Q8_K);
     GridRegs<kThreads> gr;
     if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<kThreads>((int)threadIdx.x);
-    GroupStage<DownStage<QT>::LOADS> G;
+    GroupStage<DS::LOADS> G;
     const uint8_t* const src[1] = {a.down + (size_t)e * a.expert_stride + (size_t)row0 * rb};
-    group_stage_issue<kThreads, DownStage<QT>::LOADS, 1>(G, src, kDownRows * (int)rb, DownStage<QT>::CAP, leads);
-    auto pair_x = [&](int pt, XRegs<kDownBlocks>& R) {
+    group_stage_issue<kThreads, DS::LOADS, 1>(G, src, ROWS * (int)rb, DS::CAP, leads);
+    auto pair_x = [&](int pt, XRegs<DS::NB>& R) {
         const int cnt = min(kPairTile, n_e - pt);
         const uint8_t* hrow = a.hq + (size_t)(g0 + pt + min(j, cnt - 1)) * a.hq_stride;
         load_x<QT>(R, hrow, HL, 0, nb, q);
@@ -711,25 +717,28 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_down(GroupedDownArgs a)
     group_stage_store(G, stage);
     __syncthreads();                                        // staged rows, lead and table written
     const uint8_t* rowp = stage + leads[0] + (size_t)(rbase + r) * rb;
-    XRegs<kDownBlocks> XR;
+    XRegs<DS::NB> XR;
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
         pair_x(pt, XR);
-        float c[kDownBlocks][4];
-        mfma_blocks<QT, kDownBlocks>(rowp, tabs, 0, nb, XR, valid, q, c);
-        // the lane's row for pairs 4q .. 4q + 3
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (4 * q + i >= cnt) break;
-            float acc = 0.0f;
+        for (int rg = 0; rg < DS::RG; ++rg) {
+            float c[DS::NB][4];
+            mfma_blocks<QT, DS::NB>(rowp + (size_t)(16 * rg) * rb, tabs, 0, nb, XR, valid, q, c);
+            // the lane's row for pairs 4q .. 4q + 3
 #pragma unroll
-            for (int jj = 0; jj < kDownBlocks; ++jj)
-                if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
-            const int pi = g0 + pt + 4 * q + i;
-            float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, a.pair_of[pi])
-                              : a.y + (size_t)pi * a.d_model;
-            out[row0 + rbase + r] = acc;
+            for (int i = 0; i < 4; ++i) {
+                if (4 * q + i >= cnt) break;
+                float acc = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < DS::NB; ++jj)
+                    if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
+                const int pi = g0 + pt + 4 * q + i;
+                float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, a.pair_of[pi])
+                                  : a.y + (size_t)pi * a.d_model;
+                out[row0 + rbase + 16 * rg + r] = acc;
+            }
         }
     }
 }
