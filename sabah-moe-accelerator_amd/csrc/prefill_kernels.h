@@ -625,6 +625,8 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
         if (pt) pair_x(pt, XR);
+        // MMID: the epilogue thread's dst row (pair jp = t % 16), loaded before the products
+        const int pdst = MMID && threadIdx.x < 256 ? a.pair_of[g0 + pt + min((int)(threadIdx.x & 15u), cnt - 1)] : 0;
         if (b < nb) {
             float c[1][4];
             mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
@@ -646,7 +648,7 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
                 u = __fadd_rn(u, part[1][b][rr][col]);
             }
             if constexpr (MMID) {
-                float* d = pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.k, a.pair_of[g0 + pt + jp]);
+                float* d = pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.k, pdst);
                 d[row0 + rr] = g;
                 d[row0 + kGuRows + rr] = u;
             } else {
@@ -722,6 +724,12 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_down(GroupedDownArgs a)
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
         pair_x(pt, XR);
+        // MMID: the dst rows of the lane's four pairs, loaded now so the stores
+        // after the products do not wait for them
+        int pidx[4] = {0, 0, 0, 0};
+        if constexpr (MMID)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pidx[i] = a.pair_of[g0 + pt + min(4 * q + i, cnt - 1)];
 #pragma unroll
         for (int rg = 0; rg < DS::RG; ++rg) {
             float c[DS::NB][4];
@@ -735,7 +743,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_down(GroupedDownArgs a)
                 for (int jj = 0; jj < DS::NB; ++jj)
                     if (jj < nb) acc = __fadd_rn(acc, c[jj][i]);
                 const int pi = g0 + pt + 4 * q + i;
-                float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, a.pair_of[pi])
+                float* out = MMID ? pair_dst(a.dst, a.dst_nb1, a.dst_nb2, a.n_ids, pidx[i])
                                   : a.y + (size_t)pi * a.d_model;
                 out[row0 + rbase + 16 * rg + r] = acc;
             }
