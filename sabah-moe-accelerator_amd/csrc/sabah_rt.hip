@@ -539,14 +539,30 @@ SABAH_API void sabah_host_free(void* p) {
 SABAH_API int sabah_dev_mem(size_t* free_bytes, size_t* total_bytes) {
     return ck(hipMemGetInfo(free_bytes, total_bytes), "device memory info") ? 0 : -1;
 }
+// The blocking copies and the memset are ordered after everything the
+// library's streams hold and complete before they return (the ordering a
+// null-stream call has against blocking streams).  The library's streams are
+// non-blocking, so a null-stream call alone would not wait for them: each call
+// drains the copy stream, then runs on the compute stream and waits for it.
+static int ordered_copy(void* dst, const void* src, size_t n, hipMemcpyKind kind, const char* what) {
+    if (!g_stream) return ck(hipMemcpy(dst, src, n, kind), what) ? 0 : -1;
+    return ck(hipStreamSynchronize(g_copy), what) && ck(hipMemcpyAsync(dst, src, n, kind, g_stream), what) &&
+                   ck(hipStreamSynchronize(g_stream), what)
+               ? 0
+               : -1;
+}
 SABAH_API int sabah_memcpy_h2d(void* dst, const void* src, size_t n) {
-    return ck(hipMemcpy(dst, src, n, hipMemcpyHostToDevice), "copy to device") ? 0 : -1;
+    return ordered_copy(dst, src, n, hipMemcpyHostToDevice, "copy to device");
 }
 SABAH_API int sabah_memcpy_d2h(void* dst, const void* src, size_t n) {
-    return ck(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost), "copy to host") ? 0 : -1;
+    return ordered_copy(dst, src, n, hipMemcpyDeviceToHost, "copy to host");
 }
 SABAH_API int sabah_memset_d(void* dst, int v, size_t n) {
-    return ck(hipMemset(dst, v, n), "device memset") ? 0 : -1;
+    if (!g_stream) return ck(hipMemset(dst, v, n), "device memset") && ck(hipDeviceSynchronize(), "device memset") ? 0 : -1;
+    return ck(hipStreamSynchronize(g_copy), "device memset") && ck(hipMemsetAsync(dst, v, n, g_stream), "device memset") &&
+                   ck(hipStreamSynchronize(g_stream), "device memset")
+               ? 0
+               : -1;
 }
 // host to device on the library's copy stream (ordered against the compute
 // stream only through the event calls below)

@@ -122,8 +122,12 @@ static int sabah_bridge_load(int device) {
 }
 
 /* The device copy of a host expert tensor: made and registered on first
- * sight, looked up afterwards.  Returns 0, or -1 with the bridge error set. */
-static int sabah_bridge_register_host(const sabah_bridge_tensor *src0) {
+ * sight, looked up afterwards.  The copy is issued on the call's stream and
+ * waited for there, so it is complete, in that stream's order, before the
+ * call's kernels read it (ggml's stream is non-blocking: a copy on the null
+ * stream would not be ordered before them).  Returns 0, or -1 with the bridge
+ * error set. */
+static int sabah_bridge_register_host(const sabah_bridge_tensor *src0, hipStream_t stream) {
     sabah_bridge_state *b = &g_sabah_bridge;
     const size_t bytes = src0->nb[2] * (size_t)src0->ne[2];
     int rc = 0;
@@ -140,7 +144,8 @@ static int sabah_bridge_register_host(const sabah_bridge_tensor *src0) {
     } else if (hipMalloc(&dev, bytes) != hipSuccess) {
         snprintf(b->error, sizeof(b->error), "no device memory for a %zu-byte expert tensor", bytes);
         rc = -1;
-    } else if (hipMemcpy(dev, src0->data, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    } else if (hipMemcpyAsync(dev, src0->data, bytes, hipMemcpyHostToDevice, stream) != hipSuccess ||
+               hipStreamSynchronize(stream) != hipSuccess) {
         snprintf(b->error, sizeof(b->error), "copying a %zu-byte expert tensor to the device failed", bytes);
         (void)hipFree(dev);
         rc = -1;
@@ -176,7 +181,7 @@ static int sabah_bridge_mul_mat_id(const sabah_bridge_tensor *src0, const sabah_
         sabah_bridge_fail("unsupported MUL_MAT_ID layout", 0);
         return -1;
     }
-    if (src0->is_host && sabah_bridge_register_host(src0) != 0) return -1;
+    if (src0->is_host && sabah_bridge_register_host(src0, stream) != 0) return -1;
     const int rc = b->mul_mat_id(src0->data, src0->nb[2], src0->nb[1],
                                  src1->data, src1->nb[1], (int)src1->ne[1], src1->nb[2],
                                  ids->data, ids->nb[0], ids->nb[1], (int)ids->ne[0], (int)ids->ne[1],

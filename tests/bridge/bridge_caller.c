@@ -162,9 +162,13 @@ int main(int argc, char **argv) {
         hipMalloc(&dids, ids_bytes) != hipSuccess || hipMalloc(&d21, dst_bytes) != hipSuccess ||
         hipMalloc(&d20, dst_bytes) != hipSuccess)
         return fail_json("device buffers");
-    if (hipMemcpy(dx, hx, x_bytes, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(dids, hids, ids_bytes, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemset(d21, 0xFF, dst_bytes) != hipSuccess || hipMemset(d20, 0xFF, dst_bytes) != hipSuccess)
+    /* Inputs and the NaN fill of the outputs go on the call's stream, which is
+     * non-blocking: work on the null stream would not be ordered before the
+     * calls' kernels. */
+    if (hipMemcpyAsync(dx, hx, x_bytes, hipMemcpyHostToDevice, stream) != hipSuccess ||
+        hipMemcpyAsync(dids, hids, ids_bytes, hipMemcpyHostToDevice, stream) != hipSuccess ||
+        hipMemsetAsync(d21, 0xFF, dst_bytes, stream) != hipSuccess ||
+        hipMemsetAsync(d20, 0xFF, dst_bytes, stream) != hipSuccess || hipStreamSynchronize(stream) != hipSuccess)
         return fail_json("device uploads");
 
     sabah_bridge_tensor src0, src1, ids, dst21, dst20;
@@ -186,14 +190,16 @@ int main(int argc, char **argv) {
     }
     if (hipStreamSynchronize(stream) != hipSuccess) return fail_json("stream sync");
     float *h21 = (float *)malloc(dst_bytes), *h20 = (float *)malloc(dst_bytes), *hagain = (float *)malloc(dst_bytes);
-    if (!h21 || !h20 || !hagain || hipMemcpy(h21, d21, dst_bytes, hipMemcpyDeviceToHost) != hipSuccess ||
-        hipMemcpy(h20, d20, dst_bytes, hipMemcpyDeviceToHost) != hipSuccess)
+    if (!h21 || !h20 || !hagain || hipMemcpyAsync(h21, d21, dst_bytes, hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipMemcpyAsync(h20, d20, dst_bytes, hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess)
         return fail_json("downloads");
 
     /* the same op again (the next token's graph): no second upload */
-    if (hipMemset(d21, 0xFF, dst_bytes) != hipSuccess) return fail_json("memset");
+    if (hipMemsetAsync(d21, 0xFF, dst_bytes, stream) != hipSuccess) return fail_json("memset");
     if (sabah_bridge_mul_mat_id(&src0, &src1, &ids, &dst21, stream) != 0) return fail_json("repeated call");
-    if (hipStreamSynchronize(stream) != hipSuccess || hipMemcpy(hagain, d21, dst_bytes, hipMemcpyDeviceToHost) != hipSuccess)
+    if (hipMemcpyAsync(hagain, d21, dst_bytes, hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess)
         return fail_json("repeated call download");
 
     /* a layout the bridge refuses: f16 activations */

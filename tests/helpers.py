@@ -35,6 +35,23 @@ def assert_parity(y, r, what=""):
     return mr, c
 
 
+def assert_bits_equal(got, want, what=""):
+    """Bitwise equality of two float arrays; on failure the message gives the
+    number of differing 32-bit words, the first positions, and how many of
+    them are 0xFFFFFFFF (an output fill that was not overwritten, or that
+    landed after the kernel's store)."""
+    g = np.ascontiguousarray(got).view(np.uint32)
+    w = np.ascontiguousarray(want).view(np.uint32)
+    assert g.shape == w.shape, "%s: shapes %s vs %s" % (what, g.shape, w.shape)
+    bad = np.flatnonzero(g.reshape(-1) != w.reshape(-1))
+    if bad.size:
+        gf, wf = g.reshape(-1), w.reshape(-1)
+        first = [(tuple(int(i) for i in np.unravel_index(j, g.shape)), "%08x" % gf[j], "%08x" % wf[j])
+                 for j in bad[:8]]
+        raise AssertionError("%s: %d of %d words differ (%d of them 0xffffffff in got, %d in want); first %s" % (
+            what, bad.size, g.size, int((gf[bad] == 0xFFFFFFFF).sum()), int((wf[bad] == 0xFFFFFFFF).sum()), first))
+
+
 def f16(x: float) -> bytes:
     return np.array([x], np.float16).tobytes()
 

@@ -14,7 +14,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from helpers import assert_parity, random_blocks
+from helpers import assert_bits_equal, assert_parity, random_blocks
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CALLER = os.path.join(ROOT, "tests", "bridge", "bridge_caller")
@@ -104,9 +104,9 @@ def test_bridge_caller_matches_the_oracle(tmp_path, orc, qt, k, rows, E, n_ids, 
                            for n in ("dst21.f32", "dst20.f32", "dst21_again.f32"))
     assert_parity(got21, want, "bridge qt=%d" % qt)
     if qt in BIT_EXACT:
-        assert np.array_equal(got21.view(np.uint32), want.view(np.uint32))
-    assert np.array_equal(got20.view(np.uint32), got21.view(np.uint32))      # 20-argument caller
-    assert np.array_equal(again.view(np.uint32), got21.view(np.uint32))      # repeated op
+        assert_bits_equal(got21, want, "bridge qt=%d against the oracle" % qt)
+    assert_bits_equal(got20, got21, "20-argument caller")
+    assert_bits_equal(again, got21, "repeated op")
     # one upload, on the first call, of a host expert tensor; none of a device one
     assert r["banks_after_first"] == r["banks"] == (0 if on_device else 1)
     assert r["uploaded_bytes"] == (0 if on_device else raw.nbytes)
