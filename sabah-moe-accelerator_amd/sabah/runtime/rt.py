@@ -45,8 +45,6 @@ def library_path() -> str:
     return os.environ.get("SABAH_RT_LIB") or os.path.join(CSRC, "libsabah_rt.so")
 
 
-_lib = None
-
 c_vp, c_sz, c_i, c_u64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_ulonglong
 
 
@@ -133,64 +131,79 @@ def kernel_timing(kind: str, reset: bool = False) -> tuple[float, int]:
     return ms.value, n.value
 
 
+class _Handle:
+    """The library, opened on first use and bound to SIGNATURES then.
+
+    There is exactly one handle per process: every module goes through
+    `lib()`, so argument types are set once and a missing build surfaces as
+    RuntimeUnavailable at the first call that needs the GPU path (never as a
+    silent fallback)."""
+
+    cdll = None
+
+    @classmethod
+    def open(cls):
+        if cls.cdll is None:
+            path = library_path()
+            if not os.path.isfile(path):
+                raise RuntimeUnavailable(
+                    "%s does not exist; build the HIP library first "
+                    "(__graft_entry__.build(), or make -C %s)" % (path, CSRC))
+            try:
+                handle = ctypes.CDLL(path)
+            except OSError as exc:
+                raise RuntimeUnavailable("%s did not load: %s" % (path, exc)) from exc
+            for name, (argtypes, restype) in {**SIGNATURES, **EXTRA_SIGNATURES}.items():
+                entry = getattr(handle, name)
+                entry.argtypes, entry.restype = argtypes, restype
+            cls.cdll = handle
+        return cls.cdll
+
+
 def lib():
-    """Load the runtime library once, with an actionable error if it is absent."""
-    global _lib
-    if _lib is not None:
-        return _lib
-    p = library_path()
-    if not os.path.exists(p):
-        raise RuntimeUnavailable(
-            "Sabah HIP runtime not built: %s\nBuild it with:\n"
-            "    python -c 'import __graft_entry__ as g; g.build()'   (or: make -C %s)" % (p, CSRC))
-    try:
-        L = ctypes.CDLL(p)
-    except OSError as e:
-        raise RuntimeUnavailable("could not load %s: %s" % (p, e))
-    for table in (SIGNATURES, EXTRA_SIGNATURES):
-        for name, (argt, rest) in table.items():
-            fn = getattr(L, name)
-            fn.argtypes = argt
-            fn.restype = rest
-    _lib = L
-    return _lib
+    """The bound libsabah_rt.so (raises RuntimeUnavailable when it cannot be opened)."""
+    return _Handle.open()
 
 
 def last_error() -> str:
-    try:
-        return (lib().sabah_rt_last_error() or b"").decode("utf-8", "replace")
-    except Exception:
+    """The library's message for its most recent failure ("" when there is none
+    or the library is not loaded)."""
+    if _Handle.cdll is None:
         return ""
+    raw = _Handle.cdll.sabah_rt_last_error()
+    return raw.decode("utf-8", "replace") if raw else ""
 
 
 def check(rc, what="runtime call"):
-    if rc is None or (isinstance(rc, int) and rc != 0):
-        raise SabahRuntimeError("%s failed: %s" % (what, last_error()))
-    return rc
+    """Pass a 0 return code through; turn anything else (-1, or None from a
+    missing return) into SabahRuntimeError carrying the library's message."""
+    if rc == 0:
+        return rc
+    raise SabahRuntimeError("%s returned %r: %s" % (what, rc, last_error() or "no message from the library"))
 
 
 def row_bytes(qt: int, n: int) -> int:
-    """Bytes occupied by one row of n elements at quant type qt."""
-    be, bb = QBLOCK[qt]
-    if n % be:
-        raise ValueError("row of %d elements is not a whole number of %s blocks"
-                         % (n, QTYPE_NAME.get(qt, qt)))
-    return n // be * bb
+    """GGUF bytes of one row of n elements of type qt; n must fill whole blocks."""
+    elems, nbytes = QBLOCK[qt]
+    blocks, rest = divmod(n, elems)
+    if rest:
+        raise ValueError("%d elements leave %d over a whole number of %d-element %s blocks"
+                         % (n, rest, elems, QTYPE_NAME.get(qt, str(qt))))
+    return blocks * nbytes
 
 
 def available() -> bool:
+    """True when the HIP library can be opened (a GPU is not required)."""
     try:
-        lib()
-        return True
+        _Handle.open()
     except RuntimeUnavailable:
         return False
+    return True
 
 
 def device_count() -> int:
-    try:
-        return int(lib().sabah_rt_device_count())
-    except RuntimeUnavailable:
-        return 0
+    """GPUs the library sees (0 without the library or without a GPU)."""
+    return int(_Handle.open().sabah_rt_device_count()) if available() else 0
 
 
 _initialised = None
