@@ -12,9 +12,9 @@
 // Workgroups are dispatched in id order, so every gate/up workgroup has been
 // dispatched before any down workgroup: a down workgroup waits only for
 // workgroups that are running or done, and gate/up workgroups wait for
-// nothing.  Every wait is also bounded in time (kLayerWaitTicks): one that
-// runs out poisons its rows, sets the sticky error word to 2 and ends, so
-// every wave of the grid exits.
+// nothing.  Every wait is also bounded (kLayerIdleTicks without progress):
+// one that runs out poisons its rows, sets the sticky error word to 2 and
+// ends, so every wave of the grid exits.
 //
 // The h handoff, per workgroup and without shared counters:
 //   gate/up: h rows stored write-through to memory (agent-scope stores), the
@@ -23,18 +23,30 @@
 //     the codebook table built, the weights loaded and staged in LDS,
 //     and each lane's half unit decoded to int8 in registers, all while
 //     gate/up runs; then wave 0 waits for the flags, h is read with ordinary
-//     loads, quantised, and dotted with the decoded weights.  Down
-//     workgroups 0-7 (one per XCD) poll the n_g flags with agent-scope loads
-//     (16 bytes per lane per poll) and then store their XCD's flag (agent
-//     scope), which the XCD's other down workgroups poll, one word each, so
-//     the gate/up workgroups' stores do not queue behind 256 pollers of the
-//     same lines.  The XCD is the hardware's XCC_ID register; an XCD without
-//     a polling workgroup would leave its other workgroups to their bounded
-//     wait.  An XCD's L2 and
-//     a CU's L1 start each launch without lines of h (kernel-boundary
-//     coherence of device memory), and no workgroup reads h before the flags,
-//     so the first read of a line on an XCD fetches it from memory and the
-//     XCD's other down workgroups hit the line in L2.
+//     loads, quantised, and dotted with the decoded weights.  One down
+//     workgroup per XCD (its leader) polls the n_g flags with agent-scope
+//     loads (16 bytes per lane per poll) and then stores its XCD's flag,
+//     which the XCD's other down workgroups poll, one word each, so the
+//     gate/up workgroups' stores do not queue behind 256 pollers of the same
+//     lines.  The XCD is the hardware's XCC_ID register.  The leader is
+//     elected on the device: each down workgroup, on arrival, swaps this
+//     launch's number into its XCD's ticket, and the one that gets back a
+//     different number (the previous launch's) leads.  So every XCD that runs
+//     a down workgroup has exactly one leader, wherever the dispatcher
+//     places the workgroups (all on one XCD, some XCDs without any).  An
+//     XCD's L2 and a CU's L1 start each launch without lines of h
+//     (kernel-boundary coherence of device memory), and no workgroup reads
+//     h before the flags, so the first read of a line on an XCD fetches it
+//     from memory and the XCD's other down workgroups hit the line in L2.
+// Forward progress needs no co-residency: down workgroups wait only for
+// gate/up workgroups, which were all dispatched before the first down
+// workgroup and wait for nothing; a follower waits only for its XCD's leader,
+// which is already running (it took the ticket).  The waits are bounded by
+// time without progress, not by total time: a leader's clock restarts
+// whenever more gate/up flags are set, and a follower's whenever its leader
+// reports a higher count, so a layer that is slowed (time-sliced with other
+// work, CUs held by another stream's kernel) still completes; only a wait
+// that sees no progress for kLayerIdleTicks gives up.
 // Flags never go back to zero: every entry of sync (kSyncG flags, then
 // kSyncD down counters) advances by one per launch.  A workgroup reads its
 // own entry at start (the number of launches so far, n) and waits for or
@@ -47,15 +59,22 @@ namespace sabah {
 
 // Layout in 32-bit words: kSyncG gate/up flags (dense, polled 16 bytes per
 // lane), kSyncD down counters (each read and written only by its owner, at
-// its start and end), kSyncXcds per-XCD flags (one 128-byte line each,
-// written as a whole line).  (Gate/up flags one per line, written whole,
-// measured slower: the pollers then read 240 lines per poll.)
+// its start and end), kSyncXcds per-XCD flags (one 128-byte line each:
+// word 0 the launch number once the XCD's leader saw every gate/up flag,
+// word 1 the count of flags the leader has seen so far), kSyncXcds per-XCD
+// leader tickets (one line each, touched only by the XCD's own workgroups).
+// (Gate/up flags one per line, written whole, measured slower: the pollers
+// then read 240 lines per poll.)
 constexpr int kLine = 32;                               // words per 128-byte line
 constexpr int kSyncG = 1024, kSyncD = 1024, kSyncXcds = 8;
 constexpr int kSyncDOff = kSyncG;
 constexpr int kSyncX = kSyncDOff + kSyncD;              // first per-XCD flag (line aligned)
-constexpr int kSyncWords = kSyncX + kSyncXcds * kLine;
-constexpr unsigned long long kLayerWaitTicks = 200000;   // 2 ms of s_memrealtime (100 MHz)
+constexpr int kSyncT = kSyncX + kSyncXcds * kLine;      // first per-XCD leader ticket
+constexpr int kSyncWords = kSyncT + kSyncXcds * kLine;
+// A wait gives up after this long without progress: 50 ms of s_memrealtime
+// (100 MHz).  It guards against a hang, not against a slow layer (one layer
+// takes about 12 us).
+constexpr unsigned long long kLayerIdleTicks = 5000000;
 constexpr unsigned kErrLayerWait = 2u;                  // sticky error word: a down workgroup's wait ran out
 constexpr int kLayerThreads = 512;
 
@@ -68,6 +87,12 @@ struct LayerArgs {
     uint32_t wait_skew;         // 0; a test of the timeout path sets 1: the down workgroups wait for a
                                 // flag value no gate/up workgroup writes, so their bounded wait runs out
     uint32_t d_delay;           // s_memrealtime ticks (10 ns) the down workgroups wait before their loads
+    uint32_t idle_ticks;        // kLayerIdleTicks; the timeout test shortens it
+    int xcd_groups;             // 0: down workgroups grouped by their hardware XCD; g > 0 (a placement
+                                // test): grouped as if down workgroup j ran on XCD j % g, so every
+                                // grouping the dispatcher could produce (all on one XCD, XCDs left
+                                // empty) can be exercised; the XCD flag is then stored at agent scope,
+                                // since a group's members sit on different XCDs
 };
 
 // LDS of the fused kernel: the down role's static layout (IQ3_S table, tile
@@ -89,48 +114,71 @@ __device__ inline unsigned xcc_id() {
     return v & (unsigned)(kSyncXcds - 1);
 }
 
-// Wave 0 waits until the word at p holds `target` (agent-scope loads)
-__device__ inline bool wait_word(const uint32_t* p, uint32_t target) {
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p), (short)0, 4, 0x00020000);
-    const unsigned long long t0 = wall_ticks();
+// Wave 0 of a follower waits until word 0 of its XCD's flag line holds
+// `target` (agent-scope loads of words 0 and 1).  The clock restarts whenever
+// word 1, the leader's count of flags seen, changes.
+__device__ inline bool wait_line(const uint32_t* line, uint32_t target, unsigned long long idle) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(line), (short)0, 8, 0x00020000);
+    unsigned long long t0 = wall_ticks();
+    uint32_t seen = ~0u;
     for (;;) {
-        const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 16));
-        if (v == target) return true;
-        if (wall_ticks() - t0 > kLayerWaitTicks) return false;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, 0, 0, 16);
+        const uint32_t flag = (uint32_t)__builtin_amdgcn_readfirstlane((int)v[0]);
+        const uint32_t count = (uint32_t)__builtin_amdgcn_readfirstlane((int)v[1]);
+        if (flag == target) return true;
+        const unsigned long long now = wall_ticks();
+        if (count != seen) {
+            seen = count;
+            t0 = now;
+        } else if (now - t0 > idle) {
+            return false;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
 }
 
-// Wave 0 waits until the gate/up flags [0, n) all hold `target`; true when
-// they do, false when the wait ran out.  Lane l reads flags l, l + 64, ...
-// (one agent-scope dword load per flag line per poll).
-// Wave 0 waits until the gate/up flags [0, n) all hold `target`; true when
-// they do, false when the wait ran out.  One 16-byte agent-scope load per
-// lane per poll covers 256 flags (loads past n return 0 and are masked).
-__device__ inline bool wait_flags(const uint32_t* sync, int n, uint32_t target) {
+// Wave 0 of a leader waits until the gate/up flags [0, n) all hold `target`;
+// true when they do, false when a wait saw no new flag for `idle` ticks.  One
+// 16-byte agent-scope load per lane per poll covers 256 flags (loads past n
+// return 0 and are masked).  Whenever the number of set flags rises, the
+// clock restarts and lane 0 stores the number in word 1 of `line`, the
+// followers' progress word.
+__device__ inline bool wait_flags(const uint32_t* sync, int n, uint32_t target, uint32_t* line,
+                                  unsigned long long idle) {
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(sync), (short)0, n * 4, 0x00020000);
     const int lane = (int)(threadIdx.x & 63u);
-    const unsigned long long t0 = wall_ticks();
+    unsigned long long t0 = wall_ticks();
+    int best = -1;
     for (;;) {
-        bool mine = true;
+        int set = 0;
         for (int base = 0; base < n; base += 256) {
             const int f = base + 4 * lane;
             if (f < n) {
                 const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, f * 4, 0, 16);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    if (f + j < n && v[j] != target) mine = false;
+                    if (f + j < n && v[j] == target) ++set;
             }
         }
-        if (__all(mine)) return true;
-        if (wall_ticks() - t0 > kLayerWaitTicks) return false;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) set += __shfl_xor(set, m);
+        set = __builtin_amdgcn_readfirstlane(set);
+        if (set == n) return true;
+        const unsigned long long now = wall_ticks();
+        if (set > best) {
+            best = set;
+            t0 = now;
+            if (lane == 0) __hip_atomic_store(line + 1, (uint32_t)set, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (now - t0 > idle) {
+            return false;
+        }
         __builtin_amdgcn_s_sleep(2);
     }
 }
 
 // a whole 128-byte flag line set to v by the first 32 lanes of wave 0 (one
 // ordinary store instruction).  The line stays in this XCD's L2, and the
-// XCD's agent-scope polls (wait_word) see it there at once: an agent-scope
+// XCD's agent-scope polls (wait_line) see it there at once: an agent-scope
 // load returns a line its L2 holds modified (measured on MI355X: a plain
 // store seen by the sc1 polls of every CU of its XCD before the store's own
 // completion returned to the writer, and by no CU of another XCD).
@@ -161,6 +209,12 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     const int dj = b - a.n_g;
     uint32_t* my = a.sync + kSyncDOff + dj;
     const uint32_t target = *my + 1u;
+    // this workgroup's XCD, and its leader ticket taken at once (the returned
+    // value is first needed at the wait, after the weights are staged)
+    const unsigned x = a.xcd_groups ? (unsigned)(dj % a.xcd_groups) : xcc_id();
+    uint32_t ticket = target;
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_exchange(a.sync + kSyncT + kLine * x, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (dj == 0) {                                          // advance the entries no workgroup of this launch owns
         for (int i = a.n_g + (int)threadIdx.x; i < kSyncG; i += NT) a.sync[i] = target;
         for (int i = a.n_d + (int)threadIdx.x; i < kSyncD; i += NT) a.sync[kSyncDOff + i] = target;
@@ -221,16 +275,19 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     }
     __shared__ int ok;
     if (threadIdx.x < 64) {
-        const unsigned x = xcc_id();
         uint32_t* xf = a.sync + kSyncX + kLine * x;
         bool done;
-        if (dj < kSyncXcds || a.n_d <= kSyncXcds) {
-            done = wait_flags(a.sync, a.n_g, target + a.wait_skew);
+        if ((uint32_t)__builtin_amdgcn_readfirstlane((int)ticket) != target) {   // this XCD's leader
+            done = wait_flags(a.sync, a.n_g, target + a.wait_skew, xf, a.idle_ticks);
             if (done) {
-                store_flag_line(xf, target);
+                if (a.xcd_groups) {
+                    if (threadIdx.x == 0) __hip_atomic_store(xf, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    store_flag_line(xf, target);
+                }
             }
         } else {
-            done = wait_word(xf, target + a.wait_skew);
+            done = wait_line(xf, target + a.wait_skew, a.idle_ticks);
         }
         if (threadIdx.x == 0) ok = done ? 1 : 0;
     }

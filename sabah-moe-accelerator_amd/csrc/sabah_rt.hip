@@ -82,8 +82,11 @@ struct EvPair {
     hipEvent_t a, b;
     int kind;
 };
-bool g_timing = false;
-bool g_launch_plain = false;   // set during sabah_moe_layer_noalloc: no timing events are created
+std::atomic<bool> g_timing{false};
+// set by the calling thread during sabah_moe_layer_noalloc: its launches create no timing events
+thread_local bool g_launch_plain = false;
+// the timing events' pools (launches from several threads)
+std::mutex g_ev_mu;
 std::vector<EvPair> g_ev_free, g_ev_pending;
 double g_kind_ms[KK_COUNT] = {0};
 unsigned long long g_kind_launches[KK_COUNT] = {0};
@@ -93,7 +96,8 @@ unsigned long long g_kind_launches[KK_COUNT] = {0};
 // kernel's execution on its stream and nothing else.
 template <typename K, typename... A>
 void launch_kernel(int kind, K kernel, dim3 grid, dim3 block, int lds, hipStream_t st, A... args) {
-    if (g_timing && !g_launch_plain) {
+    if (g_timing.load() && !g_launch_plain) {
+        std::lock_guard<std::mutex> lk(g_ev_mu);
         if (g_ev_free.empty()) {
             EvPair p{};
             if (hipEventCreate(&p.a) == hipSuccess && hipEventCreate(&p.b) == hipSuccess) g_ev_free.push_back(p);
@@ -177,9 +181,12 @@ uint32_t* g_layer_sync[kMaxDevices] = {};
 // measured 1,510 GB/s against 1,433 - 1,449 (same box, interleaved runs).
 std::atomic<int> g_layer_fusion{1};
 // set when a fused launch's wait ran out: the next fused launch first clears the flags
-bool g_sync_reset_pending = false;
+std::atomic<bool> g_sync_reset_pending{false};
 // one-shot test of the timeout path (sabah_rt_set_layer_fusion(2))
-bool g_layer_wait_test = false;
+std::atomic<bool> g_layer_wait_test{false};
+// placement test of the fused layer (sabah_rt_set_layer_placement_test): 0, or
+// g > 0 to group down workgroup j with XCD j % g instead of its hardware XCD
+std::atomic<int> g_layer_xcd_groups{0};
 
 // LDS a workgroup may allocate (the device's limit: 160 KB on gfx950)
 int g_max_lds = 65536;
@@ -507,13 +514,23 @@ SABAH_API int sabah_rt_set_kernel_timing(int on) {
 // bit-identical.
 // 2: as 1, and the next fused launch tests its timeout path: its down
 // workgroups wait for a flag value that no workgroup writes, so their
-// bounded wait runs out (2 ms), their rows become NaN and the next call
+// wait runs out (2 ms without progress), their rows become NaN and the next call
 // fails with the message; the flags are then cleared before the next fused
 // launch.
 SABAH_API int sabah_rt_set_layer_fusion(int mode) {
     if (mode < 0 || mode > 2) return fail("layer fusion mode %d outside {0 off, 1 on, 2 on + timeout test}", mode);
     g_layer_fusion.store(mode == 0 ? 0 : 1);
-    g_layer_wait_test = mode == 2;
+    g_layer_wait_test.store(mode == 2);
+    return 0;
+}
+
+// Placement test of the fused layer: with groups g in 1..8 its down
+// workgroups elect one leader per group as if down workgroup j ran on XCD
+// j % g (g = 1: all on one XCD; g = 3: five XCDs without any), instead of per
+// hardware XCD; 0 restores the hardware grouping.  The results do not change.
+SABAH_API int sabah_rt_set_layer_placement_test(int groups) {
+    if (groups < 0 || groups > kSyncXcds) return fail("layer placement test groups %d outside [0, %d]", groups, kSyncXcds);
+    g_layer_xcd_groups.store(groups);
     return 0;
 }
 
@@ -682,6 +699,7 @@ SABAH_API void sabah_slab_destroy(void) { slab_release(); }
 // launches still in flight.  reset != 0 clears the totals after reading.
 SABAH_API int sabah_rt_get_kernel_timing(int kind, double* total_ms, unsigned long long* launches, int reset) {
     if (kind < 0 || kind >= KK_COUNT) return fail("unknown kernel kind %d", kind);
+    std::lock_guard<std::mutex> lk(g_ev_mu);
     for (EvPair& p : g_ev_pending) {
         float ms = 0.0f;
         if (!ck(hipEventSynchronize(p.b), "timing event sync")) return -1;
@@ -1283,12 +1301,11 @@ static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, cons
     if (StaticLds<QT>::BYTES + dyn + 64 > g_max_lds) return 0;
     if (!ck(fit_lds(k_layer_decode<kLayerThreads>, dyn, StaticLds<QT>::BYTES + dyn), "fused layer LDS")) return -1;
     uint32_t* sync = g_layer_sync[g_device];
-    if (g_sync_reset_pending) {
-        launch_kernel(KK_LAYER, k_clear_sync, dim3(1), dim3(256), 0, st, sync);
-        g_sync_reset_pending = false;
-    }
-    LayerArgs a{gu, dn, n_g, g_tiles, n_d, sync, g_layer_wait_test ? 1u : 0u, layer_down_delay(n_used, D, F)};
-    g_layer_wait_test = false;
+    if (g_sync_reset_pending.exchange(false)) launch_kernel(KK_LAYER, k_clear_sync, dim3(1), dim3(256), 0, st, sync);
+    const bool wait_test = g_layer_wait_test.exchange(false);
+    // the timeout test gives up after 2 ms without progress rather than 50
+    LayerArgs a{gu, dn, n_g, g_tiles, n_d, sync, wait_test ? 1u : 0u, layer_down_delay(n_used, D, F),
+                wait_test ? 200000u : (uint32_t)kLayerIdleTicks, g_layer_xcd_groups.load()};
     launch_kernel(KK_LAYER, k_layer_decode<kLayerThreads>, dim3((unsigned)(n_g + n_d)), dim3(kLayerThreads), dyn, st, a);
     return ck(hipGetLastError(), "fused layer launch") ? 1 : -1;
 }

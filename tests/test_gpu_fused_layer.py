@@ -183,6 +183,45 @@ def test_fused_chain_graph_replays_match_eager(hip_rt, orc, fusion):
         assert torch.equal(xp, xe), "two-kernel chain, replay %d" % rep
 
 
+@pytest.mark.parametrize("groups", [1, 3, 8])
+def test_fused_layer_under_forced_down_workgroup_placements(hip_rt, orc, fusion, groups):
+    """The down workgroups grouped as if placed j % groups (1: every one on a
+    single XCD, so one leader for all; 3: five XCDs without any): one leader
+    per group is elected on the device, and the layer stays bit-identical to
+    the two-kernel form and the oracle, across consecutive launches."""
+    from sabah.runtime import routing
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(300 + groups)
+    E, D, F, K = 24, 2048, 768, 10
+    bank, raws = make_bank(orc, rng, E, D, F)
+    ids, w = routing.zipf_routing(rng, 1, E, K)
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    ex = MoEExecutor(bank, max_used=K)
+    xd, idd, wd = T(x), T(ids), T(w)
+    lib = hip_rt.lib()
+    hip_rt.check(lib.sabah_rt_set_layer_placement_test(groups), "placement test")
+    try:
+        fused, plain, n = run_both(hip_rt, fusion, lambda: ex.run_layer(0, xd, idd, wd).cpu().numpy())
+        fusion(1)
+        again = [ex.run_layer(0, xd, idd, wd).cpu().numpy() for _ in range(3)]
+    finally:
+        hip_rt.check(lib.sabah_rt_set_layer_placement_test(0), "placement test")
+    assert n == 1
+    assert lib.sabah_rt_check_errors() == 0, hip_rt.last_error()
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    for a in again:
+        assert np.array_equal(a.view(np.uint32), fused.view(np.uint32))
+    want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], (IQ3_S,) * 3, x, ids, w)
+    assert np.array_equal(fused.view(np.uint32), want.view(np.uint32))
+
+
+def test_layer_placement_test_groups_are_validated(hip_rt):
+    lib = hip_rt.lib()
+    assert lib.sabah_rt_set_layer_placement_test(9) == -1
+    assert lib.sabah_rt_set_layer_placement_test(-1) == -1
+    assert lib.sabah_rt_set_layer_placement_test(0) == 0
+
+
 def test_fused_layer_bad_id_poisons_and_fails_the_next_call(hip_rt, orc, fusion):
     from sabah.runtime import routing
     from sabah.runtime.executor import MoEExecutor
@@ -207,7 +246,8 @@ def test_fused_layer_bad_id_poisons_and_fails_the_next_call(hip_rt, orc, fusion)
 
 def test_fused_layer_timeout_path_reports_and_recovers(hip_rt, orc, fusion):
     """Forced from the host (mode 2): the down workgroups of one launch wait
-    for a flag value that is never written; their 2 ms bounded wait runs out,
+    for a flag value that is never written; their wait sees no progress for
+    2 ms (the test's bound) and runs out,
     every wave exits, their rows are NaN, the next call fails naming the wait,
     and the launches after it are correct again."""
     from sabah.runtime import routing
