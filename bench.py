@@ -417,6 +417,8 @@ def bench_batch(args, W):
         torch.cuda.synchronize()
         parity = {"grouped_equals_token_major": bool(torch.equal(outs[0], outs[1]))}
         ms_token_major = timed(run_token_major, max(1, steps // 4)) / max(1, steps // 4)
+    elif not mmid and not args.no_cpu:
+        parity = batch_parity(W, bank, shared, ex, ids_np, w_np, x_np, dev)
     L = rt.lib()
     L.sabah_rt_set_kernel_timing(1)
     for kind in rt.KERNEL_KINDS:
@@ -480,6 +482,35 @@ def bench_batch(args, W):
     print(json.dumps(line), flush=True)
     copy_probe(args, dev)
     return 0
+
+
+def batch_parity(W, bank, shared, ex, ids_np, w_np, x_np, dev, n=8):
+    """The token-major layer on the GPU against the oracle's layer (ggml's CPU
+    MUL_MAT_ID path with the shared expert), on the first n tokens of the
+    first routing, with the routed and shared experts read back from HBM."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    e_ids = ids_np[0, :n]
+    used = np.unique(e_ids)
+    remap = {int(e): i for i, e in enumerate(used)}
+    sub = {r: np.stack([bank.read_expert(0, r, int(e)) for e in used]) for r in ("gate", "up", "down")}
+    lid = np.vectorize(remap.get)(e_ids).astype(np.int32)
+    sh = None
+    if shared is not None:
+        sh = (shared.read("gate"), shared.read("up"), shared.read("down"), (shared.qt,) * 3,
+              None if shared.gate_inp is None else shared.gate_inp.cpu().numpy())
+    x = np.ascontiguousarray(x_np[:n])
+    got = ex.run_layer(0, torch.from_numpy(x).to(dev), torch.from_numpy(np.ascontiguousarray(e_ids)).to(dev),
+                       torch.from_numpy(np.ascontiguousarray(w_np[0, :n])).to(dev)).cpu().numpy()
+    ref = O.moe_layer(sub["gate"], sub["up"], sub["down"], (W.qt_gate, W.qt_up, W.qt_down), x, lid,
+                      w_np[0, :n], shared=sh)
+    d = (got.astype(np.float64) - ref).ravel()
+    r = ref.astype(np.float64).ravel()
+    return {"tokens": n, "max_rel": float(np.abs(d).max() / np.abs(r).max()),
+            "cos": float((got.ravel() @ r) / np.sqrt((got.ravel() @ got.ravel()) * (r @ r))),
+            "tolerance": {"max_rel": 1e-3, "cos": 0.99999}}
 
 
 def cpu_batch_baseline(args, W, bank, ids_np, w_np, x_np, mmid=False):

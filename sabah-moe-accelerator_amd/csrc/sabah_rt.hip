@@ -19,6 +19,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "dense_kernels.h"
 #include "layer_kernels.h"
 #include "mmid_kernels.h"
 #include "prefill_kernels.h"
@@ -45,6 +46,14 @@ std::mutex g_mu;
 int g_device = -1;
 hipStream_t g_stream = nullptr;
 hipStream_t g_copy = nullptr;     // the harness's copy stream (sabah_h2d_async, sabah_event_record_copy)
+// A batch layer's shared expert runs on g_side, forked from the caller's
+// stream at the layer's start (g_ev_fork) and joined before the launch that
+// adds its output (g_ev_join), so it overlaps the routed gate/up.  The fork,
+// the shared launches and the join's wait are issued under g_side_mu, so
+// layers issued from several threads do not interleave their event records.
+hipStream_t g_side = nullptr;
+hipEvent_t g_ev_fork = nullptr, g_ev_join = nullptr;
+std::mutex g_side_mu;
 unsigned int* g_err_host = nullptr;   // host-mapped sticky error word
 unsigned int* g_err_dev = nullptr;    // its device address
 
@@ -68,6 +77,8 @@ struct Scratch {
     size_t bytes = 0;
 };
 Scratch g_scratch_h, g_scratch_hs, g_scratch_ys, g_scratch_hq;
+// the shared expert over several tokens: x and h quantised once, the gate logits
+Scratch g_scratch_sxq, g_scratch_shq, g_scratch_sgl;
 // grouped (prefill) layer: offsets, pair maps, q8 rows of x and h, h and y in group order
 Scratch g_scratch_goff, g_scratch_gpair, g_scratch_gxq, g_scratch_gh, g_scratch_ghq, g_scratch_gy;
 uint16_t* g_nearest_dev = nullptr;   // IQ3_S encoder table, uploaded on first use
@@ -445,6 +456,10 @@ SABAH_API int sabah_rt_init(int device) {
     g_max_lds = lds;
     if (!ck(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "create stream")) return -1;
     if (!ck(hipStreamCreateWithFlags(&g_copy, hipStreamNonBlocking), "create copy stream")) return -1;
+    if (!ck(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "create shared-expert stream") ||
+        !ck(hipEventCreateWithFlags(&g_ev_fork, hipEventDisableTiming), "create fork event") ||
+        !ck(hipEventCreateWithFlags(&g_ev_join, hipEventDisableTiming), "create join event"))
+        return -1;
     if (!ck(hipHostMalloc(reinterpret_cast<void**>(&g_err_host), sizeof(unsigned int), hipHostMallocMapped),
             "sticky error word")) return -1;
     *g_err_host = 0;
@@ -468,8 +483,9 @@ SABAH_API int sabah_rt_init(int device) {
 SABAH_API int sabah_rt_shutdown(void) {
     if (g_device < 0) return 0;
     if (g_stream) (void)hipStreamSynchronize(g_stream);
-    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys, &g_scratch_hq, &g_scratch_goff, &g_scratch_gpair, &g_scratch_gxq,
-                       &g_scratch_gh, &g_scratch_ghq, &g_scratch_gy}) {
+    for (Scratch* s : {&g_scratch_h, &g_scratch_hs, &g_scratch_ys, &g_scratch_hq, &g_scratch_sxq, &g_scratch_shq,
+                       &g_scratch_sgl, &g_scratch_goff, &g_scratch_gpair, &g_scratch_gxq, &g_scratch_gh, &g_scratch_ghq,
+                       &g_scratch_gy}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->bytes = 0;
@@ -486,6 +502,11 @@ SABAH_API int sabah_rt_shutdown(void) {
     g_stream = nullptr;
     if (g_copy) (void)hipStreamDestroy(g_copy);
     g_copy = nullptr;
+    if (g_side) (void)hipStreamSynchronize(g_side), (void)hipStreamDestroy(g_side);
+    g_side = nullptr;
+    if (g_ev_fork) (void)hipEventDestroy(g_ev_fork);
+    if (g_ev_join) (void)hipEventDestroy(g_ev_join);
+    g_ev_fork = g_ev_join = nullptr;
     slab_release();
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -1095,7 +1116,7 @@ SABAH_API int sabah_quantize_act(const float* d_x, void* d_y, int qt, int n_rows
 // out; hq (or null) receives h quantised once per (token, slot) row
 static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D, const Routing& rt, int n_slots,
                      int d_model, int d_ff, int n_tokens, const float* w, const float* shared, const float* resid,
-                     float* out, int accumulate, uint8_t* hq, hipStream_t st) {
+                     float* out, int accumulate, uint8_t* hq, hipStream_t st, hipEvent_t join = nullptr) {
     if (!ck(dispatch_gate_up(qtg, gu, n_tokens, st), "gate/up launch")) return -1;
     DownArgs a{};
     a.D = D;
@@ -1120,6 +1141,7 @@ static int run_layer(const GateUpArgs& gu, int qtg, int qtd, const ExpertSrc& D,
         if (!ck(hipGetLastError(), "h quantisation launch")) return -1;
         a.hq = hq;
     }
+    if (join && !ck(hipStreamWaitEvent(st, join, 0), "join the shared expert")) return -1;
     return ck(dispatch_down(qtd, a, n_tokens, st), "down/combine launch") ? 0 : -1;
 }
 
@@ -1167,6 +1189,8 @@ SABAH_API int sabah_moe_block(const float* d_x, float* d_out, float* d_h, const 
 struct LayerBufs {
     float *h = nullptr, *hs = nullptr, *ys = nullptr;
     uint8_t* hq = nullptr;
+    uint8_t *sxq = nullptr, *shq = nullptr;   // the shared expert's quantised x and h (several tokens)
+    float* sgl = nullptr;                     // its gate logits
 };
 struct Workspace {
     uint8_t* arena = nullptr;
@@ -1179,6 +1203,17 @@ struct Workspace {
         return arena + off;
     }
 };
+// The shared expert over at least this many tokens reads each weight row once
+// per launch (k_dense_tokens) instead of once per token.
+constexpr int kDenseMinTokens = 4;
+constexpr int kDenseMaxTB = 32;                 // tokens per workgroup
+// quantised activation row stride: the ActLayout, then 16 bytes, so the
+// same offset of consecutive tokens' rows falls on different LDS banks
+static int dense_act_stride(int qt, int k) { return align16i((int)ActLayout(k, act_type(qt)).bytes) + 16; }
+static bool shared_dense(const sabah_moe_layer_desc* L, int n_tokens) {
+    return L->shared_gate && n_tokens >= kDenseMinTokens && L->qt_shared_gate == L->qt_shared_up &&
+           L->d_model % 256 == 0 && L->d_ff_shared % 256 == 0;
+}
 static size_t layer_hq_bytes(const sabah_moe_layer_desc* L, int n_used, int n_tokens) {
     if (!layer_quantises_h_once(L->qt_down, L->d_ff, n_used, n_tokens)) return 0;
     return (size_t)down_hq_row_bytes(L->qt_down, L->d_ff) * n_tokens * n_used;
@@ -1192,6 +1227,11 @@ static size_t layer_scratch_bytes(const sabah_moe_layer_desc* L, int n_used, int
         take(sizeof(float) * (size_t)n_tokens * L->d_ff_shared);
         take(sizeof(float) * (size_t)n_tokens * L->d_model);
     }
+    if (shared_dense(L, n_tokens)) {
+        take((size_t)n_tokens * dense_act_stride(L->qt_shared_gate, L->d_model));
+        take((size_t)n_tokens * dense_act_stride(L->qt_shared_down, L->d_ff_shared));
+        take(sizeof(float) * (size_t)n_tokens);
+    }
     take(sizeof(float) * (size_t)n_tokens * n_used * L->d_ff);
     if (const size_t hq = layer_hq_bytes(L, n_used, n_tokens)) take(hq);
     return used;
@@ -1202,6 +1242,14 @@ static int layer_bufs(const sabah_moe_layer_desc* L, int n_used, int n_tokens, W
         b.hs = static_cast<float*>(ws.get(g_scratch_hs, sizeof(float) * (size_t)n_tokens * L->d_ff_shared, st));
         b.ys = static_cast<float*>(ws.get(g_scratch_ys, sizeof(float) * (size_t)n_tokens * L->d_model, st));
         if (!b.hs || !b.ys) return -1;
+    }
+    if (shared_dense(L, n_tokens)) {
+        b.sxq = static_cast<uint8_t*>(
+            ws.get(g_scratch_sxq, (size_t)n_tokens * dense_act_stride(L->qt_shared_gate, L->d_model), st));
+        b.shq = static_cast<uint8_t*>(
+            ws.get(g_scratch_shq, (size_t)n_tokens * dense_act_stride(L->qt_shared_down, L->d_ff_shared), st));
+        b.sgl = static_cast<float*>(ws.get(g_scratch_sgl, sizeof(float) * (size_t)n_tokens, st));
+        if (!b.sxq || !b.shq || !b.sgl) return -1;
     }
     b.h = static_cast<float*>(ws.get(g_scratch_h, sizeof(float) * (size_t)n_tokens * n_used * L->d_ff, st));
     if (!b.h) return -1;
@@ -1214,9 +1262,98 @@ static int layer_bufs(const sabah_moe_layer_desc* L, int n_used, int n_tokens, W
 
 // dense shared expert of a layer: gate/up + SwiGLU -> hs, down -> ys (added
 // by the routed combine); nothing when the layer has none
+template <int QT, int NMAT>
+hipError_t launch_dense(const DenseArgs& a, int kind, hipStream_t st) {
+    const int dyn = dense_dyn_lds(a.TB, a.act_stride, NMAT, a.R);
+    if (const hipError_t e = fit_lds(k_dense_tokens<QT, NMAT>, dyn, StaticLds<QT>::BYTES + dyn)) return e;
+    const dim3 grid((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)((a.n_tokens + a.TB - 1) / a.TB));
+    launch_kernel(kind, k_dense_tokens<QT, NMAT>, grid, dim3(kThreads), dyn, st, a);
+    return hipGetLastError();
+}
+template <int NMAT>
+hipError_t dispatch_dense(int qt, const DenseArgs& a, int kind, hipStream_t st) {
+    switch (qt) {
+    case QT_Q8_0: return launch_dense<QT_Q8_0, NMAT>(a, kind, st);
+    case QT_Q4_K: return launch_dense<QT_Q4_K, NMAT>(a, kind, st);
+    case QT_Q6_K: return launch_dense<QT_Q6_K, NMAT>(a, kind, st);
+    case QT_IQ3_S: return launch_dense<QT_IQ3_S, NMAT>(a, kind, st);
+    case QT_IQ3_XXS: return launch_dense<QT_IQ3_XXS, NMAT>(a, kind, st);
+    case QT_IQ4_NL: return launch_dense<QT_IQ4_NL, NMAT>(a, kind, st);
+    case QT_Q2_0: return launch_dense<QT_Q2_0, NMAT>(a, kind, st);
+    case QT_IQ4_XS: return launch_dense<QT_IQ4_XS, NMAT>(a, kind, st);
+    case QT_IQ2_S: return launch_dense<QT_IQ2_S, NMAT>(a, kind, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+// Tokens and rows per workgroup of a dense launch: up to kDenseMaxTB tokens,
+// one thread per (token, matrix, row), the tiles staged in one pass, the
+// activation rows within kDenseActLoads loads per thread and the LDS limit.
+static bool dense_shape(int qt, int k, int n_mat, int n_tokens, int act_stride, int& R, int& TB) {
+    const int rmax = std::max(1, (16 * tile_chunk_cap(qt, n_mat) - 30) / (int)row_bytes(qt, k));
+    for (TB = std::min(n_tokens, kDenseMaxTB); TB >= 1; TB = TB > 1 ? (TB + 1) / 2 : 0) {
+        R = std::min(rmax, kThreads / (TB * n_mat));
+        if (R < 1) continue;
+        const int lds = table_bytes(qt) + 4 * kMaxTiles + 2 * kStageGuard + kStageBytes +
+                        dense_dyn_lds(TB, act_stride, n_mat, R) + 64;
+        if (TB * act_stride <= 16 * kThreads * kDenseActLoads && lds <= g_max_lds) return true;
+        if (TB == 1) break;
+    }
+    return false;
+}
+
+// The shared expert over n_tokens >= kDenseMinTokens: x quantised once, gate/up
+// + SwiGLU with every weight row read once per kDenseMaxTB tokens (and the gate
+// logits), h quantised once, down scaled by the gate.  The same values as the
+// token-major launches, bit for bit.
+static int shared_expert_dense(const sabah_moe_layer_desc* L, const float* d_x, int n_tokens, float* hs, float* ys,
+                               uint8_t* sxq, uint8_t* shq, float* sgl, hipStream_t st) {
+    const int D = L->d_model, Fs = L->d_ff_shared;
+    const int qg = L->qt_shared_gate, qd = L->qt_shared_down;
+    DenseArgs g{};
+    g.act_stride = dense_act_stride(qg, D);
+    DenseArgs d{};
+    d.act_stride = dense_act_stride(qd, Fs);
+    if (!dense_shape(qg, D, 2, n_tokens, g.act_stride, g.R, g.TB) ||
+        !dense_shape(qd, Fs, 1, n_tokens, d.act_stride, d.R, d.TB))
+        return 1;                                            // the token-major launches then
+    const size_t xrows = (size_t)n_tokens * (D / 256);
+    launch_kernel(KK_GATE_UP, k_quant_rows, dim3((unsigned)((xrows + 15) / 16)), dim3(kThreads), 0, st, d_x,
+                  n_tokens, D, act_type(qg), sxq, g.act_stride, (const int*)nullptr, 1, (const int*)nullptr, 0);
+    g.w0 = static_cast<const uint8_t*>(L->shared_gate);
+    g.w1 = static_cast<const uint8_t*>(L->shared_up);
+    g.xq = sxq;
+    g.n_tokens = n_tokens;
+    g.k = D;
+    g.rows = Fs;
+    g.out = hs;
+    g.sg_w = L->shared_gate_inp;
+    g.sg_x = d_x;
+    g.sg_n = D;
+    g.sg_logit = sgl;
+    if (!ck(dispatch_dense<2>(qg, g, KK_GATE_UP, st), "shared gate/up launch")) return -1;
+    const size_t hrows = (size_t)n_tokens * (Fs / 256);
+    launch_kernel(KK_MMID, k_quant_rows, dim3((unsigned)((hrows + 15) / 16)), dim3(kThreads), 0, st,
+                  (const float*)hs, n_tokens, Fs, act_type(qd), shq, d.act_stride, (const int*)nullptr, 1,
+                  (const int*)nullptr, 0);
+    d.w0 = static_cast<const uint8_t*>(L->shared_down);
+    d.w1 = nullptr;
+    d.xq = shq;
+    d.n_tokens = n_tokens;
+    d.k = Fs;
+    d.rows = D;
+    d.out = ys;
+    d.sg_logit = L->shared_gate_inp ? sgl : nullptr;
+    return ck(dispatch_dense<1>(qd, d, KK_MMID, st), "shared down launch") ? 0 : -1;
+}
+
 static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_tokens, float* hs, float* ys,
-                         hipStream_t st) {
+                         hipStream_t st, uint8_t* sxq = nullptr, uint8_t* shq = nullptr, float* sgl = nullptr) {
     if (!L->shared_gate) return 0;
+    if (sxq && shared_dense(L, n_tokens)) {
+        const int rc = shared_expert_dense(L, d_x, n_tokens, hs, ys, sxq, shq, sgl, st);
+        if (rc <= 0) return rc;
+    }
     const int D = L->d_model;
     const int Fs = L->d_ff_shared;
     GateUpArgs gs{};
@@ -1310,12 +1447,35 @@ static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, cons
     return ck(hipGetLastError(), "fused layer launch") ? 1 : -1;
 }
 
+// The batched shared expert on g_side: the fork (an event of the caller's
+// stream the side stream waits for), its launches, and the join event
+// recorded after them.  Called with g_side_mu held.
+static int shared_expert_forked(const sabah_moe_layer_desc* L, const float* d_x, int n_tokens, float* hs, float* ys,
+                                uint8_t* sxq, uint8_t* shq, float* sgl, hipStream_t st) {
+    if (!ck(hipEventRecord(g_ev_fork, st), "fork the shared expert") ||
+        !ck(hipStreamWaitEvent(g_side, g_ev_fork, 0), "fork the shared expert"))
+        return -1;
+    if (shared_expert(L, d_x, n_tokens, hs, ys, g_side, sxq, shq, sgl)) return -1;
+    return ck(hipEventRecord(g_ev_join, g_side), "join the shared expert") ? 0 : -1;
+}
+// the batches whose shared expert overlaps the routed experts (the batched
+// shared expert's own launches then run beside the routed gate/up)
+static bool shared_overlaps(const sabah_moe_layer_desc* L, int n_tokens) { return g_side && shared_dense(L, n_tokens); }
+
 static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const int32_t* d_ids, const float* d_w,
                         int n_used, int n_tokens, float* d_out, const float* d_resid, Workspace& ws, hipStream_t st) {
     const int D = L->d_model, F = L->d_ff;
     LayerBufs b;
     if (layer_bufs(L, n_used, n_tokens, ws, st, b)) return -1;
-    if (shared_expert(L, d_x, n_tokens, b.hs, b.ys, st)) return -1;
+    std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
+    hipEvent_t join = nullptr;
+    if (shared_overlaps(L, n_tokens)) {
+        side_lock.lock();
+        if (shared_expert_forked(L, d_x, n_tokens, b.hs, b.ys, b.sxq, b.shq, b.sgl, st)) return -1;
+        join = g_ev_join;
+    } else if (shared_expert(L, d_x, n_tokens, b.hs, b.ys, st, b.sxq, b.shq, b.sgl)) {
+        return -1;
+    }
     const Routing rt{reinterpret_cast<const uint8_t*>(d_ids), 4, (size_t)n_used * 4, L->n_experts};
     GateUpArgs gu{};
     gu.G = {reinterpret_cast<const uint8_t*>(L->gate), nullptr, row_bytes(L->qt_gate, D) * (size_t)F};
@@ -1334,7 +1494,7 @@ static int moe_layer_on(const sabah_moe_layer_desc* L, const float* d_x, const i
         if (f) return f > 0 ? 0 : -1;
     }
     return run_layer(gu, L->qt_gate, L->qt_down, DS, rt, n_used, D, F, n_tokens, d_w, b.ys, d_resid, d_out, 0, b.hq,
-                     st);
+                     st, join);
 }
 
 static int check_layer_desc(const sabah_moe_layer_desc* L) {
@@ -1444,13 +1604,30 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     float* y = static_cast<float*>(grow_scratch(g_scratch_gy, sizeof(float) * P * D, st));
     if (!off || !pair_of || !xq || !h || !hq || !y) return -1;
     int* pos_of = pair_of + P;
-    float *hs = nullptr, *shared = nullptr;
+    float *hs = nullptr, *shared = nullptr, *sgl = nullptr;
+    uint8_t *sxq = nullptr, *shq = nullptr;
     if (L->shared_gate) {
         hs = static_cast<float*>(grow_scratch(g_scratch_hs, sizeof(float) * (size_t)n_tokens * L->d_ff_shared, st));
         shared = static_cast<float*>(grow_scratch(g_scratch_ys, sizeof(float) * (size_t)n_tokens * D, st));
         if (!hs || !shared) return -1;
     }
-    if (shared_expert(L, d_x, n_tokens, hs, shared, st)) return -1;
+    if (shared_dense(L, n_tokens)) {
+        sxq = static_cast<uint8_t*>(
+            grow_scratch(g_scratch_sxq, (size_t)n_tokens * dense_act_stride(L->qt_shared_gate, D), st));
+        shq = static_cast<uint8_t*>(
+            grow_scratch(g_scratch_shq, (size_t)n_tokens * dense_act_stride(L->qt_shared_down, L->d_ff_shared), st));
+        sgl = static_cast<float*>(grow_scratch(g_scratch_sgl, sizeof(float) * (size_t)n_tokens, st));
+        if (!sxq || !shq || !sgl) return -1;
+    }
+    std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
+    hipEvent_t join = nullptr;
+    if (shared_overlaps(L, n_tokens)) {
+        side_lock.lock();
+        if (shared_expert_forked(L, d_x, n_tokens, hs, shared, sxq, shq, sgl, st)) return -1;
+        join = g_ev_join;
+    } else if (shared_expert(L, d_x, n_tokens, hs, shared, st, sxq, shq, sgl)) {
+        return -1;
+    }
 
     GroupArgs ga{d_ids, n_tokens, n_used, E, off, pair_of, pos_of, g_err_dev, nullptr, 0, 0, 0};
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(kGroupThreads), sizeof(int) * (2 * E + kGroupThreads), st, ga);
@@ -1484,6 +1661,7 @@ static int moe_prefill_on(const sabah_moe_layer_desc* L, const float* d_x, const
     dn.d_model = D;
     dn.d_ff = F;
     launch_grouped_down<false>(L->qt_down, KK_GDOWN, D, E, st, dn);
+    if (join && !ck(hipStreamWaitEvent(st, join, 0), "join the shared expert")) return -1;
     CombineArgs cb{y, pos_of, d_w, shared, d_resid, d_out, n_used, D};
     const bool v4 = D % 4 == 0 && ((reinterpret_cast<uintptr_t>(d_out) | reinterpret_cast<uintptr_t>(d_resid) |
                                     reinterpret_cast<uintptr_t>(shared)) & 15) == 0;

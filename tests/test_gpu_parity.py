@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_parity, random_blocks, unfused_rounding_row
+from helpers import assert_parity, random_blocks, unfused_rounding_row, assert_bits_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -434,6 +434,96 @@ def test_moe_layer_with_a_sigmoid_gated_shared_expert(hip_rt, orc):
         assert np.array_equal(ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()[t], ungated[t])
         shared.set_gate(-1e4 * x[t])
         assert np.array_equal(ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()[t], routed[t])
+
+
+def _dense_shared_case(orc, rng, qt_routed, qt_shared, E, D, F, Fs, K):
+    from sabah.runtime.bank import DenseExpert
+    bank, raws = make_bank(orc, rng, (qt_routed,) * 3, E, D, F)
+    shared = DenseExpert(D, Fs, qt_shared, device="cuda:0")
+    sh_raw = {}
+    for role, (rows, cols) in {"gate": (Fs, D), "up": (Fs, D), "down": (D, Fs)}.items():
+        sh_raw[role] = orc.quantize_weights(qt_shared, (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+        shared.load(role, sh_raw[role])
+    return bank, raws, shared, sh_raw
+
+
+def test_shared_expert_over_a_batch_is_bit_exact_with_the_oracle(hip_rt, orc):
+    """At four tokens and more the shared expert reads each weight row once
+    per launch for all tokens (k_dense_tokens); with Q8_0 throughout the
+    layer is bit-exact with the oracle."""
+    from sabah.runtime import routing
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(6061)
+    E, D, F, Fs, K, Tn = 16, 1024, 512, 768, 4, 6
+    bank, raws, shared, sh_raw = _dense_shared_case(orc, rng, Q8_0, Q8_0, E, D, F, Fs, K)
+    ids, w = routing.uniform_routing(rng, Tn, E, K)
+    x = rng.standard_normal((Tn, D)).astype(np.float32)
+    got = MoEExecutor(bank, max_used=K, shared=shared).run_layer(0, T(x), T(ids), T(w)).cpu().numpy()
+    want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], (Q8_0,) * 3, x, ids, w,
+                         shared=(sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3))
+    assert_bits_equal(got, want, "Q8_0 layer with a shared expert over 6 tokens")
+
+
+@pytest.mark.parametrize("qt_shared,Tn,gated", [(Q8_0, 7, True), (Q4_K, 40, True), (IQ3_S, 5, False)])
+def test_shared_expert_over_a_batch_equals_one_token_calls(hip_rt, orc, qt_shared, Tn, gated):
+    """The batched shared expert (x and h quantised once, each weight row read
+    once per 32 tokens, the gate logits computed in the gate/up launch) gives
+    every token the bits of a one-token call of the same layer (the per-token
+    launches), with and without the sigmoid gate; 40 tokens take two token
+    groups."""
+    from sabah.runtime import routing
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(6062 + Tn)
+    E, D, F, Fs, K = 16, 1024, 512, 512, 4
+    bank, raws, shared, _ = _dense_shared_case(orc, rng, Q8_0, qt_shared, E, D, F, Fs, K)
+    if gated:
+        shared.set_gate((rng.standard_normal(D) * 0.05).astype(np.float32))
+    ids, w = routing.uniform_routing(rng, Tn, E, K)
+    x = rng.standard_normal((Tn, D)).astype(np.float32)
+    ex = MoEExecutor(bank, max_used=K, shared=shared)
+    batch = ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()
+    for t in range(Tn):
+        one = ex.run_layer(0, T(x[t:t + 1]), T(ids[t:t + 1]), T(w[t:t + 1])).cpu().numpy()
+        assert_bits_equal(batch[t:t + 1], one, "token %d of %d" % (t, Tn))
+
+
+def test_batched_shared_expert_on_its_side_stream_in_a_graph(hip_rt, orc):
+    """The batched shared expert runs on the library's side stream, forked
+    from the caller's stream and joined before the routed combine.  Captured
+    in a HIP graph (the fork and join become graph edges) and replayed with
+    new inputs, eager layers in between: every replay equals the eager layer,
+    and the eager layer equals the oracle."""
+    from sabah.runtime import routing
+    from sabah.runtime.executor import MoEExecutor
+    rng = np.random.default_rng(6071)
+    E, D, F, Fs, K, Tn = 16, 1024, 512, 512, 4, 8
+    bank, raws, shared, sh_raw = _dense_shared_case(orc, rng, Q8_0, Q8_0, E, D, F, Fs, K)
+    shared.set_gate((rng.standard_normal(D) * 0.05).astype(np.float32))
+    ex = MoEExecutor(bank, max_used=K, shared=shared)
+    xs = torch.zeros(Tn, D, dtype=torch.float32, device=DEV)
+    ids_s = torch.zeros(Tn, K, dtype=torch.int32, device=DEV)
+    w_s = torch.zeros(Tn, K, dtype=torch.float32, device=DEV)
+    out = torch.zeros(Tn, D, dtype=torch.float32, device=DEV)
+    ex.run_layer(0, xs, ids_s, w_s, out=out)                # sizes the library scratch
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ex.run_layer(0, xs, ids_s, w_s, out=out)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
+        x = rng.standard_normal((Tn, D)).astype(np.float32)
+        eager = ex.run_layer(0, T(x), T(ids), T(w)).cpu().numpy()
+        xs.copy_(T(x))
+        ids_s.copy_(T(ids))
+        w_s.copy_(T(w))
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bits_equal(out.cpu().numpy(), eager, "replay %d" % rep)
+        want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], (Q8_0,) * 3, x, ids, w,
+                             shared=(sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3,
+                                     shared.gate_inp.cpu().numpy()))
+        assert_parity(eager, want, "gated shared expert, replay %d" % rep)
 
 
 @pytest.mark.parametrize("D,F", [(512, 544), (1024, 800)])
