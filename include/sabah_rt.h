@@ -48,8 +48,9 @@ int sabah_rt_device_count(void);
 
 /* ggml MUL_MAT_ID on the HBM-resident expert bank:
  *   dst[t][i][0..rows) = W[ids[t][i]] . x[t][i % x_rows]
- * with x quantised to q8 exactly as ggml's CPU path does (q8_0 for Q8_0 and
- * IQ4_NL weights, q8_K for Q4_K / Q6_K / IQ3_S / IQ3_XXS / IQ2_S / IQ4_XS).  Same 21
+ * with x quantised to q8 exactly as ggml's CPU path does (q8_0 for Q8_0, IQ4_NL
+ * and Q2_0 weights, q8_1 for Q5_1, q8_K for Q4_K / Q5_K / Q6_K / IQ3_S /
+ * IQ3_XXS / IQ2_S / IQ4_XS).  Same 21
  * arguments, order and
  * meaning as sabah_rt_mul_mat_id_v2 (sabah_rt.cu:3494-3515; bridge call
  * 0001 patch:193-200):
@@ -64,8 +65,9 @@ int sabah_rt_device_count(void);
  *   d_dst         dst->data f32, rows contiguous; dst_id_stride = nb[1],
  *                 dst_token_stride = nb[2]
  *   rows, k, n_experts, qt   src0->ne[1], ne[0], ne[2], ggml_type
- *                 (8 Q8_0, 12 Q4_K, 14 Q6_K, 18 IQ3_XXS, 20 IQ4_NL, 21 IQ3_S,
- *                 22 IQ2_S, 23 IQ4_XS; k % block size == 0)
+ *                 (7 Q5_1, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K, 18 IQ3_XXS,
+ *                 20 IQ4_NL, 21 IQ3_S, 22 IQ2_S, 23 IQ4_XS, 42 Q2_0;
+ *                 k % block size == 0)
  *   stream        hipStream_t the kernel is enqueued on (NULL: the null stream)
  *   ids_key       accepted and ignored: ids are read on the device, never
  *                 downloaded, so there is nothing to reuse.  Callers passing

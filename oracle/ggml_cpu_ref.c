@@ -1,13 +1,14 @@
 /*
  * ORACLE - test infrastructure only (see ggml_cpu_ref.h).
  *
- * Restatement of ggml's portable CPU path for MUL_MAT_ID on Q8_0 / Q4_K /
- * Q6_K / IQ3_S expert weights.  ggml (llama.cpp @ 96ffdc41) is a third-party
+ * Restatement of ggml's portable CPU path for MUL_MAT_ID on Q8_0 / Q5_1 /
+ * Q4_K / Q5_K / Q6_K / IQ3_S (and the other IQ) expert weights.  ggml (llama.cpp @ 96ffdc41) is a third-party
  * dependency that the reference does not vendor; the algorithm followed here
  * is its published generic C form:
- *   quantize_row_q8_0_ref, quantize_row_q8_K_ref        (activation quantisers)
+ *   quantize_row_q8_0_ref, quantize_row_q8_1_ref, quantize_row_q8_K_ref
+ *                                                        (activation quantisers)
  *   dequantize_row_{q8_0,q4_K,q6_K,iq3_s}                (format readers)
- *   ggml_vec_dot_{q8_0_q8_0,q4_K_q8_K,q6_K_q8_K,iq3_s_q8_K}_generic
+ *   ggml_vec_dot_{q8_0_q8_0,q5_1_q8_1,q4_K_q8_K,q5_K_q8_K,q6_K_q8_K,iq3_s_q8_K}_generic
  *   ggml_compute_forward_mul_mat_id                      (slot i reads row i % ne11)
  * anchored on the reference's own readers of the same formats
  * (sabah_rt.cu:2233-2423; gguf-py quants.py:412-435, 509-556, 586-606,
@@ -29,8 +30,8 @@
 
 int orc_block_elems(int qt) {
     switch (qt) {
-    case ORC_Q8_0: case ORC_IQ4_NL: return 32;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS:
+    case ORC_Q8_0: case ORC_Q8_1: case ORC_Q5_1: case ORC_IQ4_NL: return 32;
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_Q8_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS:
     case ORC_IQ2_S: return 256;
     case ORC_Q2_0: return 64;
     }
@@ -40,6 +41,9 @@ int orc_block_elems(int qt) {
 int orc_block_bytes(int qt) {
     switch (qt) {
     case ORC_Q8_0: return 34;    /* fp16 d + 32 x int8                       */
+    case ORC_Q8_1: return 36;    /* fp16 d, fp16 s = d * sum(q), 32 x int8   */
+    case ORC_Q5_1: return 24;    /* fp16 d, fp16 m, u32 qh, 16 B nibbles     */
+    case ORC_Q5_K: return 176;   /* d, dmin, 12 B scales/mins, qh[32], qs[128] */
     case ORC_Q4_K: return 144;   /* d, dmin, 12 B scales/mins, 128 B nibbles */
     case ORC_Q6_K: return 210;   /* ql[128], qh[64], int8 sc[16], fp16 d      */
     case ORC_Q8_K: return 292;   /* float d, int8 qs[256], int16 bsums[16]    */
@@ -62,7 +66,8 @@ size_t orc_row_bytes(int qt, int n) {
 int orc_vec_dot_type(int qt) {
     switch (qt) {
     case ORC_Q8_0: case ORC_IQ4_NL: case ORC_Q2_0: return ORC_Q8_0;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: case ORC_IQ2_S:
+    case ORC_Q5_1: return ORC_Q8_1;
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ4_XS: case ORC_IQ2_S:
         return ORC_Q8_K;
     }
     return -1;
@@ -146,6 +151,30 @@ void orc_quantize_q8_0(const float *x, uint8_t *y, int k) {
     }
 }
 
+/* quantize_row_q8_1_ref: the q8_0 steps (d = amax/127 stored fp16, q =
+ * roundf(x * (1/d)) with the fp32 d), plus s = fp16((float)sum(q) * d), the
+ * fp32 d again (ggml-quants.c; the vec_dot_type of Q5_1, sabah_rt.cu's Q5_1
+ * readers at 2241-2252 and 2522-2541 take the same block). */
+void orc_quantize_q8_1(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 32; ++b, x += 32, y += 36) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = fabsf(x[j]);
+            amax = amax > v ? amax : v;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        st_f16(y, d);
+        int sum = 0;
+        for (int j = 0; j < 32; ++j) {
+            const int q = (int)roundf(x[j] * id);
+            y[4 + j] = (uint8_t)(int8_t)q;
+            sum += q;
+        }
+        st_f16(y + 2, (float)sum * d);
+    }
+}
+
 /* quantize_row_q8_K_ref: the signed value of largest magnitude (first one on
  * ties) sets iscale = -127/max; q = min(127, nearest-even(iscale*x)); d = 1/iscale
  * kept in fp32; bsums[j] = sum of q over elements 16j..16j+15.  opcheck.py:73-80
@@ -183,6 +212,7 @@ int orc_quantize_act(int qt, const float *x, uint8_t *y, int k) {
     const int vt = orc_vec_dot_type(qt);
     if (vt < 0 || k % orc_block_elems(vt)) return -1;
     if (vt == ORC_Q8_0) orc_quantize_q8_0(x, y, k);
+    else if (vt == ORC_Q8_1) orc_quantize_q8_1(x, y, k);
     else orc_quantize_q8_K(x, y, k);
     return 0;
 }
@@ -224,6 +254,40 @@ int orc_dequantize_row(int qt, const uint8_t *x, float *y, int k) {
                 const float d2 = d * (float)s1, n2 = dmin * (float)m1;
                 for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] & 0xF) - n1;
                 for (int l = 0; l < 32; ++l) *y++ = d2 * (float)(q[l] >> 4) - n2;
+            }
+        }
+        return 0;
+    case ORC_Q5_1:
+        /* element j (j < 16) = (qs[j] & 15) | bit j of qh << 4, element j + 16 =
+         * (qs[j] >> 4) | bit j + 16 of qh << 4; value = d * q + m
+         * (sabah_rt.cu:2241-2252, quants.py:390-409) */
+        for (int b = 0; b < k / 32; ++b, x += 24, y += 32) {
+            const float d = ld_f16(x), m = ld_f16(x + 2);
+            const uint32_t qh = (uint32_t)x[4] | ((uint32_t)x[5] << 8) | ((uint32_t)x[6] << 16) | ((uint32_t)x[7] << 24);
+            const uint8_t *qs = x + 8;
+            for (int j = 0; j < 16; ++j) {
+                const int q0 = (qs[j] & 0xF) | (int)(((qh >> j) & 1u) << 4);
+                const int q1 = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+                y[j] = (float)q0 * d + m;
+                y[j + 16] = (float)q1 * d + m;
+            }
+        }
+        return 0;
+    case ORC_Q5_K:
+        /* sub-block j, element l: nibble (low for even j) of qs[32 (j / 2) + l]
+         * plus 16 when bit j of qh[l] is set; value = d * sc_j * q - dmin * m_j
+         * (sabah_rt.cu:2271-2290, quants.py:559-583) */
+        for (int b = 0; b < k / 256; ++b, x += 176) {
+            const float d = ld_f16(x), dmin = ld_f16(x + 2);
+            const uint8_t *sc = x + 4, *qh = x + 16, *q = x + 48;
+            for (int c = 0; c < 4; ++c, q += 32) {
+                int s0, m0, s1, m1;
+                scale_min_k4(2 * c, sc, &s0, &m0);
+                scale_min_k4(2 * c + 1, sc, &s1, &m1);
+                const float d1 = d * (float)s0, n1 = dmin * (float)m0;
+                const float d2 = d * (float)s1, n2 = dmin * (float)m1;
+                for (int l = 0; l < 32; ++l) *y++ = d1 * (float)((q[l] & 0xF) + ((qh[l] >> (2 * c)) & 1) * 16) - n1;
+                for (int l = 0; l < 32; ++l) *y++ = d2 * (float)((q[l] >> 4) + ((qh[l] >> (2 * c + 1)) & 1) * 16) - n2;
             }
         }
         return 0;
@@ -373,6 +437,60 @@ static float dot_q4_K(const uint8_t *w, const uint8_t *a, int k) {
         const uint8_t *q = w + 16;
         for (int c = 0; c < 4; ++c, q += 32)
             for (int l = 0; l < 32; ++l) { v[64 * c + l] = (int8_t)(q[l] & 0xF); v[64 * c + 32 + l] = (int8_t)(q[l] >> 4); }
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) scale_min_k4(j, w + 4, &sc[j], &mn[j]);
+        int msum = 0;
+        for (int j = 0; j < 16; ++j) msum += q8K_bsum(a, j) * mn[j / 2];
+        const int8_t *q8 = q8K_qs(a);
+        int aux[8] = {0};
+        for (int j = 0; j < 8; ++j)
+            for (int m = 0; m < 4; ++m)
+                for (int l = 0; l < 8; ++l) {
+                    const int e = 32 * j + 8 * m + l;
+                    aux[l] += sc[j] * ((int)q8[e] * (int)v[e]);
+                }
+        const float d = ld_f16(w) * q8K_d(a);
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux[l];
+        const float dmin = ld_f16(w + 2) * q8K_d(a);
+        sumf -= dmin * (float)msum;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+/* ggml_vec_dot_q5_1_q8_1 (generic): per 32-block the exact int32 sum of
+ * q5 * q8, then sumf += (d_w * d_x) * sumi + m_w * s_x, blocks in order. */
+static float dot_q5_1(const uint8_t *w, const uint8_t *a, int k) {
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 32; ++b, w += 24, a += 36) {
+        const uint32_t qh = (uint32_t)w[4] | ((uint32_t)w[5] << 8) | ((uint32_t)w[6] << 16) | ((uint32_t)w[7] << 24);
+        const int8_t *q8 = (const int8_t *)(a + 4);
+        int sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < 16; ++j) {
+            const int x0 = (w[8 + j] & 0xF) | (int)(((qh >> j) & 1u) << 4);
+            const int x1 = (w[8 + j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+            sumi0 += x0 * q8[j];
+            sumi1 += x1 * q8[j + 16];
+        }
+        const int sumi = sumi0 + sumi1;
+        sumf += (ld_f16(w) * ld_f16(a)) * (float)sumi + ld_f16(w + 2) * ld_f16(a + 2);
+    }
+    return sumf;
+}
+
+/* ggml_vec_dot_q5_K_q8_K (generic): the q4_K lanes with each value's fifth
+ * bit (qh) added; the same eight int32 lanes, fp32 lane sums and min term. */
+static float dot_q5_K(const uint8_t *w, const uint8_t *a, int k) {
+    float sums[8] = {0};
+    float sumf = 0.0f;
+    for (int b = 0; b < k / 256; ++b, w += 176, a += 292) {
+        int8_t v[256];
+        const uint8_t *q = w + 48, *hm = w + 16;
+        for (int c = 0; c < 4; ++c, q += 32)
+            for (int l = 0; l < 32; ++l) {
+                v[64 * c + l] = (int8_t)((q[l] & 0xF) + ((hm[l] >> (2 * c)) & 1) * 16);
+                v[64 * c + 32 + l] = (int8_t)((q[l] >> 4) + ((hm[l] >> (2 * c + 1)) & 1) * 16);
+            }
         int sc[8], mn[8];
         for (int j = 0; j < 8; ++j) scale_min_k4(j, w + 4, &sc[j], &mn[j]);
         int msum = 0;
@@ -577,7 +695,9 @@ static float dot_iq4_xs(const uint8_t *w, const uint8_t *a, int k) {
 float orc_vec_dot(int qt, const uint8_t *w, const uint8_t *a, int k) {
     switch (qt) {
     case ORC_Q8_0: return dot_q8_0(w, a, k);
+    case ORC_Q5_1: return dot_q5_1(w, a, k);
     case ORC_Q4_K: return dot_q4_K(w, a, k);
+    case ORC_Q5_K: return dot_q5_K(w, a, k);
     case ORC_Q6_K: return dot_q6_K(w, a, k);
     case ORC_IQ3_S: return dot_iq3_s(w, a, k);
     case ORC_IQ3_XXS: return dot_iq3_xxs(w, a, k);
@@ -690,6 +810,68 @@ static void enc_q4_K(const float *x, uint8_t *y, int k) {
     }
 }
 
+/* Q5_1: per 32-block the range [min, max] in 31 steps (ggml's
+ * quantize_row_q5_1_ref steps: d = (max - min) / 31, m = min, q = x / d -
+ * m / d rounded half up, clamped to 31) */
+static void enc_q5_1(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 32; ++b, x += 32, y += 24) {
+        float lo = x[0], hi = x[0];
+        for (int j = 1; j < 32; ++j) { lo = fminf(lo, x[j]); hi = fmaxf(hi, x[j]); }
+        const float d = (hi - lo) / 31.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        st_f16(y, d);
+        st_f16(y + 2, lo);
+        uint32_t qh = 0;
+        for (int j = 0; j < 16; ++j) {
+            const int q0 = clampi((int)((x[j] - lo) * id + 0.5f), 0, 31);
+            const int q1 = clampi((int)((x[j + 16] - lo) * id + 0.5f), 0, 31);
+            y[8 + j] = (uint8_t)((q0 & 0xF) | ((q1 & 0xF) << 4));
+            qh |= ((uint32_t)(q0 >> 4) << j) | ((uint32_t)(q1 >> 4) << (j + 16));
+        }
+        memcpy(y + 4, &qh, 4);
+    }
+}
+
+/* Q5_K: enc_q4_K's scales and mins with 31 levels per sub-block and the fifth
+ * bit in qh (this project's encoder; any valid bytes serve the parity tests) */
+static void enc_q5_K(const float *x, uint8_t *y, int k) {
+    for (int b = 0; b < k / 256; ++b, x += 256, y += 176) {
+        memset(y, 0, 176);
+        float scl[8], mns[8], msc = 0.0f, mmn = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            float lo = 0.0f, hi = 0.0f;
+            for (int l = 0; l < 32; ++l) { lo = fminf(lo, x[32 * j + l]); hi = fmaxf(hi, x[32 * j + l]); }
+            scl[j] = (hi - lo) / 31.0f;
+            mns[j] = -lo;
+            msc = fmaxf(msc, scl[j]);
+            mmn = fmaxf(mmn, mns[j]);
+        }
+        st_f16(y, msc / 63.0f);
+        st_f16(y + 2, mmn / 63.0f);
+        const float df = ld_f16(y), dmf = ld_f16(y + 2);
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) {
+            sc[j] = df > 0.0f ? clampi((int)lrintf(scl[j] / df), 0, 63) : 0;
+            mn[j] = dmf > 0.0f ? clampi((int)lrintf(mns[j] / dmf), 0, 63) : 0;
+        }
+        uint8_t *p = y + 4;
+        for (int j = 0; j < 4; ++j) {
+            p[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+            p[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+            p[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+        }
+        uint8_t *qh = y + 16, *qs = y + 48;
+        for (int j = 0; j < 8; ++j) {
+            const float step = df * (float)sc[j], off = dmf * (float)mn[j];
+            for (int l = 0; l < 32; ++l) {
+                const int q = step > 0.0f ? clampi((int)lrintf((x[32 * j + l] + off) / step), 0, 31) : 0;
+                qs[32 * (j / 2) + l] |= (uint8_t)((q & 0xF) << (4 * (j & 1)));
+                qh[l] |= (uint8_t)((q >> 4) << j);
+            }
+        }
+    }
+}
+
 static void enc_q6_K(const float *x, uint8_t *y, int k) {
     for (int b = 0; b < k / 256; ++b, x += 256, y += 210) {
         memset(y, 0, 210);
@@ -797,6 +979,8 @@ int orc_quantize_weights(int qt, const float *x, uint8_t *y, int k) {
     switch (qt) {
     case ORC_Q8_0: orc_quantize_q8_0(x, y, k); return 0;
     case ORC_Q4_K: enc_q4_K(x, y, k); return 0;
+    case ORC_Q5_1: enc_q5_1(x, y, k); return 0;
+    case ORC_Q5_K: enc_q5_K(x, y, k); return 0;
     case ORC_Q6_K: enc_q6_K(x, y, k); return 0;
     case ORC_IQ3_S: enc_iq3_s(x, y, k); return 0;
     case ORC_IQ4_NL: enc_iq4_nl(x, y, k); return 0;

@@ -2,7 +2,8 @@
  * ORACLE - test infrastructure only.
  *
  * A plain-C restatement of ggml's CPU MUL_MAT_ID path for the eight expert
- * formats (Q8_0, Q4_K, Q6_K, IQ3_S, IQ3_XXS, IQ2_S, IQ4_NL, IQ4_XS), used as
+ * formats (Q8_0, Q5_1, Q4_K, Q5_K, Q6_K, IQ3_S, IQ3_XXS, IQ2_S, IQ4_NL, IQ4_XS,
+ * Q2_0), used as
  * the checker for the HIP kernels.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
  * it.  The product library never links or calls it.
@@ -19,9 +20,16 @@
  *     round-to-nearest-even conversion on random values and exact ties.
  *   orc_quantize_q8_0: hand-computed blocks; halves rounded away from zero
  *     (quants.py:413-427, np_roundf 44-48); the all-zero block.
+ *   orc_quantize_q8_1: the q8_0 bytes (same d and q) plus s = fp16(d * sum q),
+ *     hand-computed blocks and the all-zero block.
  *   orc_quantize_q8_K: hand-computed blocks; ties to even; the scale takes
  *     the sign of the first maximum; clamp at 127; zero block; bsums
  *     (tools/rc4/opcheck.py:73-80).
+ *   Q5_1 / Q5_K dequantisation: known-answer blocks (the fifth bit of
+ *     element i is bit i of qh for Q5_1, bit j of qh[l] for element l of
+ *     Q5_K sub-block j; d, m / dmin, 6-bit scales and mins) from
+ *     sabah_rt.cu:2241-2290 and quants.py:367-409, 559-583; Q5_K equals Q4_K
+ *     on the same scale and nibble bytes when qh is zero.
  *   orc_dequantize_row: known-answer blocks per format (d = 1, unit scales,
  *     codebook rows, sign / qh / scale bits) from the closed forms of
  *     sabah_rt.cu:2233-2423 and quants.py:412-435, 509-556, 586-606, 1091-1159.
@@ -36,7 +44,8 @@
  *     (grid row, sign bytes, 4-bit scale; grid index high bits from qh and
  *     the two scale nibbles; level bytes and d; 6-bit sub-block scales) from
  *     sabah_rt.cu:2293-2344, 2380-2409 and quants.py:935-1075, 1364-1411.
- *   orc_vec_dot: the float64 dot of the decoded operands (all formats); the
+ *   orc_vec_dot: the float64 dot of the decoded operands (all formats; for
+ *     Q5_1 the q8_1 s term equals d_x times the block's q sum); the
  *     IQ3_S integer block sums exactly; IQ3_XXS exactly a quarter and IQ2_S
  *     exactly an eighth of their integer sums; the Q4_K min term through
  *     bsums.
@@ -45,9 +54,9 @@
  *     expert is added last; duplicate ids of the reference's recorded routing
  *     trace give identical slot outputs.
  *   orc_quantize_weights: round trip (its output only has to be valid input).
- * Parity unpinned: the fp32 accumulation order inside orc_vec_dot for Q4_K
- * and Q6_K (ggml's generic eight-lane order, restated from its published
- * source, which cannot be built or run here).  Checks against those two use
+ * Parity unpinned: the fp32 accumulation order inside orc_vec_dot for Q4_K,
+ * Q5_K and Q6_K (ggml's generic eight-lane order, restated from its published
+ * source, which cannot be built or run here).  Checks against those three use
  * the floating-point tolerance, not bit equality.  The other formats sum one
  * fp32 term per block (per 32-element sub-block for IQ4_XS) serially in block
  * order, the HIP kernels do the same, and their outputs are compared bit for
@@ -64,8 +73,11 @@ extern "C" {
 /* ggml_type codes (sabah/runtime/rt.py:20-23 uses the same enum values). */
 enum {
     ORC_F32 = 0,
+    ORC_Q5_1 = 7,
     ORC_Q8_0 = 8,
+    ORC_Q8_1 = 9,
     ORC_Q4_K = 12,
+    ORC_Q5_K = 13,
     ORC_Q6_K = 14,
     ORC_Q8_K = 15,
     ORC_IQ3_XXS = 18,
@@ -88,8 +100,10 @@ int orc_vec_dot_type(int qt);
 float orc_fp16_to_fp32(uint16_t h);
 uint16_t orc_fp32_to_fp16(float f);
 
-/* Activation quantisers (ggml quantize_row_q8_0_ref / quantize_row_q8_K_ref). */
+/* Activation quantisers (ggml quantize_row_q8_0_ref / quantize_row_q8_1_ref /
+ * quantize_row_q8_K_ref). */
 void orc_quantize_q8_0(const float *x, uint8_t *y, int k);
+void orc_quantize_q8_1(const float *x, uint8_t *y, int k);
 void orc_quantize_q8_K(const float *x, uint8_t *y, int k);
 /* quantise a row of k floats into the activation format for weight type qt */
 int orc_quantize_act(int qt, const float *x, uint8_t *y, int k);

@@ -17,7 +17,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsabah_oracle.so")
 
 Q8_0, Q4_K, Q6_K, Q8_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0 = 8, 12, 14, 15, 18, 20, 21, 22, 23, 42
+Q5_1, Q8_1, Q5_K = 7, 9, 13
 BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292), IQ3_S: (256, 110),
+         Q5_1: (32, 24), Q8_1: (32, 36), Q5_K: (256, 176),
          IQ3_XXS: (256, 98), IQ4_NL: (32, 18), IQ4_XS: (256, 136),
          IQ2_S: (256, 82), Q2_0: (64, 18)}
 
@@ -38,7 +40,7 @@ def lib():
     vp, sz, ci, cf = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
     L.orc_fp16_to_fp32.argtypes, L.orc_fp16_to_fp32.restype = [ctypes.c_uint16], cf
     L.orc_fp32_to_fp16.argtypes, L.orc_fp32_to_fp16.restype = [cf], ctypes.c_uint16
-    for n in ("orc_quantize_q8_0", "orc_quantize_q8_K"):
+    for n in ("orc_quantize_q8_0", "orc_quantize_q8_1", "orc_quantize_q8_K"):
         getattr(L, n).argtypes, getattr(L, n).restype = [vp, vp, ci], None
     L.orc_quantize_act.argtypes, L.orc_quantize_act.restype = [ci, vp, vp, ci], ci
     L.orc_quantize_weights.argtypes, L.orc_quantize_weights.restype = [ci, vp, vp, ci], ci
@@ -92,6 +94,13 @@ def quantize_q8_0(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     y = np.zeros(x.size // 32 * 34, np.uint8)
     lib().orc_quantize_q8_0(_p(x), _p(y), x.size)
+    return y
+
+
+def quantize_q8_1(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    y = np.zeros(x.size // 32 * 36, np.uint8)
+    lib().orc_quantize_q8_1(_p(x), _p(y), x.size)
     return y
 
 

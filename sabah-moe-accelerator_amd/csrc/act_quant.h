@@ -1,8 +1,9 @@
-// Activation quantisation on the device: fp32 rows -> q8_0 or q8_K, in the
+// Activation quantisation on the device: fp32 rows -> q8_0, q8_1 or q8_K, in the
 // ActLayout scratch form (quant_formats.h).  The integer values and scales are
 // the ones ggml's CPU path feeds its vec_dot kernels:
 //   q8_0 (quantize_row_q8_0_ref): per 32 elements d = amax/127 rounded to fp16,
 //        q = roundf(x * (1/d)) (halves away from zero);
+//   q8_1 (quantize_row_q8_1_ref): q8_0's d and q, plus s = sum(q) * d rounded to fp16;
 //   q8_K (quantize_row_q8_K_ref): per 256 elements the signed value of largest
 //        magnitude (first on ties) gives iscale = -127/max, q = min(127, rint(iscale*x))
 //        (nearest even), d = 1/iscale in fp32, bsums = sums of 16 consecutive q.
@@ -149,8 +150,11 @@ __device__ inline void row16_quant_q8K(const Act16& a, int c, uint8_t* act, cons
     if (l == 0) reinterpret_cast<float*>(act + L.off_d)[c] = d;
 }
 
-// q8_0: the 32-element block b of the chunk is lanes 2b and 2b+1
-__device__ inline void row16_quant_q8_0(const Act16& a, int c, uint8_t* act, const ActLayout& L) {
+// q8_0: the 32-element block b of the chunk is lanes 2b and 2b+1.  q8_1
+// (with_sum) also stores s = fp16(sum(q) * d), d the fp32 scale before its
+// fp16 rounding (quantize_row_q8_1_ref), in the layout's s area.
+__device__ inline void row16_quant_q8_0(const Act16& a, int c, uint8_t* act, const ActLayout& L,
+                                        bool with_sum = false) {
     const uint32_t l = threadIdx.x & 15u;
     float amax = 0.0f;
 #pragma unroll
@@ -168,6 +172,20 @@ __device__ inline void row16_quant_q8_0(const Act16& a, int c, uint8_t* act, con
     packed.w = pack4_i8(q[12], q[13], q[14], q[15]);
     reinterpret_cast<uint4*>(act + c * kActChunkStride)[l] = packed;
     if ((l & 1u) == 0) reinterpret_cast<float*>(act + L.off_d)[c * 8 + (l >> 1)] = __half2float(__float2half_rn(d));
+    if (with_sum) {
+        int s = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += q[j];
+        s += (int)dpp<kDppXor1>((uint32_t)s);            // the block's other sixteen
+        // the fp32 product is rounded before its fp16 rounding: the empty asm
+        // keeps the compiler from selecting one mixed-precision multiply that
+        // rounds the exact product to fp16 once (a tie of the fp32 product
+        // then rounds differently)
+        float sd = __fmul_rn((float)s, d);
+        asm volatile("" : "+v"(sd));
+        if ((l & 1u) == 0)
+            reinterpret_cast<float*>(act + L.off_bsum)[c * 8 + (l >> 1)] = __half2float(__float2half_rn(sd));
+    }
 }
 
 // Load sixteen consecutive floats: elements e..e+15 of a row of k (k is a
@@ -240,7 +258,7 @@ __device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q, 
 #pragma unroll
     for (int j = 0; j < 16; ++j) a.v[j] = in ? a_in.v[j] : 0.0f;
     if (B.at == QT_Q8_K) row16_quant_q8K(a, c, B.act + r * B.act_stride, L, mfma_order);
-    else row16_quant_q8_0(a, c, B.act + r * B.act_stride, L);
+    else row16_quant_q8_0(a, c, B.act + r * B.act_stride, L, B.at == QT_Q8_1);
 }
 
 template <int ROUNDS>

@@ -25,9 +25,11 @@ __device__ inline float unit_accumulate(const LdsWindow<QT>& Wn, const uint8_t* 
     const ActLayout AL(k, act_type(QT));
     const float* dxa = reinterpret_cast<const float*>(act + AL.off_d);
     const int16_t* bsa = reinterpret_cast<const int16_t*>(act + AL.off_bsum);
-    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL) {
+    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL || QT == QT_Q5_1) {
+        const int16_t* bs = QT == QT_Q5_1 ? reinterpret_cast<const int16_t*>(reinterpret_cast<const float*>(bsa) + 4 * us)
+                                          : bsa;
         const uint8_t* chunk = act + (us >> 1) * kActChunkStride + (us & 1) * 128;
-        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + 4 * us, bsa);
+        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + 4 * us, bs);
         const int nb = min(4, k / 32 - 4 * us);
 #pragma unroll
         for (int j = 0; j < 4; ++j)

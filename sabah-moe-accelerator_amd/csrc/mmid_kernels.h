@@ -133,8 +133,8 @@ constexpr int kMaxTiles = 64;
 
 // 16-byte loads per lane per pass
 __host__ __device__ constexpr int stage_iters(int qt) {
-    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7
-         : (qt == QT_IQ4_NL || qt == QT_Q2_0) ? 5
+    return qt == QT_IQ3_S ? 7 : qt == QT_Q4_K ? 10 : qt == QT_Q5_K ? 12 : qt == QT_Q6_K ? 14 : qt == QT_IQ3_XXS ? 7
+         : (qt == QT_IQ4_NL || qt == QT_Q2_0) ? 5 : qt == QT_Q5_1 ? 7
          : qt == QT_IQ2_S ? 6 : 9;
 }
 // the same load count spread over nt threads
@@ -173,7 +173,9 @@ __host__ __device__ inline int pass_units(int qt, int n_mat, int unit_bytes) {
 
 // Q8_0, IQ4_NL (32-element blocks) and Q2_0 (64) rows need only be whole
 // blocks: their units are four blocks, the last of a row 1..3
-__host__ __device__ inline bool four_block_units(int qt) { return qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0; }
+__host__ __device__ inline bool four_block_units(int qt) {
+    return qt == QT_Q8_0 || qt == QT_Q5_1 || qt == QT_IQ4_NL || qt == QT_Q2_0;
+}
 __host__ __device__ inline int units_per_row(int qt, int k) {
     return four_block_units(qt) ? (k + 4 * block_elems(qt) - 1) / (4 * block_elems(qt)) : k / 256;
 }
@@ -233,7 +235,7 @@ __host__ inline int launch_lds(int qt, const Plan& P) {
 // bytes of unit us of a row of k elements
 template <int QT>
 __device__ inline int unit_len(int k, int us) {
-    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL || QT == QT_Q2_0)
+    if constexpr (QT == QT_Q8_0 || QT == QT_Q5_1 || QT == QT_IQ4_NL || QT == QT_Q2_0)
         return block_bytes(QT) * min(4, k / block_elems(QT) - 4 * us);
     return UnitFmt<QT>::BYTES;
 }
@@ -246,9 +248,12 @@ __device__ inline void unit_into_part(const LdsWindow<QT>& Wn, const uint8_t* ta
     const ActLayout AL(k, act_type(QT));
     const float* dxa = reinterpret_cast<const float*>(act + AL.off_d);
     const int16_t* bsa = reinterpret_cast<const int16_t*>(act + AL.off_bsum);
-    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL) {
+    if constexpr (QT == QT_Q8_0 || QT == QT_IQ4_NL || QT == QT_Q5_1) {
+        // Q5_1: the q8_1 s values ride in the bsum argument
+        const int16_t* bs = QT == QT_Q5_1 ? reinterpret_cast<const int16_t*>(reinterpret_cast<const float*>(bsa) + 4 * us)
+                                          : bsa;
         const uint8_t* chunk = act + (us >> 1) * kActChunkStride + (us & 1) * 128;
-        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + 4 * us, bsa);
+        const UnitDot<QT> r = unit_dot<QT>(Wn, tabs, chunk, dxa + 4 * us, bs);
         const int nb = min(4, k / 32 - 4 * us);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -941,8 +946,9 @@ __global__ __launch_bounds__(kThreads) void k_dequant(const uint8_t* __restrict_
 
 // ---------------------------------------------------------------------------
 // Activation quantiser exposed for byte-level checks: rows of k floats into
-// ggml's own block layout (block_q8_0: fp16 d + 32 int8; block_q8_K: f32 d +
-// 256 int8 + 16 int16 bsums).  grid = n_rows, one workgroup per row.
+// ggml's own block layout (block_q8_0: fp16 d + 32 int8; block_q8_1: fp16 d,
+// fp16 s + 32 int8; block_q8_K: f32 d + 256 int8 + 16 int16 bsums).
+// grid = n_rows, one workgroup per row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void k_quantize_act_ggml(const float* __restrict__ x, uint8_t* __restrict__ y,
                                                                 int k, int at) {
@@ -956,7 +962,7 @@ __global__ __launch_bounds__(kThreads) void k_quantize_act_ggml(const float* __r
     const float* d = reinterpret_cast<const float*>(smem + L.off_d);
     for (int q = threadIdx.x; q < k; q += blockDim.x) {
         const int b = q / qb, j = q - b * qb;
-        yr[(size_t)b * bb + (at == QT_Q8_K ? 4 : 2) + j] = smem[(q >> 8) * kActChunkStride + (q & 255)];
+        yr[(size_t)b * bb + (at == QT_Q8_K ? 4 : at == QT_Q8_1 ? 4 : 2) + j] = smem[(q >> 8) * kActChunkStride + (q & 255)];
     }
     for (int b = threadIdx.x; b < nb; b += blockDim.x) {
         if (at == QT_Q8_K) {
@@ -968,6 +974,12 @@ __global__ __launch_bounds__(kThreads) void k_quantize_act_ggml(const float* __r
             const unsigned short hb = __half_as_ushort(__float2half_rn(d[b]));
             yr[(size_t)b * bb] = (uint8_t)(hb & 0xff);
             yr[(size_t)b * bb + 1] = (uint8_t)(hb >> 8);
+            if (at == QT_Q8_1) {                        // s, already fp16-rounded
+                const float sv = reinterpret_cast<const float*>(smem + L.off_bsum)[b];
+                const unsigned short hs = __half_as_ushort(__float2half_rn(sv));
+                yr[(size_t)b * bb + 2] = (uint8_t)(hs & 0xff);
+                yr[(size_t)b * bb + 3] = (uint8_t)(hs >> 8);
+            }
         }
     }
 }

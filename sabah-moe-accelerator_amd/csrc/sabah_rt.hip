@@ -317,6 +317,8 @@ hipError_t dispatch_mmid(int qt, const MmidArgs& a, hipStream_t st) {
     switch (qt) {
     case QT_Q8_0: return launch_mmid<QT_Q8_0>(a, st);
     case QT_Q4_K: return launch_mmid<QT_Q4_K>(a, st);
+    case QT_Q5_K: return launch_mmid<QT_Q5_K>(a, st);
+    case QT_Q5_1: return launch_mmid<QT_Q5_1>(a, st);
     case QT_Q6_K: return launch_mmid<QT_Q6_K>(a, st);
     case QT_IQ3_S: return launch_mmid<QT_IQ3_S>(a, st);
     case QT_IQ3_XXS: return launch_mmid<QT_IQ3_XXS>(a, st);
@@ -350,6 +352,8 @@ hipError_t dispatch_gate_up(int qt, const GateUpArgs& a, int n_tokens, hipStream
     switch (qt) {
     case QT_Q8_0: return launch_gate_up<QT_Q8_0>(a, n_tokens, st);
     case QT_Q4_K: return launch_gate_up<QT_Q4_K>(a, n_tokens, st);
+    case QT_Q5_K: return launch_gate_up<QT_Q5_K>(a, n_tokens, st);
+    case QT_Q5_1: return launch_gate_up<QT_Q5_1>(a, n_tokens, st);
     case QT_Q6_K: return launch_gate_up<QT_Q6_K>(a, n_tokens, st);
     case QT_IQ3_S: return launch_gate_up<QT_IQ3_S>(a, n_tokens, st);
     case QT_IQ3_XXS: return launch_gate_up<QT_IQ3_XXS>(a, n_tokens, st);
@@ -381,6 +385,8 @@ hipError_t dispatch_down(int qt, const DownArgs& a, int n_tokens, hipStream_t st
     switch (qt) {
     case QT_Q8_0: return launch_down<QT_Q8_0>(a, n_tokens, st);
     case QT_Q4_K: return launch_down<QT_Q4_K>(a, n_tokens, st);
+    case QT_Q5_K: return launch_down<QT_Q5_K>(a, n_tokens, st);
+    case QT_Q5_1: return launch_down<QT_Q5_1>(a, n_tokens, st);
     case QT_Q6_K: return launch_down<QT_Q6_K>(a, n_tokens, st);
     case QT_IQ3_S: return launch_down<QT_IQ3_S>(a, n_tokens, st);
     case QT_IQ3_XXS: return launch_down<QT_IQ3_XXS>(a, n_tokens, st);
@@ -1063,6 +1069,8 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
     switch (qt) {
     case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_Q5_K: hipLaunchKernelGGL(k_dequant<QT_Q5_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
+    case QT_Q5_1: hipLaunchKernelGGL(k_dequant<QT_Q5_1>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
     case QT_IQ3_XXS: hipLaunchKernelGGL(k_dequant<QT_IQ3_XXS>, grid, dim3(kThreads), lds, g_stream, s, d_dst, n_rows, row_elems); break;
@@ -1275,6 +1283,8 @@ hipError_t dispatch_dense(int qt, const DenseArgs& a, int kind, hipStream_t st) 
     switch (qt) {
     case QT_Q8_0: return launch_dense<QT_Q8_0, NMAT>(a, kind, st);
     case QT_Q4_K: return launch_dense<QT_Q4_K, NMAT>(a, kind, st);
+    case QT_Q5_K: return launch_dense<QT_Q5_K, NMAT>(a, kind, st);
+    case QT_Q5_1: return launch_dense<QT_Q5_1, NMAT>(a, kind, st);
     case QT_Q6_K: return launch_dense<QT_Q6_K, NMAT>(a, kind, st);
     case QT_IQ3_S: return launch_dense<QT_IQ3_S, NMAT>(a, kind, st);
     case QT_IQ3_XXS: return launch_dense<QT_IQ3_XXS, NMAT>(a, kind, st);

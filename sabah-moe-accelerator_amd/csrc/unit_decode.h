@@ -1,8 +1,8 @@
 // Register-resident decoding of quantised weights, one "unit" per lane.
 //
-// A unit is one 256-element super-block (Q4_K 144 B, Q6_K 210 B, IQ3_S 110 B,
-// IQ3_XXS 98 B, IQ2_S 82 B, IQ4_XS 136 B), four 32-element blocks (Q8_0 136 B, IQ4_NL
-// 72 B) or four 64-element blocks (Q2_0 72 B).  Each lane loads its unit straight
+// A unit is one 256-element super-block (Q4_K 144 B, Q5_K 176 B, Q6_K 210 B,
+// IQ3_S 110 B, IQ3_XXS 98 B, IQ2_S 82 B, IQ4_XS 136 B), four 32-element blocks
+// (Q8_0 136 B, Q5_1 96 B, IQ4_NL 72 B) or four 64-element blocks (Q2_0 72 B).  Each lane loads its unit straight
 // from HBM into VGPRs with 8-byte loads that cover exactly the unit's 8-byte
 // granules (so a load never touches a page the unit does not), then
 // re-aligns the bytes so that every field of the format sits at a static
@@ -11,11 +11,12 @@
 //
 // Field origin: all fields used in the inner loops start at the same residue
 // mod 4 inside the block (IQ3_S, IQ3_XXS, IQ2_S: byte 2; Q8_0 and IQ4_NL even
-// blocks: byte 2; Q4_K, Q6_K and IQ4_XS: byte 0).  F[i] is the dword at
+// blocks: byte 2; Q4_K, Q5_K, Q6_K, IQ4_XS and Q5_1: byte 0).  F[i] is the dword at
 // (unit start + ORG + 4 i); Fm1 is the dword before it (the IQ formats read
 // their fp16 d there).
 //
-// Block layouts: sabah_rt.cu:2462-2485 (Q4_K), 2537-2545 (Q8_0), 2618-2647
+// Block layouts: sabah_rt.cu:2462-2485 (Q4_K), 2487-2512 (Q5_K), 2514-2535
+// (Q5_1), 2537-2545 (Q8_0), 2618-2647
 // (IQ3_S), 2293-2318 (IQ2_S), 2320-2344 (IQ3_XXS), 2380-2409 (IQ4_NL,
 // IQ4_XS); gguf-py
 // quants.py:586-606 (Q6_K: ql[128] qh[64] int8 sc[16] d).
@@ -51,6 +52,8 @@ template <> struct UnitFmt<QT_IQ4_XS> { static constexpr int BYTES = 136, ELEMS 
 template <> struct UnitFmt<QT_IQ4_NL> { static constexpr int BYTES = 72, ELEMS = 128, ORG = 2, NF = 18, CONTRIB = 4; };
 template <> struct UnitFmt<QT_IQ2_S> { static constexpr int BYTES = 82, ELEMS = 256, ORG = 2, NF = 20, CONTRIB = 1; };
 template <> struct UnitFmt<QT_Q2_0> { static constexpr int BYTES = 72, ELEMS = 256, ORG = 2, NF = 18, CONTRIB = 8; };
+template <> struct UnitFmt<QT_Q5_K> { static constexpr int BYTES = 176, ELEMS = 256, ORG = 0, NF = 44, CONTRIB = 1; };
+template <> struct UnitFmt<QT_Q5_1> { static constexpr int BYTES = 96, ELEMS = 128, ORG = 0, NF = 24, CONTRIB = 4; };
 
 // Window: the unit's granules, loaded from base = (origin - 4) rounded down to
 // 8 bytes; the origin then sits at byte p in [4, 11] of the window.
@@ -435,7 +438,8 @@ __device__ inline int iq3s_half_dot(const Iq3sHalf& W, const uint32_t (&A)[4][8]
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t byte_of(const uint32_t* F, int b) { return (F[b >> 2] >> (8 * (b & 3))) & 0xFFu; }
 
-__device__ inline void q4k_scale_min(const uint32_t (&F)[36], int j, int& sc, int& mn) {
+template <int NF>
+__device__ inline void q4k_scale_min(const uint32_t (&F)[NF], int j, int& sc, int& mn) {
     const uint32_t* q = F + 1;      // the 12 scale bytes
     if (j < 4) {
         sc = (int)(byte_of(q, j) & 63u);
@@ -450,6 +454,37 @@ __device__ inline void q4k_item(const uint32_t (&F)[36], int j, uint32_t (&v)[8]
     const int sh = 4 * (j & 1);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = (F[4 + 8 * (j >> 1) + i] >> sh) & 0x0F0F0F0Fu;
+}
+
+// ---------------------------------------------------------------------------
+// Q5_K: Q4_K's d, dmin and packed 6-bit scales / mins in F[0..3], qh[32] in
+// F[4..11], qs[128] in F[12..43]; element 32 j + l (sub-block j) is the nibble
+// (low for even j) of qs[32 (j / 2) + l] plus 16 when bit j of qh[l] is set.
+// ---------------------------------------------------------------------------
+__device__ inline void q5k_item(const uint32_t (&F)[44], int j, uint32_t (&v)[8]) {
+    const int sh = 4 * (j & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        v[i] = ((F[12 + 8 * (j >> 1) + i] >> sh) & 0x0F0F0F0Fu) | (((F[4 + i] >> j) & 0x01010101u) << 4);
+}
+
+// ---------------------------------------------------------------------------
+// Q5_1 (four 24-byte blocks per unit): block J's fp16 d and m in F[6 J], qh in
+// F[6 J + 1], qs in F[6 J + 2 .. 6 J + 5]; element j < 16 is the low nibble of
+// qs[j] plus bit j of qh times 16, element j + 16 the high nibble plus bit
+// j + 16; value d q + m.  v: the 32 values as int8 (0 .. 31) in element order.
+// ---------------------------------------------------------------------------
+__device__ inline uint32_t spread4_x16(uint32_t n) { return spread4(n) << 4; }
+template <int J>
+__device__ inline void q5_1_block(const uint32_t (&F)[24], uint32_t (&v)[8], uint32_t& dm) {
+    dm = F[6 * J];
+    const uint32_t qh = F[6 * J + 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t q = F[6 * J + 2 + i];
+        v[i] = (q & 0x0F0F0F0Fu) | spread4_x16((qh >> (4 * i)) & 15u);
+        v[4 + i] = ((q >> 4) & 0x0F0F0F0Fu) | spread4_x16((qh >> (16 + 4 * i)) & 15u);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -647,6 +682,37 @@ __device__ inline UnitDot<QT> unit_dot(const Window& Wn, const uint8_t* smem, co
         }
         const float d = h2f(F[0]), dmin = h2f(F[0] >> 16);
         r.c[0] = __fsub_rn(__fmul_rn(__fmul_rn(d, dx[0]), (float)isum), __fmul_rn(__fmul_rn(dmin, dx[0]), (float)msum));
+    } else if constexpr (QT == QT_Q5_K) {
+        int isum = 0, msum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[8], A[8];
+            q5k_item(F, j, v);
+            act8(chunk, j, A);
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);
+            int sc, mn;
+            q4k_scale_min(F, j, sc, mn);
+            isum += __mul24(sc, s);             // sc, mn < 64; |s| < 2^17
+            msum += __mul24(mn, (int)bs[2 * j] + (int)bs[2 * j + 1]);
+        }
+        const float d = h2f(F[0]), dmin = h2f(F[0] >> 16);
+        r.c[0] = __fsub_rn(__fmul_rn(__fmul_rn(d, dx[0]), (float)isum), __fmul_rn(__fmul_rn(dmin, dx[0]), (float)msum));
+    } else if constexpr (QT == QT_Q5_1) {
+        // ggml: per block sumf += (d_w * d_x) * sumi + m_w * s_x; bs carries the q8_1 s values
+        const float* sx = reinterpret_cast<const float*>(bs);
+        uint32_t v[8], A[8], dm;
+#define SB_Q51_BLOCK(J)                                                                          \
+        {                                                                                        \
+            q5_1_block<J>(F, v, dm);                                                             \
+            act8(chunk, J, A);                                                                   \
+            int s = 0;                                                                           \
+            _Pragma("unroll") for (int i = 0; i < 8; ++i) s = sdot4(v[i], A[i], s);              \
+            r.c[J] = __fadd_rn(__fmul_rn(__fmul_rn(h2f(dm), dx[J]), (float)s), __fmul_rn(h2f(dm >> 16), sx[J])); \
+        }
+        SB_Q51_BLOCK(0) SB_Q51_BLOCK(1) SB_Q51_BLOCK(2) SB_Q51_BLOCK(3)
+#undef SB_Q51_BLOCK
     } else if constexpr (QT == QT_Q6_K) {
         int isum = 0;
 #pragma unroll
@@ -780,6 +846,29 @@ __device__ inline void unit_dequant(const UnitWindow<QT>& Wn, const uint8_t* sme
             for (int e = 0; e < 32; ++e)
                 out[32 * j + e] = __fsub_rn(__fmul_rn(d1, (float)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu)), m1);
         }
+    } else if constexpr (QT == QT_Q5_K) {
+        const float d = h2f(F[0]), dmin = h2f(F[0] >> 16);
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[8];
+            q5k_item(F, j, v);
+            int sc, mn;
+            q4k_scale_min(F, j, sc, mn);
+            const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+            for (int e = 0; e < 32; ++e)
+                out[32 * j + e] = __fsub_rn(__fmul_rn(d1, (float)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu)), m1);
+        }
+    } else if constexpr (QT == QT_Q5_1) {
+        uint32_t v[8], dm;
+#define SB_Q51_DEQ(J)                                                                              \
+        {                                                                                          \
+            q5_1_block<J>(F, v, dm);                                                               \
+            const float d = h2f(dm), m = h2f(dm >> 16);                                            \
+            if (32 * J < n)                                                                        \
+                for (int e = 0; e < 32; ++e)                                                       \
+                    out[32 * J + e] = __fadd_rn(__fmul_rn((float)((v[e >> 2] >> (8 * (e & 3))) & 0xFFu), d), m); \
+        }
+        SB_Q51_DEQ(0) SB_Q51_DEQ(1) SB_Q51_DEQ(2) SB_Q51_DEQ(3)
+#undef SB_Q51_DEQ
     } else if constexpr (QT == QT_Q6_K) {
         const float d = h2f(F[52]);
         for (int j = 0; j < 8; ++j) {

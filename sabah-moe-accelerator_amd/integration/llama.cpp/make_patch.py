@@ -94,9 +94,9 @@ CUDA_HUNKS = [
 +// expert tensor in device memory or left it on the host.
 +static bool ggml_cuda_sabah_type(ggml_type type) {
 +    switch (type) {
-+        case GGML_TYPE_Q8_0: case GGML_TYPE_Q4_K: case GGML_TYPE_Q6_K: case GGML_TYPE_IQ3_XXS:
-+        case GGML_TYPE_IQ4_NL: case GGML_TYPE_IQ3_S: case GGML_TYPE_IQ2_S: case GGML_TYPE_IQ4_XS:
-+        case GGML_TYPE_Q2_0:
++        case GGML_TYPE_Q8_0: case GGML_TYPE_Q5_1: case GGML_TYPE_Q4_K: case GGML_TYPE_Q5_K:
++        case GGML_TYPE_Q6_K: case GGML_TYPE_IQ3_XXS: case GGML_TYPE_IQ4_NL: case GGML_TYPE_IQ3_S:
++        case GGML_TYPE_IQ2_S: case GGML_TYPE_IQ4_XS: case GGML_TYPE_Q2_0:
 +            return true;
 +        default:
 +            return false;

@@ -34,8 +34,8 @@ from . import gguf
 from .bank import ROLES, ExpertBank
 
 # the expert types the HIP kernels decode (ggml type codes)
-RUNTIME_TYPES = {8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 18: "IQ3_XXS", 20: "IQ4_NL", 21: "IQ3_S", 22: "IQ2_S",
-                 23: "IQ4_XS", 42: "Q2_0"}
+RUNTIME_TYPES = {7: "Q5_1", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 18: "IQ3_XXS", 20: "IQ4_NL",
+                 21: "IQ3_S", 22: "IQ2_S", 23: "IQ4_XS", 42: "Q2_0"}
 
 
 class UnsupportedModel(Exception):

@@ -20,13 +20,13 @@ PKG_ROOT = os.path.dirname(os.path.dirname(HERE))          # sabah-moe-accelerat
 CSRC = os.path.join(PKG_ROOT, "csrc")
 
 # ggml type codes, so a runtime trace and a llama.cpp trace mean the same thing
-QTYPE = {"Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "IQ3_XXS": 18, "IQ4_NL": 20, "IQ3_S": 21, "IQ2_S": 22, "IQ4_XS": 23,
-         "Q2_0": 42}
+QTYPE = {"Q5_1": 7, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ3_XXS": 18, "IQ4_NL": 20, "IQ3_S": 21,
+         "IQ2_S": 22, "IQ4_XS": 23, "Q2_0": 42}
 QTYPE_NAME = {v: k for k, v in QTYPE.items()}
 
 # (elements per block, bytes per block)
-QBLOCK = {8: (32, 34), 12: (256, 144), 14: (256, 210), 18: (256, 98), 20: (32, 18), 21: (256, 110),
-          22: (256, 82), 23: (256, 136), 42: (64, 18)}
+QBLOCK = {7: (32, 24), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 18: (256, 98), 20: (32, 18),
+          21: (256, 110), 22: (256, 82), 23: (256, 136), 42: (64, 18)}
 
 
 class RuntimeUnavailable(Exception):

@@ -25,8 +25,10 @@ static int type_traits(int type, int64_t *blck, size_t *bytes) {
     switch (type) {
     case 0: case 26: *blck = 1; *bytes = 4; return 0;           /* F32, I32 */
     case 1: *blck = 1; *bytes = 2; return 0;                    /* F16 */
+    case 7: *blck = 32; *bytes = 24; return 0;                  /* Q5_1 */
     case 8: *blck = 32; *bytes = 34; return 0;                  /* Q8_0 */
     case 12: *blck = 256; *bytes = 144; return 0;               /* Q4_K */
+    case 13: *blck = 256; *bytes = 176; return 0;               /* Q5_K */
     case 14: *blck = 256; *bytes = 210; return 0;               /* Q6_K */
     case 18: *blck = 256; *bytes = 98; return 0;                /* IQ3_XXS */
     case 20: *blck = 32; *bytes = 18; return 0;                 /* IQ4_NL */

@@ -63,6 +63,10 @@ def dequant_act(O, qt: int, act: np.ndarray, k: int) -> np.ndarray:
         blk = act.reshape(-1, 34)
         d = blk[:, :2].copy().view(np.float16).astype(np.float64)
         return (blk[:, 2:].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
+    if qt == O.Q5_1:                                  # q8_1 activations: d, s, 32 values
+        blk = act.reshape(-1, 36)
+        d = blk[:, :2].copy().view(np.float16).astype(np.float64)
+        return (blk[:, 4:].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
     blk = act.reshape(-1, 292)
     d = blk[:, :4].copy().view(np.float32).astype(np.float64)
     return (blk[:, 4:260].view(np.int8).astype(np.float64) * d).reshape(-1)[:k]
@@ -104,12 +108,57 @@ def random_blocks(rng, qt: int, n_rows: int, k: int) -> np.ndarray:
 
     if qt in (8, 18, 20, 21, 22, 23, 42):   # Q8_0, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0: fp16 d at 0
         raw[:, :, 0:2] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
-    elif qt == 12:                          # Q4_K: d, dmin at 0, 2 (non-negative in real data)
+    elif qt == 7:                           # Q5_1: d, m at 0, 2
+        raw[:, :, 0:2] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)
+        raw[:, :, 2:4] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
+    elif qt in (12, 13):                    # Q4_K, Q5_K: d, dmin at 0, 2 (non-negative in real data)
         raw[:, :, 0:2] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)
         raw[:, :, 2:4] = np.abs(scales(n_rows * nb)).view(np.uint8).reshape(n_rows, nb, 2)
     elif qt == 14:                          # Q6_K: d at 208
         raw[:, :, 208:210] = scales(n_rows * nb).view(np.uint8).reshape(n_rows, nb, 2)
     return raw.reshape(n_rows, nb * bb)
+
+
+def q8_1_tie_row(k: int, seed: int = 0) -> np.ndarray:
+    """A row of k fp32 values (k a multiple of 32) whose every 32-block has a
+    q8_1 scaled sum at an fp16 tie: fl32(sum(q) * d) lies exactly halfway
+    between two halves while the exact product does not, so rounding the
+    product once to fp16 (a fused mixed-precision multiply) gives the other
+    half than rounding it to fp32 first, as ggml does.  Built per block: a
+    tie value v and a sum S, a scale d with fl32(S * d) = v != S * d, the
+    block's largest magnitude 127 d, and the other values multiples of d
+    whose quantised sum makes S."""
+    rng = np.random.default_rng(seed)
+    f32 = np.float32
+    out = []
+    while len(out) < k // 32:
+        S = int(rng.integers(-600, 600))
+        if abs(S) < 150:
+            continue
+        # an fp16 tie: a half h and its successor, midpoint v (exact in fp32)
+        h = np.float16(rng.uniform(0.05, 20.0) * (1 if S > 0 else -1))
+        v = f32((float(h) + float(np.nextafter(h, np.float16(np.inf if S > 0 else -np.inf)))) / 2)
+        d0 = f32(float(v) / S)
+        for dd in (d0, np.nextafter(d0, f32(1)), np.nextafter(d0, f32(-1))):
+            amax = f32(float(dd) * 127)
+            if not (f32(amax / f32(127)) == dd and f32(f32(S) * dd) == v and float(S) * float(dd) != float(v)):
+                continue
+            q = np.zeros(32, np.int64)
+            q[0] = 127
+            rest = S - 127
+            for j in range(1, 32):             # spread the rest over the other 31, each within [-126, 126]
+                share = int(np.clip(round(rest / (32 - j)), -126, 126))
+                q[j] = share
+                rest -= share
+            if rest != 0:
+                break
+            blk = (q.astype(np.float64) * float(dd)).astype(np.float32)
+            idv = f32(1) / dd
+            back = np.array([np.sign(x) * np.floor(abs(float(x * idv)) + 0.5) for x in blk])
+            if np.array_equal(back, q) and f32(np.abs(blk).max()) == amax:
+                out.append(blk)
+            break
+    return np.concatenate(out)
 
 
 def unfused_rounding_row(k: int, amax: float = 3.0) -> np.ndarray:

@@ -21,7 +21,8 @@ CALLER = os.path.join(ROOT, "tests", "bridge", "bridge_caller")
 LIB = os.path.join(ROOT, "sabah-moe-accelerator_amd", "csrc", "libsabah_rt.so")
 
 Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0 = 8, 12, 14, 18, 20, 21, 22, 23, 42
-BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S, Q2_0)
+Q5_1, Q5_K = 7, 13
+BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S, Q2_0, Q5_1)
 
 
 def run_caller(arg, lib=LIB, timeout=120):
@@ -84,6 +85,8 @@ CASES = [
     (IQ4_XS, 1024, 256, 16, 4, 2, 4, 16, False),
     (IQ2_S, 1024, 256, 16, 4, 2, 1, 16, True),
     (Q2_0, 960, 512, 16, 4, 3, 1, 16, False),        # 64-element blocks, a partial last unit
+    (Q5_1, 2048, 256, 16, 4, 2, 1, 16, False),
+    (Q5_K, 768, 512, 16, 4, 2, 4, 16, True),
 ]
 
 
@@ -132,6 +135,7 @@ def test_patch_routes_exactly_the_types_the_library_decodes():
     body = text[text.index("static bool ggml_cuda_sabah_type"):]
     body = body[:body.index("default:")]
     routed = set(re.findall(r"GGML_TYPE_(\w+)", body))
-    assert routed == {"Q8_0", "Q4_K", "Q6_K", "IQ3_XXS", "IQ4_NL", "IQ3_S", "IQ2_S", "IQ4_XS", "Q2_0"}
+    assert routed == {"Q8_0", "Q5_1", "Q4_K", "Q5_K", "Q6_K", "IQ3_XXS", "IQ4_NL", "IQ3_S", "IQ2_S", "IQ4_XS",
+                      "Q2_0"}
     assert routed <= set(rt.QTYPE)
     assert all(rt.row_bytes(rt.QTYPE[n], 256) > 0 for n in routed)

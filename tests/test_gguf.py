@@ -126,7 +126,7 @@ def test_inspector_refuses(tmp_path, orc, case, needle):
             return gguf.WriterTensor("blk.0.ffn_%s_exps.weight" % role, shape, qt, np.zeros(n, np.uint8))
         ts = [t("gate", 21, (D, F, E)), t("up", 21, (D, F, E))]
         if case == "type":
-            ts.append(t("down", 13, (F, D, E)))             # Q5_K: a GGUF type the kernels do not decode
+            ts.append(t("down", 6, (F, D, E)))              # Q5_0: a GGUF type the kernels do not decode
         elif case == "axis":
             ts.append(t("down", 21, (F, E, D)))             # experts not the slowest axis
         gguf.write_gguf(p, kv, ts)

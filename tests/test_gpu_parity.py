@@ -13,13 +13,14 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_parity, random_blocks, unfused_rounding_row, assert_bits_equal
+from helpers import assert_parity, random_blocks, unfused_rounding_row, assert_bits_equal, q8_1_tie_row
 
 pytestmark = pytest.mark.gpu
 
 Q8_0, Q4_K, Q6_K, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, Q2_0 = 8, 12, 14, 18, 20, 21, 22, 23, 42
+Q5_1, Q5_K = 7, 13
 # formats whose fp32 steps follow ggml's vec_dot order exactly: results bit-identical to the oracle's
-BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S, Q2_0)
+BIT_EXACT = (Q8_0, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, IQ2_S, Q2_0, Q5_1)
 DEV = torch.device("cuda:0")
 
 
@@ -58,7 +59,7 @@ def make_bank(orc, rng, qts, E, D, F, n_layers=1):
 # ---------------------------------------------------------------------------
 # bit-exact pieces
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("qt", [Q8_0, IQ3_S])
+@pytest.mark.parametrize("qt", [Q8_0, IQ3_S, Q5_1])
 def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
     rng = np.random.default_rng(100 + qt)
     k = 2048
@@ -66,13 +67,15 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
     x[1] *= 1e-3
     x[2] = 0.0                                              # zero rows
     x[3, :] = np.round(rng.standard_normal(k) * 40) + 0.5   # many exact ties
-    x[3, 0] = -127.0 if qt != Q8_0 else 127.0
+    x[3, 0] = -127.0 if qt not in (Q8_0, Q5_1) else 127.0
     x[4, 5] = 7.0
     x[4, 900] = -7.0                                        # equal magnitudes, opposite signs
     x[5] = 0.75                                             # constant row
     x[6, ::2] = 0.0
     x[7] *= 1e4
     x[8] = unfused_rounding_row(k)                          # q8_K bytes that a fused multiply-add changes
+    if qt == Q5_1:
+        x[8] = q8_1_tie_row(k)                              # q8_1 sums whose fp16 rounding a fused multiply changes
     ab = orc.act_row_bytes(qt, k)
     y = torch.zeros(9, ab, dtype=torch.uint8, device=DEV)
     hip_rt.check(hip_rt.lib().sabah_quantize_act(vp(T(x)), vp(y), qt, 9, k, stream()), "quantize_act")
@@ -84,7 +87,7 @@ def test_activation_quantisation_is_bit_exact(hip_rt, orc, qt):
 @pytest.mark.parametrize("qt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2048), (Q6_K, 768), (IQ3_S, 2048), (IQ3_S, 768),
                                   (IQ3_XXS, 2048), (IQ3_XXS, 768), (IQ4_NL, 640), (IQ4_NL, 96), (IQ4_XS, 2048),
                                   (IQ4_XS, 768), (IQ2_S, 2048), (IQ2_S, 768), (Q2_0, 2048), (Q2_0, 192),
-                                  (Q2_0, 64)])
+                                  (Q2_0, 64), (Q5_1, 1024), (Q5_1, 96), (Q5_K, 2048), (Q5_K, 768)])
 def test_dequant_is_bit_exact(hip_rt, orc, qt, k):
     rng = np.random.default_rng(qt * 7 + k)
     raw = random_blocks(rng, qt, 37, k)
@@ -115,7 +118,7 @@ CASES = [(Q8_0, 1024, 96), (Q8_0, 2048, 40), (Q8_0, 160, 24), (Q4_K, 2048, 48), 
          (Q6_K, 768, 72), (IQ3_S, 2048, 48), (IQ3_S, 768, 104), (Q8_0, 32768, 6),
          (IQ3_XXS, 2048, 48), (IQ3_XXS, 2560, 40), (IQ4_NL, 640, 64), (IQ4_NL, 96, 24), (IQ4_XS, 2048, 48),
          (IQ4_XS, 768, 72), (IQ2_S, 2048, 48), (IQ2_S, 768, 80), (Q2_0, 2048, 48), (Q2_0, 768, 64),
-         (Q2_0, 192, 40), (Q2_0, 64, 24)]
+         (Q2_0, 192, 40), (Q2_0, 64, 24), (Q5_1, 2048, 48), (Q5_1, 96, 24), (Q5_K, 2048, 48), (Q5_K, 768, 64)]
 
 
 @pytest.mark.parametrize("qt,k,rows", CASES)
@@ -307,7 +310,8 @@ def test_moe_block_single_token_q8_0(hip_rt, orc):
 # iq4nl_down_t3_hq take that path with q8_0 rows (Q8_0 / IQ4_NL down, d_ff 768)
 @pytest.mark.parametrize("name", ["q4k_e128_top8", "mixed_t32_q4k_q6k_shared", "iq3s_small", "iq3s_t32",
                                   "iq3xxs_iq4nl_artifact_shape", "iq4xs_small", "iq2s_iq3s_mix", "q8_0_t4_hq",
-                                  "iq4nl_down_t3_hq", "q2_0_decode", "q2_0_down_t3_hq", "q2_0_partial_units"])
+                                  "iq4nl_down_t3_hq", "q2_0_decode", "q2_0_down_t3_hq", "q2_0_partial_units",
+                                  "q4k_q5_1_block", "q5_1_down_t3_hq", "q5k_decode", "q5k_t4_hq"])
 def test_moe_layer_matches_oracle(hip_rt, orc, name):
     from sabah.runtime import routing
     from sabah.runtime.bank import DenseExpert
@@ -344,6 +348,19 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     elif name == "q2_0_down_t3_hq":
         E, D, F, K, Tn, qts = 24, 2048, 768, 6, 3, (IQ3_XXS, IQ3_XXS, Q2_0)
         ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "q4k_q5_1_block":
+        # the reference's Q4_K / Q4_K / Q5_1 block (results/bench_moe_blk0.json), one token
+        E, D, F, K, Tn, qts = 32, 2048, 768, 8, 1, (Q4_K, Q4_K, Q5_1)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
+    elif name == "q5_1_down_t3_hq":
+        E, D, F, K, Tn, qts = 24, 2048, 768, 6, 3, (Q5_1, Q5_1, Q5_1)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "q5k_decode":
+        E, D, F, K, Tn, qts = 64, 2048, 768, 10, 1, (Q5_K, Q5_K, Q5_K)
+        ids, w = routing.zipf_routing(rng, Tn, E, K)
+    elif name == "q5k_t4_hq":
+        E, D, F, K, Tn, qts = 32, 2048, 768, 8, 4, (Q5_K, Q5_K, Q5_K)
+        ids, w = routing.uniform_routing(rng, Tn, E, K)
     elif name == "q2_0_partial_units":
         # d_model 960 = 3 units + 3 blocks, d_ff 576 = 2 units + 1 block
         E, D, F, K, Tn, qts = 16, 960, 576, 4, 2, (Q2_0, Q2_0, Q2_0)
@@ -367,7 +384,7 @@ def test_moe_layer_matches_oracle(hip_rt, orc, name):
     sh = None if sh_raw is None else (sh_raw["gate"], sh_raw["up"], sh_raw["down"], (Q8_0,) * 3)
     want = orc.moe_layer(raws[(0, "gate")], raws[(0, "up")], raws[(0, "down")], qts, x, ids, w, shared=sh)
     assert_parity(out.cpu().numpy(), want, name)
-    if name.startswith("q2_0"):
+    if name.startswith("q2_0") or name.startswith("q5_1"):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
