@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "dense_kernels.h"
+#include "host_decode.h"
 #include "layer_kernels.h"
 #include "mmid_kernels.h"
 #include "prefill_kernels.h"
@@ -68,6 +69,21 @@ std::vector<BankEntry> g_banks;
 std::unordered_set<uintptr_t> g_device_sources;   // sources already proven to be device memory
 
 std::atomic<unsigned long long> g_calls{0}, g_empty_calls{0}, g_tokens{0}, g_lookups{0}, g_layer_calls{0};
+
+// Sampled self-check of sabah_rt_mul_mat_id_v2 (the reference's
+// sb_selfcheck, sabah_rt.cu:3435-3492): after each call, k (token, slot)
+// outputs are recomputed on the host in float64 from the expert's bytes and
+// the call's input row, quantised as the kernels quantise it (host_decode.h),
+// and compared by relative L2 error.  Enabled by SABAH_LLAMA_SELFCHECK=k (or
+// SABAH_RT_SELFCHECK) with SABAH_LLAMA_SELFCHECK_TOL, or sabah_rt_set_selfcheck.
+// g_sc_sentinel (tests only) perturbs the host recomputation's mapping: 1 the
+// neighbouring expert, 2 the next slot's input row, 3 the next token's input
+// row; a check that catches those catches a kernel that makes them.
+std::atomic<int> g_sc_k{0}, g_sc_sentinel{0};
+double g_sc_tol = 1e-5;
+std::atomic<unsigned long long> g_sc_ok{0}, g_sc_fail{0}, g_sc_calls{0};
+double g_sc_max = 0.0;                           // guarded by g_sc_mu
+std::mutex g_sc_mu;
 // MUL_MAT_ID calls that took the grouped (expert-major) path
 std::atomic<unsigned long long> g_grouped_calls{0};
 
@@ -453,6 +469,8 @@ SABAH_API int sabah_rt_device_count(void) {
     return n;
 }
 
+static void report_trace_at_exit();
+
 SABAH_API int sabah_rt_init(int device) {
     if (g_device == device && g_stream) return 0;
     if (g_device >= 0) return fail("sabah_rt_init(%d): already initialised on device %d", device, g_device);
@@ -483,6 +501,15 @@ SABAH_API int sabah_rt_init(int device) {
         g_noalloc_scratch[device] = static_cast<uint8_t*>(p) + kSyncBytes;
     }
     g_device = device;
+    {
+        const char* k = std::getenv("SABAH_LLAMA_SELFCHECK");
+        if (!k || !*k) k = std::getenv("SABAH_RT_SELFCHECK");
+        const char* tol = std::getenv("SABAH_LLAMA_SELFCHECK_TOL");
+        if (k && *k) g_sc_k.store(std::max(0, std::atoi(k)));
+        if (tol && *tol && std::atof(tol) > 0.0) g_sc_tol = std::atof(tol);
+        static bool registered = false;
+        if (!registered) registered = std::atexit(report_trace_at_exit) == 0;
+    }
     return 0;
 }
 
@@ -921,6 +948,124 @@ static int mmid_grouped(int form, int qt, const uint8_t* bank, size_t expert_str
     return ck(hipGetLastError(), "grouped MUL_MAT_ID launch") ? 0 : -1;
 }
 
+static uint64_t mix64(uint64_t z) {   // splitmix64's finaliser
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// The self-check of one v2 call (see g_sc_k): waits for the stream, then
+// recomputes min(k, n_tokens * n_ids) sampled (token, slot) output rows.  The
+// samples are a hash of the call's number, never of its results.  Expert
+// rows, inputs and outputs are copied from the device on the call's stream.
+static void selfcheck_call(const uint8_t* bank, size_t expert_stride, size_t row_stride, const uint8_t* d_x,
+                           size_t x_id_stride, int x_rows, size_t x_token_stride, const uint8_t* d_ids,
+                           size_t ids_id_stride, size_t ids_token_stride, int n_ids, int n_tokens, const float* d_dst,
+                           size_t dst_id_stride, size_t dst_token_stride, int rows, int k, int n_experts, int qt,
+                           hipStream_t st) {
+    const int K = g_sc_k.load();
+    if (K <= 0) return;
+    (void)hipStreamSynchronize(st);
+    const uint64_t call_no = g_sc_calls++;
+    const int sentinel = g_sc_sentinel.load();
+    const size_t rb = row_bytes(qt, k);
+    std::vector<float> x(k), out(rows), w(k);
+    std::vector<uint8_t> wb((size_t)rows * row_stride);
+    host::ActRow act;
+    const int n_pairs = n_ids * n_tokens, samples = std::min(K, n_pairs);
+    const uint64_t h0 = mix64(call_no * 0x9E3779B97F4A7C15ull + 0x5AB4ull);
+    for (int smp = 0; smp < samples; ++smp) {
+        const uint64_t h = mix64(h0 + (uint64_t)smp);
+        int t = (int)(h % (uint64_t)n_tokens);
+        int slot = (int)((mix64(h) + (uint64_t)smp) % (uint64_t)n_ids);
+        int32_t e = 0;
+        if (hipMemcpyAsync(&e, d_ids + (size_t)t * ids_token_stride + (size_t)slot * ids_id_stride, 4,
+                           hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            ++g_sc_fail;
+            continue;
+        }
+        if (e < 0 || e >= n_experts) continue;          // the kernel reports the id through the error word
+        const int t_out = t, slot_out = slot;
+        if (sentinel == 1) e = (e + 1) % n_experts;
+        if (sentinel == 2) slot = (slot + 1) % n_ids;
+        if (sentinel == 3) t = (t + 1) % n_tokens;
+        const uint8_t* xp = d_x + (size_t)t * x_token_stride + (size_t)(slot % x_rows) * x_id_stride;
+        const uint8_t* op = reinterpret_cast<const uint8_t*>(d_dst) + (size_t)t_out * dst_token_stride +
+                            (size_t)slot_out * dst_id_stride;
+        if (hipMemcpyAsync(x.data(), xp, (size_t)k * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipMemcpyAsync(out.data(), op, (size_t)rows * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipMemcpyAsync(wb.data(), bank + (size_t)e * expert_stride, wb.size(), hipMemcpyDeviceToHost, st) !=
+                hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            ++g_sc_fail;
+            continue;
+        }
+        host::quantize_act(qt, x.data(), k, act);
+        double num = 0.0, den = 0.0;
+        for (int r = 0; r < rows; ++r) {
+            const uint8_t* wr = wb.data() + (size_t)r * row_stride;
+            host::dequant_row(qt, wr, w.data(), k);
+            const double ref = host::ref_dot(qt, wr, w.data(), act, k);
+            const double err = (double)out[r] - ref;
+            num += err * err;
+            den += ref * ref;
+        }
+        (void)rb;
+        const double rel = den > 0.0 ? std::sqrt(num / den) : std::sqrt(num);
+        std::lock_guard<std::mutex> lk(g_sc_mu);
+        if (rel <= g_sc_tol) {
+            ++g_sc_ok;
+        } else {
+            if (g_sc_fail.load() == 0)
+                std::fprintf(stderr, "SABAH_SELFCHECK_FAIL call=%llu token=%d/%d slot=%d expert=%d rel_l2=%.3e\n",
+                             (unsigned long long)call_no, t_out, n_tokens, slot_out, e, rel);
+            ++g_sc_fail;
+        }
+        if (!(rel <= g_sc_max)) g_sc_max = rel;
+    }
+}
+
+// SABAH_LLAMA_STATUS_FILE: the snapshot rewritten after every v2 call, before
+// it returns (sabah_rt.cu:3418-3428), so a read after a request is exact.
+static void write_status_file() {
+    static const char* path = std::getenv("SABAH_LLAMA_STATUS_FILE");
+    if (!path || !*path) return;
+    char buf[1024];
+    if (sabah_rt_snapshot(buf, sizeof(buf)) != 0) return;
+    if (FILE* f = std::fopen(path, "wb")) {
+        std::fputs(buf, f);
+        std::fputc('\n', f);
+        std::fclose(f);
+    }
+}
+
+// SABAH_LLAMA_TRACE: the counters on stderr when the process exits
+// (sabah_rt.cu:3096-3188)
+static void report_trace_at_exit() {
+    if (!std::getenv("SABAH_LLAMA_TRACE")) return;
+    char buf[1024];
+    if (sabah_rt_snapshot(buf, sizeof(buf)) == 0) std::fprintf(stderr, "SABAH_SNAPSHOT %s\n", buf);
+    std::fprintf(stderr, "SABAH_DIAG calls=%llu tokens=%llu lookups=%llu overflow=0 verify_ok=%llu verify_fail=%llu\n",
+                 g_calls.load(), g_tokens.load(), g_lookups.load(), g_sc_ok.load(), g_sc_fail.load());
+}
+
+// Harness control of the self-check (the environment sets it at init): k
+// samples per call (0: off), the relative L2 tolerance, and the test-only
+// perturbation of the recomputation (0 none, 1 expert, 2 slot row, 3 token row).
+SABAH_API int sabah_rt_set_selfcheck(int k, double tol, int sentinel) {
+    if (k < 0 || !(tol > 0.0) || sentinel < 0 || sentinel > 3)
+        return fail("selfcheck: k %d >= 0, tol %g > 0 and sentinel %d in 0..3 expected", k, tol, sentinel);
+    std::lock_guard<std::mutex> lk(g_sc_mu);
+    g_sc_k.store(k);
+    g_sc_tol = tol;
+    g_sc_sentinel.store(sentinel);
+    g_sc_ok.store(0);
+    g_sc_fail.store(0);
+    g_sc_max = 0.0;
+    return 0;
+}
+
 SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, size_t row_stride, const void* d_x,
                                      size_t x_id_stride, int x_rows, size_t x_token_stride, const void* d_ids,
                                      size_t ids_id_stride, size_t ids_token_stride, int n_ids, int n_tokens,
@@ -968,6 +1113,10 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
         ++g_grouped_calls;
         g_tokens += (unsigned long long)n_tokens;
         g_lookups += (unsigned long long)n_tokens * (unsigned long long)n_ids;
+        selfcheck_call(bank, expert_stride, row_stride, static_cast<const uint8_t*>(d_x), x_id_stride, x_rows,
+                       x_token_stride, static_cast<const uint8_t*>(d_ids), ids_id_stride, ids_token_stride, n_ids,
+                       n_tokens, d_dst, dst_id_stride, dst_token_stride, rows, k, n_experts, qt, st);
+        write_status_file();
         return 0;
     }
 
@@ -1000,6 +1149,10 @@ SABAH_API int sabah_rt_mul_mat_id_v2(const void* source, size_t expert_stride, s
     ++g_calls;
     g_tokens += (unsigned long long)n_tokens;
     g_lookups += (unsigned long long)n_tokens * (unsigned long long)n_ids;
+    selfcheck_call(bank, expert_stride, row_stride, static_cast<const uint8_t*>(d_x), x_id_stride, x_rows,
+                   x_token_stride, static_cast<const uint8_t*>(d_ids), ids_id_stride, ids_token_stride, n_ids, n_tokens,
+                   d_dst, dst_id_stride, dst_token_stride, rows, k, n_experts, qt, st);
+    write_status_file();
     return 0;
 }
 
@@ -1028,13 +1181,18 @@ SABAH_API int sabah_rt_get_diag(unsigned long long* calls, unsigned long long* t
     if (calls) *calls = g_calls.load();
     if (tokens) *tokens = g_tokens.load();
     if (overflow) *overflow = 0;
-    if (verify_ok) *verify_ok = 0;
-    if (verify_fail) *verify_fail = 0;
+    if (verify_ok) *verify_ok = g_sc_ok.load();         // self-check samples within / beyond tolerance
+    if (verify_fail) *verify_fail = g_sc_fail.load();
     return 0;
 }
 
 SABAH_API int sabah_rt_snapshot(char* buf, size_t n) {
     if (!buf || n == 0) return fail("snapshot buffer is empty");
+    double sc_max;
+    {
+        std::lock_guard<std::mutex> lk(g_sc_mu);
+        sc_max = g_sc_max;
+    }
     size_t nbanks;
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -1044,10 +1202,11 @@ SABAH_API int sabah_rt_snapshot(char* buf, size_t n) {
                            "{\"calls\":%llu,\"empty_calls\":%llu,\"tokens\":%llu,\"lookups\":%llu,\"hits\":%llu,"
                            "\"misses\":0,\"evictions\":0,\"bytes_fetched\":0,\"resident_bytes\":%llu,"
                            "\"banks\":%zu,\"layer_calls\":%llu,\"grouped_calls\":%llu,\"scratch_bytes\":%zu,"
-                           "\"device\":%d,\"sentinel\":0}",
+                           "\"device\":%d,\"selfcheck_k\":%d,\"selfcheck_ok\":%llu,\"selfcheck_fail\":%llu,"
+                           "\"selfcheck_max_rel\":%.3e,\"sentinel\":%d}",
                            g_calls.load(), g_empty_calls.load(), g_tokens.load(), g_lookups.load(), g_lookups.load(),
                            resident_bytes(), nbanks, g_layer_calls.load(), g_grouped_calls.load(), g_scratch_total,
-                           g_device);
+                           g_device, g_sc_k.load(), g_sc_ok.load(), g_sc_fail.load(), sc_max, g_sc_sentinel.load());
     return (w < 0 || (size_t)w >= n) ? fail("snapshot buffer too small") : 0;
 }
 
@@ -1083,29 +1242,14 @@ SABAH_API int sabah_dequant(const void* d_src, float* d_dst, int qt, int n_rows,
     return ck(hipStreamSynchronize(g_stream), "dequant sync") ? 0 : -1;
 }
 
-// n elements of type qt at host address src, decoded on the device by the same
-// decoders (sabah_dequant) into n floats at host address dst; synchronous.
-// Callable before sabah_rt_init, as the reference's host routine is: the
-// library is then initialised on the current HIP device.
+// n elements of type qt at host address src decoded on the host into n floats
+// at dst (sabah_rt.cu:3845-3849): no GPU and no initialisation; the values are
+// bit-identical to sabah_dequant's.
 SABAH_API int sabah_rt_host_dequant(const void* src, float* dst, int qt, int n) {
     if (!src || !dst || n <= 0) return fail("invalid host dequant arguments");
-    if (!supported_weight_type(qt) || row_bytes(qt, n) == 0)
+    if (!host::dequant_row(qt, static_cast<const uint8_t*>(src), dst, n))
         return fail("host dequant: unsupported type %d or %d elements", qt, n);
-    if (g_device < 0) {
-        int dev = 0;
-        if (!ck(hipGetDevice(&dev), "host dequant: current device") || sabah_rt_init(dev) != 0) return -1;
-    }
-    const size_t nb = row_bytes(qt, n);
-    uint8_t* d = nullptr;
-    if (!ck(hipMalloc(reinterpret_cast<void**>(&d), nb + sizeof(float) * (size_t)n + 256), "host dequant buffers"))
-        return -1;
-    float* df = reinterpret_cast<float*>(d + ((nb + 255) & ~(size_t)255));
-    int rc = ck(hipMemcpy(d, src, nb, hipMemcpyHostToDevice), "host dequant upload") ? 0 : -1;
-    if (rc == 0) rc = sabah_dequant(d, df, qt, 1, n);
-    if (rc == 0 && !ck(hipMemcpy(dst, df, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost), "host dequant download"))
-        rc = -1;
-    (void)hipFree(d);
-    return rc;
+    return 0;
 }
 
 SABAH_API int sabah_quantize_act(const float* d_x, void* d_y, int qt, int n_rows, int k, void* stream) {

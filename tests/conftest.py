@@ -25,6 +25,15 @@ def gpu_available() -> bool:
 
 
 @pytest.fixture(scope="session")
+def hip_rt_cpu():
+    """The HIP runtime library loaded for its host-only entry points (no GPU,
+    no sabah_rt_init).  Fails loudly if the library is missing."""
+    from sabah.runtime import rt
+    rt.lib()
+    return rt
+
+
+@pytest.fixture(scope="session")
 def hip_rt():
     """The HIP runtime, initialised on device 0.  Fails loudly if the library is missing."""
     if not gpu_available():
