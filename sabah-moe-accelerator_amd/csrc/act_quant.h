@@ -228,16 +228,17 @@ struct ActRegs {
     Act16 a[ROUNDS];
 };
 
-// The batch is handled by threads w0 .. blockDim.x-1 (whole 16-lane rows).
+// The batch is handled by threads w0 .. NT-1 (whole 16-lane rows) of a
+// workgroup of NT threads (a constant, so no kernel reads its launch size).
 __device__ inline bool act_vec(const ActBatch& B) {
     return (reinterpret_cast<uintptr_t>(B.x) & 15) == 0 && (B.row_stride & 3) == 0;
 }
 
 // every lane loads in every round (slots past the batch re-load its last
 // chunk-row and skip the quantisation)
-template <int ROUNDS>
+template <int ROUNDS, int NT>
 __device__ inline void act_prefetch(const ActBatch& B, ActRegs<ROUNDS>& R, int w0 = 0) {
-    const int slot = ((int)threadIdx.x - w0) >> 4, nslots = ((int)blockDim.x - w0) >> 4, l = threadIdx.x & 15;
+    const int slot = ((int)threadIdx.x - w0) >> 4, nslots = (NT - w0) >> 4, l = threadIdx.x & 15;
     const int nch = (B.k + 255) / 256, nq = B.n_rows * nch;
     const float rcp_nch = __builtin_amdgcn_rcpf((float)nch);
     const bool vec = act_vec(B);
@@ -261,9 +262,9 @@ __device__ inline void quant_chunk(const ActBatch& B, const Act16& a_in, int q, 
     else row16_quant_q8_0(a, c, B.act + r * B.act_stride, L, B.at == QT_Q8_1);
 }
 
-template <int ROUNDS>
+template <int ROUNDS, int NT>
 __device__ inline void act_quantize(const ActBatch& B, const ActRegs<ROUNDS>& R, int w0 = 0) {
-    const int slot = ((int)threadIdx.x - w0) >> 4, nslots = ((int)blockDim.x - w0) >> 4, l = threadIdx.x & 15;
+    const int slot = ((int)threadIdx.x - w0) >> 4, nslots = (NT - w0) >> 4, l = threadIdx.x & 15;
     const int nch = (B.k + 255) / 256, nq = B.n_rows * nch;
 #pragma unroll
     for (int i = 0; i < ROUNDS; ++i) {
@@ -280,12 +281,12 @@ __device__ inline void act_quantize(const ActBatch& B, const ActRegs<ROUNDS>& R,
     }
 }
 
-// All threads of the workgroup: quantise one row of k floats at x into act.
+// All threads of a 256-thread workgroup: quantise one row of k floats at x into act.
 __device__ inline void wg_quantize_row(const float* __restrict__ x, int k, int at, uint8_t* act) {
     const ActBatch B{x, 0, 1, k, at, act, 0};
     ActRegs<1> R;
-    act_prefetch<1>(B, R);
-    act_quantize<1>(B, R);
+    act_prefetch<1, 256>(B, R);
+    act_quantize<1, 256>(B, R);
 }
 
 }  // namespace sabah

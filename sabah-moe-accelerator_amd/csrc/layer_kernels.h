@@ -295,14 +295,14 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     float* o = d.out + row0;
     if (!ok) {
         if (threadIdx.x == 0) *reinterpret_cast<volatile unsigned int*>(d.err) = kErrLayerWait;
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) o[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += NT) o[r] = __builtin_nanf("");
         if (threadIdx.x == 0) *my = target;
         return;
     }
     const ActBatch hb{d.h, (size_t)d.d_ff, d.n_slots, d.d_ff, act_type(QT), act, P.act_bytes};
     ActRegs<1> ha;
-    act_prefetch<1>(hb, ha);
-    act_quantize<1>(hb, ha);
+    act_prefetch<1, NT>(hb, ha);
+    act_quantize<1, NT>(hb, ha);
     __syncthreads();                                        // q8 h rows ready
     if (has) {
         const uint8_t* arow = act + ut * P.act_bytes;
@@ -319,17 +319,17 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     __syncthreads();
     if (bad) {
         flag_error(d.err);
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) o[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += NT) o[r] = __builtin_nanf("");
         if (threadIdx.x == 0) *my = target;
         return;
     }
     // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
-    for (int i = i0; i < d.n_slots * d.R; i += blockDim.x) {
+    for (int i = i0; i < d.n_slots * d.R; i += NT) {
         const int sl = div_small(i, rcp_r);
         if (i - sl * d.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : wt[sl]);
     }
     __syncthreads();
-    for (int r = r0; r < nrows; r += blockDim.x) {
+    for (int r = r0; r < nrows; r += NT) {
         float acc = ordered_sum_from(part[r * NCB], part + r * NCB, d.R * NCB, d.n_slots);
         const size_t q = (size_t)row0 + r;
         if (d.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : d.shared[q]);

@@ -553,12 +553,12 @@ __global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_mmid(MmidArgs 
     // id is a scalar load with its own counter
     const ActBatch xb{xr, 0, 1, a.k, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
-    act_prefetch<kRoundsX>(xb, xa);
+    act_prefetch<kRoundsX, kThreads>(xb, xa);
     const TableRegs<QT, kThreads> gr = load_tables<QT, kThreads>((int)threadIdx.x);
     const uint8_t* w = expert_ptr(a.W, a.rt, t, i, a.n_ids);
     if (w == nullptr) {   // uniform across the workgroup
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) out[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += kThreads) out[r] = __builtin_nanf("");
         return;
     }
     w += (size_t)row0 * a.row_stride;
@@ -567,14 +567,14 @@ __global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_mmid(MmidArgs 
     TileRun<QT> S{TileWalk<QT>(packed ? 1 : nrows, packed ? nrows : 1, rb, a.k)};
     tiles_begin(S, tile_ptr);
     store_tables<QT, kThreads>(tabs, gr, (int)threadIdx.x);
-    act_quantize<kRoundsX>(xb, xa);
+    act_quantize<kRoundsX, kThreads>(xb, xa);
     // the gate's loads come after the weights', so it waits for what the
     // staging waits for anyway; the staging's barrier publishes the sums
     __shared__ float sg_sums[4];
     if (a.sg_w) gate_dot_part(a.sg_w, a.sg_x + (size_t)t * a.sg_n, a.sg_n, sg_sums);
     tiles_finish(S, tabs, stage, leads, a.k, act, 0, packed ? a.R : 1, part);
     const float sg = a.sg_w ? sigmoid_f32(gate_dot_total(sg_sums)) : 1.0f;
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+    for (int r = threadIdx.x; r < nrows; r += kThreads) {
         const float y = row_sum(part + r * NCB, NCB);
         out[r] = a.sg_w ? __fmul_rn(y, sg) : y;
     }
@@ -611,13 +611,13 @@ __global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUp
     float* part = reinterpret_cast<float*>(smem + P.off_part);
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
-    act_prefetch<kRoundsX>(xb, xa);
+    act_prefetch<kRoundsX, kThreads>(xb, xa);
     const TableRegs<QT, kThreads> gr = load_tables<QT, kThreads>((int)threadIdx.x);
     const uint8_t *wg, *wu;
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) h[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += kThreads) h[r] = __builtin_nanf("");
         return;
     }
     wg += (size_t)row0 * rb;
@@ -626,9 +626,9 @@ __global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUp
     TileRun<QT> S{TileWalk<QT>(2, nrows, rb, a.d_model)};
     tiles_begin(S, tile_ptr);
     store_tables<QT, kThreads>(tabs, gr, (int)threadIdx.x);
-    act_quantize<kRoundsX>(xb, xa);
+    act_quantize<kRoundsX, kThreads>(xb, xa);
     tiles_finish(S, tabs, stage, leads, a.d_model, act, 0, a.R, part);
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+    for (int r = threadIdx.x; r < nrows; r += kThreads) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
         h[r] = __fmul_rn(silu_f32(g), up);
@@ -712,14 +712,14 @@ __device__ inline void gate_up_rounds_tile(const GateUpArgs& a, int t, int s, in
     float* part = reinterpret_cast<float*>(smem + P.off_part);
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
-    act_prefetch<kRoundsX>(xb, xa);
+    act_prefetch<kRoundsX, NT>(xb, xa);
     GridRegs<NT> gr;
     if constexpr (QT == QT_IQ3_S) gr = load_grid_regs<NT>((int)threadIdx.x);
     const uint8_t *wg, *wu;
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) store_h(h + r, __builtin_nanf(""), publish);
+        for (int r = threadIdx.x; r < nrows; r += NT) store_h(h + r, __builtin_nanf(""), publish);
         return;
     }
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63u);
@@ -746,7 +746,7 @@ __device__ inline void gate_up_rounds_tile(const GateUpArgs& a, int t, int s, in
     };
     issue_round(0);
     if constexpr (QT == QT_IQ3_S) store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
-    act_quantize<kRoundsX>(xb, xa);
+    act_quantize<kRoundsX, NT>(xb, xa);
 #pragma unroll
     for (int rd = 1; rd < RD; ++rd) issue_round(rd);
     __syncthreads();                                        // activations and tables ready
@@ -792,7 +792,7 @@ __device__ inline void gate_up_rounds_tile(const GateUpArgs& a, int t, int s, in
         }
     }
     __syncthreads();                                        // partials complete
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+    for (int r = threadIdx.x; r < nrows; r += NT) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
         store_h(h + r, __fmul_rn(silu_f32(g), up), publish);
@@ -871,7 +871,7 @@ __global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_down_combine(DownArg
 #pragma unroll
         for (int i = 0; i < HQN; ++i) hqv[i] = src[min((int)threadIdx.x + NT * i, hq_chunks - 1)];
     } else {
-        act_prefetch<RH>(hb, ha);
+        act_prefetch<RH, NT>(hb, ha);
     }
     // the epilogue's own inputs (router weight of this thread's first
     // (slot, row) and this thread's row of shared / resid / out) are read now,
@@ -897,22 +897,22 @@ __global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_down_combine(DownArg
         for (int i = 0; i < HQN; ++i)
             if ((int)threadIdx.x + NT * i < hq_chunks) reinterpret_cast<u32x4*>(act)[threadIdx.x + NT * i] = hqv[i];
     } else {
-        act_quantize<RH>(hb, ha);
+        act_quantize<RH, NT>(hb, ha);
     }
     tiles_finish(S, tabs, stage, leads, a.d_ff, act, P.act_bytes, a.R, part);
     float* o = a.out + (size_t)t * a.d_model + row0;
     if (bad) {
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) o[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += NT) o[r] = __builtin_nanf("");
         return;
     }
     // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
-    for (int i = i0; i < a.n_slots * a.R; i += blockDim.x) {
+    for (int i = i0; i < a.n_slots * a.R; i += NT) {
         const int sl = div_small(i, rcp_r);
         if (i - sl * a.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : wt[sl]);
     }
     __syncthreads();
-    for (int r = r0; r < nrows; r += blockDim.x) {
+    for (int r = r0; r < nrows; r += NT) {
         const size_t q = (size_t)t * a.d_model + row0 + r;
         float acc = ordered_sum_from(part[r * NCB], part + r * NCB, a.R * NCB, a.n_slots);
         if (a.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : a.shared[q]);
@@ -933,7 +933,7 @@ __global__ __launch_bounds__(kThreads) void k_dequant(const uint8_t* __restrict_
     store_tables<QT, kThreads>(smem, load_tables<QT, kThreads>((int)threadIdx.x), (int)threadIdx.x);
     __syncthreads();
     const int NUS = units_per_row(QT, k);
-    const long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long u = (long long)blockIdx.x * kThreads + threadIdx.x;
     if (u >= (long long)n_rows * NUS) return;
     const long long r = u / NUS;
     const int us = (int)(u % NUS);
@@ -954,17 +954,17 @@ __global__ __launch_bounds__(kThreads) void k_quantize_act_ggml(const float* __r
                                                                 int k, int at) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int r = blockIdx.x;
-    wg_quantize_row(x + (size_t)r * k, k, at, smem);   // blockDim.x == 256: sixteen row-slots
+    wg_quantize_row(x + (size_t)r * k, k, at, smem);   // 256 threads: sixteen row-slots
     __syncthreads();
     const ActLayout L(k, at);
     const int qb = block_elems(at), bb = block_bytes(at), nb = k / qb;
     uint8_t* yr = y + (size_t)r * nb * bb;
     const float* d = reinterpret_cast<const float*>(smem + L.off_d);
-    for (int q = threadIdx.x; q < k; q += blockDim.x) {
+    for (int q = threadIdx.x; q < k; q += kThreads) {
         const int b = q / qb, j = q - b * qb;
         yr[(size_t)b * bb + (at == QT_Q8_K ? 4 : at == QT_Q8_1 ? 4 : 2) + j] = smem[(q >> 8) * kActChunkStride + (q & 255)];
     }
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+    for (int b = threadIdx.x; b < nb; b += kThreads) {
         if (at == QT_Q8_K) {
             const float dv = d[b];
             memcpy(yr + (size_t)b * bb, &dv, 4);
