@@ -186,6 +186,49 @@ __device__ inline void store_flag_line(uint32_t* line, uint32_t v) {
     if (threadIdx.x < kLine) line[threadIdx.x] = v;
 }
 
+// Wave 0 of a down workgroup waits for h: its XCD's leader (whose ticket
+// swap returned another launch's number) for every gate/up flag, then sets
+// the XCD's flag; a follower for that flag.  True once h is complete, false
+// when the wait ran out.
+__device__ inline bool layer_wait_h(const LayerArgs& a, uint32_t target, unsigned x, uint32_t ticket) {
+    uint32_t* xf = a.sync + kSyncX + kLine * x;
+    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)ticket) != target) {   // this XCD's leader
+        const bool done = wait_flags(a.sync, a.n_g, target + a.wait_skew, xf, a.idle_ticks);
+        if (done) {
+            if (a.xcd_groups) {
+                if (threadIdx.x == 0) __hip_atomic_store(xf, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                store_flag_line(xf, target);
+            }
+        }
+        return done;
+    }
+    return wait_line(xf, target + a.wait_skew, a.idle_ticks);
+}
+
+// The down workgroups' epilogue (k_down_combine's order): y_s[r] * w_s of
+// every (slot, row) in parallel, kept in the row's first partial, then each
+// row's slot-ordered sum, shared row, residual and accumulator.  w0, sh0,
+// rs0, ac0: this thread's prefetched router weight and row values.
+__device__ inline void layer_combine(const DownArgs& d, int NCB, int nrows, float* part, float* o, size_t row0,
+                                     float w0, float sh0, float rs0, float ac0, int NT) {
+    const float rcp_r = __builtin_amdgcn_rcpf((float)d.R);
+    const int i0 = (int)threadIdx.x, r0 = (int)threadIdx.x;
+    for (int i = i0; i < d.n_slots * d.R; i += NT) {
+        const int sl = div_small(i, rcp_r);
+        if (i - sl * d.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : d.w[sl]);
+    }
+    __syncthreads();
+    for (int r = r0; r < nrows; r += NT) {
+        float acc = ordered_sum_from(part[r * NCB], part + r * NCB, d.R * NCB, d.n_slots);
+        const size_t q = row0 + r;
+        if (d.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : d.shared[q]);
+        if (d.resid) acc = __fadd_rn(r == r0 ? rs0 : d.resid[q], acc);
+        if (d.accumulate) acc = __fadd_rn(r == r0 ? ac0 : o[r], acc);
+        o[r] = acc;
+    }
+}
+
 template <int NT>
 __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     constexpr int QT = QT_IQ3_S;
@@ -275,20 +318,7 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
     }
     __shared__ int ok;
     if (threadIdx.x < 64) {
-        uint32_t* xf = a.sync + kSyncX + kLine * x;
-        bool done;
-        if ((uint32_t)__builtin_amdgcn_readfirstlane((int)ticket) != target) {   // this XCD's leader
-            done = wait_flags(a.sync, a.n_g, target + a.wait_skew, xf, a.idle_ticks);
-            if (done) {
-                if (a.xcd_groups) {
-                    if (threadIdx.x == 0) __hip_atomic_store(xf, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
-                    store_flag_line(xf, target);
-                }
-            }
-        } else {
-            done = wait_line(xf, target + a.wait_skew, a.idle_ticks);
-        }
+        const bool done = layer_wait_h(a, target, x, ticket);
         if (threadIdx.x == 0) ok = done ? 1 : 0;
     }
     __syncthreads();                                        // flags seen
@@ -323,20 +353,7 @@ __global__ __launch_bounds__(NT) void k_layer_decode(LayerArgs a) {
         if (threadIdx.x == 0) *my = target;
         return;
     }
-    // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
-    for (int i = i0; i < d.n_slots * d.R; i += NT) {
-        const int sl = div_small(i, rcp_r);
-        if (i - sl * d.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : wt[sl]);
-    }
-    __syncthreads();
-    for (int r = r0; r < nrows; r += NT) {
-        float acc = ordered_sum_from(part[r * NCB], part + r * NCB, d.R * NCB, d.n_slots);
-        const size_t q = (size_t)row0 + r;
-        if (d.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : d.shared[q]);
-        if (d.resid) acc = __fadd_rn(r == r0 ? rs0 : d.resid[q], acc);
-        if (d.accumulate) acc = __fadd_rn(r == r0 ? ac0 : o[r], acc);
-        o[r] = acc;
-    }
+    layer_combine(d, NCB, nrows, part, o, (size_t)row0, w0, sh0, rs0, ac0, NT);
     if (threadIdx.x == 0) *my = target;
 }
 

@@ -597,16 +597,26 @@ struct GateUpArgs {
 
 __device__ inline float silu_f32(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf(-v))); }
 
+// h row r of a workgroup: a plain store, or (publish) an agent-scope store
+// written through to memory, so a workgroup of the same grid on another XCD
+// can read it once this one has waited for its stores and set its flag
+__device__ inline void store_h(float* p, float v, bool publish) {
+    if (publish) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
+// One workgroup of k_gate_up (kThreads threads): token t, slot s, rows
+// row0 .. row0 + R of gate and up, h = silu(g) * u to hbase (laid out as
+// a.h), published with store_h when `publish`.  tabs, leads, stage: the
+// static LDS; smem: the plan's dynamic LDS.
 template <int QT>
-__global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUpArgs a) {
-    SABAH_STATIC_LDS(QT)
-    extern __shared__ __align__(16) uint8_t smem[];
+__device__ inline void gate_up_tile(const GateUpArgs& a, int t, int s, int row0, uint8_t* tabs, int* leads,
+                                    uint8_t* stage, uint8_t* smem, bool publish, float* hbase) {
     const int NCB = contribs_per_row(QT, a.d_model);
     const Plan P = make_plan(QT, a.d_model, 1, 2 * a.R * NCB);
-    const int t = blockIdx.z, s = blockIdx.y, row0 = blockIdx.x * a.R;
     const int nrows = min(a.R, a.d_ff - row0);
     const size_t rb = row_bytes(QT, a.d_model);
-    float* h = a.h + ((size_t)t * a.n_slots + s) * a.d_ff + row0;
+    float* h = hbase + ((size_t)t * a.n_slots + s) * a.d_ff + row0;
     uint8_t* act = smem + P.off_act;
     float* part = reinterpret_cast<float*>(smem + P.off_part);
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
@@ -617,7 +627,7 @@ __global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUp
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += kThreads) h[r] = __builtin_nanf("");
+        for (int r = threadIdx.x; r < nrows; r += kThreads) store_h(h + r, __builtin_nanf(""), publish);
         return;
     }
     wg += (size_t)row0 * rb;
@@ -631,8 +641,15 @@ __global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUp
     for (int r = threadIdx.x; r < nrows; r += kThreads) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
-        h[r] = __fmul_rn(silu_f32(g), up);
+        store_h(h + r, __fmul_rn(silu_f32(g), up), publish);
     }
+}
+
+template <int QT>
+__global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUpArgs a) {
+    SABAH_STATIC_LDS(QT)
+    extern __shared__ __align__(16) uint8_t smem[];
+    gate_up_tile<QT>(a, blockIdx.z, blockIdx.y, blockIdx.x * a.R, tabs, leads, stage, smem, false, a.h);
 }
 
 // ---------------------------------------------------------------------------
@@ -683,14 +700,6 @@ __host__ __device__ inline int rows_gate_up_rounds(int qt, int d_model) { return
 constexpr int kGateUpRoundThreads = 2 * kThreads;
 // dynamic LDS of a launch: the plan, then the staging regions
 __host__ __device__ inline int gate_up_rounds_lds(const Plan& P, int stage) { return align16i(P.bytes) + stage; }
-
-// h row r of a workgroup: a plain store, or (publish) an agent-scope store
-// written through to memory, so a workgroup of the same grid on another XCD
-// can read it once this one has waited for its stores and set its flag
-__device__ inline void store_h(float* p, float v, bool publish) {
-    if (publish) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
-}
 
 // One workgroup of k_gate_up_rounds: token t, slot s, rows row0 .. row0 + R.
 // tabs: the IQ3_S table (kLdsTables bytes); smem: the plan's dynamic LDS;

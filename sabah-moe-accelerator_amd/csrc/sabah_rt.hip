@@ -1551,22 +1551,37 @@ static int shared_expert(const sabah_moe_layer_desc* L, const float* d_x, int n_
 // On the 48-layer decode (13.5 MB of gate/up weights, 180 ticks) the layer
 // measured 11.7 us against 12.7 us without the wait (per-workgroup stamps,
 // same box, interleaved launches); 150-200 ticks were best.
-static uint32_t layer_down_delay(int n_used, int D, int F) {
-    const size_t g_bytes = (size_t)n_used * 2 * F * row_bytes(QT_IQ3_S, D);
+static uint32_t layer_down_delay(int qt, int n_used, int D, int F) {
+    const size_t g_bytes = (size_t)n_used * 2 * F * row_bytes(qt, D);
     return (uint32_t)std::min<size_t>(g_bytes / 75000, 1000);
+}
+
+// The layer's lockstep arguments for a fused launch (the flags cleared first
+// when an earlier wait ran out)
+static LayerArgs layer_args(const GateUpArgs& gu, const DownArgs& dn, int qt, int n_g, int g_tiles, int n_d,
+                            hipStream_t st) {
+    uint32_t* sync = g_layer_sync[g_device];
+    if (g_sync_reset_pending.exchange(false)) launch_kernel(KK_LAYER, k_clear_sync, dim3(1), dim3(256), 0, st, sync);
+    const bool wait_test = g_layer_wait_test.exchange(false);
+    // the timeout test gives up after 2 ms without progress rather than 50
+    return LayerArgs{gu, dn, n_g, g_tiles, n_d, sync, wait_test ? 1u : 0u,
+                     layer_down_delay(qt, dn.n_slots, dn.d_model, dn.d_ff),
+                     wait_test ? 200000u : (uint32_t)kLayerIdleTicks, g_layer_xcd_groups.load()};
 }
 
 // A one-token IQ3_S layer as one launch (k_layer_decode) when it applies:
 // returns 1 when launched, 0 when the two-kernel form must run, -1 on error.
+// (The same fusion for Q8_0 / Q4_K / Q5_K / Q6_K layers, down rows staged in
+// one pass before the wait, measured slower than their two kernels on the
+// 1-token Q8_0 E=8 and Q4_K E=128 layers: 12.1 against 11.4 us and 15.4
+// against 13.0 us per layer; there the hand-over costs more than the
+// second launch and the down weights' load it would hide.)
 static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, const ExpertSrc& DS, const Routing& rt,
                        int n_used, const float* w, const float* shared, const float* resid, float* out,
                        hipStream_t st) {
     constexpr int QT = QT_IQ3_S;
     if (!g_layer_fusion.load() || g_device < 0 || g_device >= kMaxDevices || !g_layer_sync[g_device]) return 0;
-    if (L->qt_gate != QT || L->qt_up != QT || L->qt_down != QT) return 0;
     const int D = L->d_model, F = L->d_ff;
-    if (!gate_up_rounds_ok(QT, D) || gu.R != rows_gate_up_rounds(QT, D) || F % 256) return 0;
-    static_assert(GateUpRounds<QT, kLayerThreads, 2>::STAGE <= kStageBytes, "gate/up rounds stage in the static area");
     DownArgs dn{};
     dn.D = DS;
     dn.rt = rt;
@@ -1578,8 +1593,11 @@ static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, cons
     dn.n_slots = n_used;
     dn.d_model = D;
     dn.d_ff = F;
-    dn.R = rows_down(QT, F, n_used, D, 1);
     dn.err = g_err_dev;
+    if (L->qt_gate != QT || L->qt_up != QT || L->qt_down != QT) return 0;
+    if (!gate_up_rounds_ok(QT, D) || gu.R != rows_gate_up_rounds(QT, D) || F % 256) return 0;
+    static_assert(GateUpRounds<QT, kLayerThreads, 2>::STAGE <= kStageBytes, "gate/up rounds stage in the static area");
+    dn.R = rows_down(QT, F, n_used, D, 1);
     const int g_tiles = (F + gu.R - 1) / gu.R;
     const int n_g = g_tiles * n_used, n_d = (D + dn.R - 1) / dn.R;
     if (n_g > kSyncG || n_d > kSyncD) return 0;
@@ -1591,12 +1609,7 @@ static int layer_fused(const sabah_moe_layer_desc* L, const GateUpArgs& gu, cons
     const int dyn = layer_dyn_lds(gu, dn);
     if (StaticLds<QT>::BYTES + dyn + 64 > g_max_lds) return 0;
     if (!ck(fit_lds(k_layer_decode<kLayerThreads>, dyn, StaticLds<QT>::BYTES + dyn), "fused layer LDS")) return -1;
-    uint32_t* sync = g_layer_sync[g_device];
-    if (g_sync_reset_pending.exchange(false)) launch_kernel(KK_LAYER, k_clear_sync, dim3(1), dim3(256), 0, st, sync);
-    const bool wait_test = g_layer_wait_test.exchange(false);
-    // the timeout test gives up after 2 ms without progress rather than 50
-    LayerArgs a{gu, dn, n_g, g_tiles, n_d, sync, wait_test ? 1u : 0u, layer_down_delay(n_used, D, F),
-                wait_test ? 200000u : (uint32_t)kLayerIdleTicks, g_layer_xcd_groups.load()};
+    const LayerArgs a = layer_args(gu, dn, QT, n_g, g_tiles, n_d, st);
     launch_kernel(KK_LAYER, k_layer_decode<kLayerThreads>, dim3((unsigned)(n_g + n_d)), dim3(kLayerThreads), dyn, st, a);
     return ck(hipGetLastError(), "fused layer launch") ? 1 : -1;
 }

@@ -44,13 +44,13 @@ def launches(hip_rt, kind):
     return hip_rt.kernel_timing(kind)[1]
 
 
-def make_bank(orc, rng, E, D, F, n_layers=1):
+def make_bank(orc, rng, E, D, F, n_layers=1, qt=IQ3_S):
     from sabah.runtime.bank import ExpertBank
-    bank = ExpertBank(n_layers, E, D, F, {"gate": IQ3_S, "up": IQ3_S, "down": IQ3_S}, device="cuda:0")
+    bank = ExpertBank(n_layers, E, D, F, {"gate": qt, "up": qt, "down": qt}, device="cuda:0")
     raws = {}
     for l in range(n_layers):
         for role, (rows, cols) in {"gate": (F, D), "up": (F, D), "down": (D, F)}.items():
-            raws[(l, role)] = orc.quantize_weights(IQ3_S, (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32))
+            raws[(l, role)] = orc.quantize_weights(qt, (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32))
             bank.load(l, role, raws[(l, role)])
     return bank, raws
 
