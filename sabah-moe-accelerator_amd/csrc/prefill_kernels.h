@@ -465,6 +465,42 @@ __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int
     }
 }
 
+// One IQ3_S block of the lane's row decoded once into MFMA B operands (its
+// eight sub-blocks), for a wave that runs the same rows against several pair
+// tiles: each tile then costs only its MFMAs and the block sum.
+struct Iq3sBlockOps {
+    long B[8];
+    uint32_t sc, d;
+};
+__device__ inline void iq3s_block_ops(const uint8_t* unit, const uint8_t* tabs, int q, Iq3sBlockOps& O) {
+    Iq3sQuarter F;
+    iq3s_quarter_fields(unit, q, F);
+#pragma unroll
+    for (int sub = 0; sub < 8; ++sub) O.B[sub] = iq3s_quarter_operand(F, tabs, sub, q);
+    O.sc = F.sc;
+    O.d = F.d;
+}
+// mfma_blocks' IQ3_S block (one block, the same integer sums and fp32 steps)
+// from operands decoded by iq3s_block_ops
+__device__ inline void mfma_block_iq3s_ops(const Iq3sBlockOps& O, const XRegs<1>& R, bool valid, int q, float (&c)[4]) {
+    const v4i32 z = {0, 0, 0, 0};
+    const float dxv = valid ? R.dx[0] : 0.0f;
+    int bs[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int sub = 0; sub < 8; ++sub) {
+        const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(valid ? R.X[0][sub] : 0, O.B[sub], z, 0, 0, 0);
+        const int ls = 2 * (int)((O.sc >> (4 * sub)) & 15u) + 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bs[i] += __mul24(ls, d[i]);
+        if (sub == 3)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(bs[i]));
+    }
+    const float dw = h2f(O.d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = __fmul_rn(__fmul_rn(dw, __shfl(dxv, 4 * q + i)), (float)bs[i]);
+}
+
 // Staging of a grouped workgroup's weights: n_reg regions (matrices) of
 // `bytes` contiguous bytes each, loaded as aligned 16-byte chunks by the NT
 // threads (NL loads each; loads past the last chunk repeat it) and stored in
@@ -535,8 +571,10 @@ __host__ __device__ constexpr int group_cap(int rows, int rb) { return (rows * r
 // pair tile's activations for a block are loaded by one wave, once (the
 // loads of 16 rows x 8 bytes each are what a workgroup's start waits on);
 // up to four blocks, wave w takes block w & 3 of matrix w >> 2.  Each wave
-// runs its rows against every 16-pair tile of the expert, decoding the
-// staged rows into MFMA operands as it goes; the block results meet in LDS
+// runs its rows against every 16-pair tile of the expert: IQ3_S rows are
+// decoded into MFMA operands once, before the first tile, and kept in
+// registers for the rest (an expert with 95 pairs has six tiles); the other
+// formats decode the staged rows per tile.  The block results meet in LDS
 // and are summed in block order before SwiGLU.  The activation rows are the pairs' rows in group order (k_quant_rows
 // with the grouping as its gather), so a pair tile's activations load from
 // the group offset alone, at the start.
@@ -621,6 +659,14 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
     auto rstride = [&](int lead) { return GuStage<QT>::PAD ? stage_row_stride((int)rb, lead) : (int)rb; };
     const uint8_t* rowp = stage + GuStage<QT>::CAP * m + leads[m] + r * rstride(leads[m]);
     const uint8_t* rowp1 = stage + GuStage<QT>::CAP + leads[1] + r * rstride(leads[1]);
+    // IQ3_S: the wave's block of each of its matrices decoded once, for every pair tile
+    Iq3sBlockOps O0, O1;
+    if constexpr (QT == QT_IQ3_S) {
+        if (b < nb) {
+            iq3s_block_ops(rowp + UnitFmt<QT>::BYTES * b, tabs, q, O0);
+            if (both) iq3s_block_ops(rowp1 + UnitFmt<QT>::BYTES * b, tabs, q, O1);
+        }
+    }
     for (int pt = 0; pt < n_e; pt += kPairTile) {
         const int cnt = min(kPairTile, n_e - pt);
         const bool valid = j < cnt;
@@ -629,10 +675,12 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
         const int pdst = MMID && threadIdx.x < 256 ? a.pair_of[g0 + pt + min((int)(threadIdx.x & 15u), cnt - 1)] : 0;
         if (b < nb) {
             float c[1][4];
-            mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
+            if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O0, XR, valid, q, c[0]);
+            else mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
             *reinterpret_cast<float4*>(&part[m][b][r][part_col(r, 4 * q)]) = make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
             if (both) {
-                mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
+                if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O1, XR, valid, q, c[0]);
+                else mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
                 *reinterpret_cast<float4*>(&part[1][b][r][part_col(r, 4 * q)]) =
                     make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
             }
