@@ -884,15 +884,21 @@ __global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_down_combine(DownArg
     }
     // the epilogue's own inputs (router weight of this thread's first
     // (slot, row) and this thread's row of shared / resid / out) are read now,
-    // so their latency hides behind the expert loads
+    // so their latency hides behind the expert loads -- except in Q6_K's
+    // q8-h form, where the four registers held across the decode loop spill
+    // (the epilogue then reads them itself)
+    constexpr bool EARLY = !(QT == QT_Q6_K && HQ);
     const float* wt = a.w + (size_t)t * a.n_slots;
     const float rcp_r = __builtin_amdgcn_rcpf((float)a.R);
     const int i0 = (int)threadIdx.x, r0 = (int)threadIdx.x;
-    const float w0 = i0 < a.n_slots * a.R ? wt[div_small(i0, rcp_r)] : 0.0f;
     const size_t orow = (size_t)t * a.d_model + row0 + r0;
-    const float sh0 = a.shared && r0 < nrows ? a.shared[orow] : 0.0f;
-    const float rs0 = a.resid && r0 < nrows ? a.resid[orow] : 0.0f;
-    const float ac0 = a.accumulate && r0 < nrows ? a.out[orow] : 0.0f;
+    float w0 = 0.0f, sh0 = 0.0f, rs0 = 0.0f, ac0 = 0.0f;
+    if constexpr (EARLY) {
+        w0 = i0 < a.n_slots * a.R ? wt[div_small(i0, rcp_r)] : 0.0f;
+        sh0 = a.shared && r0 < nrows ? a.shared[orow] : 0.0f;
+        rs0 = a.resid && r0 < nrows ? a.resid[orow] : 0.0f;
+        ac0 = a.accumulate && r0 < nrows ? a.out[orow] : 0.0f;
+    }
     const TableRegs<QT, NT> gr = load_tables<QT, NT>((int)threadIdx.x);
     const uint8_t* e = resolve_slot_word(a.D, a.rt, sw);
     const bool bad = __any(e == nullptr);
@@ -918,15 +924,17 @@ __global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_down_combine(DownArg
     // y_s[r] * w_s of every (slot, row) in parallel, kept in the row's first partial
     for (int i = i0; i < a.n_slots * a.R; i += NT) {
         const int sl = div_small(i, rcp_r);
-        if (i - sl * a.R < nrows) part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), i == i0 ? w0 : wt[sl]);
+        if (i - sl * a.R < nrows)
+            part[i * NCB] = __fmul_rn(row_sum(part + i * NCB, NCB), EARLY && i == i0 ? w0 : wt[sl]);
     }
     __syncthreads();
     for (int r = r0; r < nrows; r += NT) {
         const size_t q = (size_t)t * a.d_model + row0 + r;
+        const bool first = EARLY && r == r0;
         float acc = ordered_sum_from(part[r * NCB], part + r * NCB, a.R * NCB, a.n_slots);
-        if (a.shared) acc = __fadd_rn(acc, r == r0 ? sh0 : a.shared[q]);
-        if (a.resid) acc = __fadd_rn(r == r0 ? rs0 : a.resid[q], acc);
-        if (a.accumulate) acc = __fadd_rn(r == r0 ? ac0 : o[r], acc);
+        if (a.shared) acc = __fadd_rn(acc, first ? sh0 : a.shared[q]);
+        if (a.resid) acc = __fadd_rn(first ? rs0 : a.resid[q], acc);
+        if (a.accumulate) acc = __fadd_rn(first ? ac0 : o[r], acc);
         o[r] = acc;
     }
 }

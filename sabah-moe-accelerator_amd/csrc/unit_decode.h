@@ -131,37 +131,46 @@ struct LdsWindow {
         // lanes on consecutive units then cover every bank, where dword reads
         // put 32 lanes on 8 (Q4_K) or 16 banks.  W[0] and W[NF + 1] hold only
         // bytes outside the unit, which no field uses.
+        // Both forms write sh first and then W[0], W[1], ..., W[NF + 1] in that
+        // order: branches that end in stores to different members get them
+        // merged into one store at a selected address, which keeps the struct
+        // in scratch memory.  Each wide word passes whole through an empty
+        // asm: with only its elements used, the compiler otherwise splits it
+        // into dword reads.
         constexpr int UB = UnitFmt<QT>::BYTES;
         constexpr int A = UB % 16 == 0 && (UB / 16) % 2 == 1 ? 16 : UB % 8 == 0 && (UB / 8) % 2 == 1 ? 8 : 0;
+        const uint8_t* o = unit_lds + ORG - 4;
+        sh = (uint32_t)(reinterpret_cast<uintptr_t>(o) & 3);   // ORG & 3 for an A-aligned unit
         if constexpr (A != 0 && 4 * NF == UB) {
             if ((reinterpret_cast<uintptr_t>(unit_lds) & (A - 1)) == 0) {
+                typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+                typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+                W[0] = 0;
                 if constexpr (A == 16) {
-                    const uint4* g = reinterpret_cast<const uint4*>(unit_lds);
+                    const v4u* g = reinterpret_cast<const v4u*>(unit_lds);
 #pragma unroll
                     for (int c = 0; c < NF / 4; ++c) {
-                        const uint4 v = g[c];
+                        v4u v = g[c];
+                        asm("" : "+v"(v));
                         W[1 + 4 * c] = v.x;
                         W[2 + 4 * c] = v.y;
                         W[3 + 4 * c] = v.z;
                         W[4 + 4 * c] = v.w;
                     }
                 } else {
-                    const uint2* g = reinterpret_cast<const uint2*>(unit_lds);
+                    const v2u* g = reinterpret_cast<const v2u*>(unit_lds);
 #pragma unroll
                     for (int c = 0; c < NF / 2; ++c) {
-                        const uint2 v = g[c];
+                        v2u v = g[c];
+                        asm("" : "+v"(v));
                         W[1 + 2 * c] = v.x;
                         W[2 + 2 * c] = v.y;
                     }
                 }
-                W[0] = 0;
                 W[NF + 1] = 0;
-                sh = ORG & 3;
                 return;
             }
         }
-        const uint8_t* o = unit_lds + ORG - 4;
-        sh = (uint32_t)(reinterpret_cast<uintptr_t>(o) & 3);
         const uint32_t* g = reinterpret_cast<const uint32_t*>(o - sh);
 #pragma unroll
         for (int i = 0; i < NF + 2; ++i) W[i] = g[i];
