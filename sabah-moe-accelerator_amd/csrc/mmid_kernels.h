@@ -818,6 +818,107 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// MUL_MAT_ID of one token's IQ3_S slots in per-wave rounds: k_gate_up_rounds'
+// scheme for the one matrix of a drop-in call (llama.cpp's gate, up and down
+// nodes at decode).  A workgroup of kMmidRoundThreads threads takes R = 256 /
+// (units per row) packed rows of the slot's matrix, at most 256 units; each of
+// its eight waves owns 32 consecutive units (its contiguous bytes), issues
+// their loads as soon as the expert id is in, stages them in a private LDS
+// region and decodes them, two lanes per unit, without waiting for the other
+// waves; x is quantised while the loads fly.  k_mmid instead stages the whole
+// tile behind one barrier, one lane per unit.  The integer unit sums and the
+// fp32 steps are k_mmid's (and the row sums row_sum's), so the results are
+// bit-identical to it.
+// grid = (ceil(rows / R), n_ids, n_tokens)
+// ---------------------------------------------------------------------------
+constexpr int kMmidRoundThreads = 2 * kThreads;
+// static LDS of k_mmid_rounds: the codebook table and the guarded staging regions
+constexpr int kMmidRoundStaticLds = kLdsTables + 32 + (kMmidRoundThreads / 64) * 16 * WaveRoundChunks<QT_IQ3_S, 2>::V;
+__host__ __device__ inline int rows_mmid_rounds(int qt, int k) { return 256 / units_per_row(qt, k); }
+// the calls it serves: IQ3_S, packed rows of whole 256-element units, no gate row
+__host__ __device__ inline bool mmid_rounds_ok(int qt, int k, size_t row_stride, bool gated) {
+    return qt == QT_IQ3_S && k % 256 == 0 && k <= 256 * 256 && row_stride == row_bytes(qt, k) && !gated;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_mmid_rounds(MmidArgs a) {
+    constexpr int QT = QT_IQ3_S, PER = 2;
+    constexpr int UB = UnitFmt<QT>::BYTES, UPW = RoundUnits<PER>::V, NW = NT / 64;
+    constexpr int WCH = WaveRoundChunks<QT, PER>::V, N = WaveRoundChunks<QT, PER>::LOADS;
+    static_assert(NW * UPW == 256, "a workgroup's waves cover its 256 units in one round");
+    __shared__ __align__(16) uint8_t tabs[kLdsTables];
+    // the waves' staging regions, with a guard on each side: a unit's field
+    // reads start two bytes before it and end four bytes past it (never used)
+    __shared__ __align__(16) uint8_t stage_mem[16 + NW * 16 * WCH + 16];
+    static_assert(kLdsTables + sizeof(stage_mem) == kMmidRoundStaticLds, "static LDS as the host counts it");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int NUS = units_per_row(QT, a.k), NCB = contribs_per_row(QT, a.k);
+    const Plan P = make_plan(QT, a.k, 1, a.R * NCB);
+    const int t = blockIdx.z, i = blockIdx.y, row0 = blockIdx.x * a.R;
+    const int nrows = min(a.R, a.rows - row0);
+    const size_t rb = row_bytes(QT, a.k);
+    float* out = reinterpret_cast<float*>(a.dst + (size_t)t * a.dst_token_stride + (size_t)i * a.dst_id_stride) + row0;
+    uint8_t* act = smem + P.off_act;
+    float* part = reinterpret_cast<float*>(smem + P.off_part);
+    const float* xr = reinterpret_cast<const float*>(a.x + (size_t)t * a.x_token_stride +
+                                                     (size_t)(i % a.x_rows) * a.x_id_stride);
+    const ActBatch xb{xr, 0, 1, a.k, act_type(QT), act, 0};
+    ActRegs<kRoundsX> xa;
+    act_prefetch<kRoundsX, NT>(xb, xa);
+    const GridRegs<NT> gr = load_grid_regs<NT>((int)threadIdx.x);
+    const uint8_t* w = expert_ptr(a.W, a.rt, t, i, a.n_ids);
+    if (w == nullptr) {   // uniform across the workgroup
+        flag_error(a.err);
+        for (int r = threadIdx.x; r < nrows; r += NT) out[r] = __builtin_nanf("");
+        return;
+    }
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63u);
+    // the wave's units v0 .. v0 + nu (none for a wave past a short last tile):
+    // consecutive lanes load consecutive 16-byte chunks of their bytes
+    const int v0 = UPW * wave, nu = min(UPW, nrows * NUS - v0);
+    const uint8_t* p = w + (size_t)row0 * rb + (nu > 0 ? (size_t)v0 * UB : 0);
+    const int lead = (int)(reinterpret_cast<uintptr_t>(p) & 15);
+    const uint8_t* g = p - lead;
+    const int last = nu > 0 ? (lead + nu * UB - 1) >> 4 : 0;
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    u32x4 d[N];
+    int q[N];
+#pragma unroll
+    for (int it = 0; it < N; ++it) {
+        q[it] = min(lane + 64 * it, last);
+        d[it] = *(g_u32x4*)(g + 16 * q[it]);
+    }
+    store_iq3s_tables<NT>(tabs, gr, (int)threadIdx.x);
+    act_quantize<kRoundsX, NT>(xb, xa);
+    __syncthreads();                                        // activations and table ready
+    // the wave's own chunks: LDS operations of one wave complete in order, so
+    // its reads below see these writes
+    uint8_t* region = stage_mem + 16 + 16 * WCH * wave;
+#pragma unroll
+    for (int it = 0; it < N; ++it) *reinterpret_cast<u32x4*>(region + 16 * q[it]) = d[it];
+    // two lanes per unit, its halves 32 lanes apart (a half-wave's field reads
+    // then come from 32 units rather than 16 units twice)
+    const int j = lane & 31, half = lane >> 5;
+    if (j < nu) {                                           // both lanes of a pair alike
+        const int v = v0 + j;
+        const int r = div_small(v, __builtin_amdgcn_rcpf((float)NUS)), us = v - r * NUS;
+        uint32_t A[4][8];
+        act_half(act + us * kActChunkStride, half, A);
+        uint32_t G[UnitFmt<QT>::NF], dbits;
+        iq3s_half_fields(region + lead + j * UB, half, G, dbits);
+        int bs = iq3s_half_bsum(G, tabs, A);
+        bs += __shfl_xor(bs, 32);                          // the partner lane's half
+        if (half == 0) {
+            const ActLayout AL(a.k, QT_Q8_K);
+            part[r * NCB + us] =
+                __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(act + AL.off_d)[us]), (float)bs);
+        }
+    }
+    __syncthreads();                                        // partials complete
+    for (int r = threadIdx.x; r < nrows; r += NT) out[r] = row_sum(part + r * NCB, NCB);
+}
+
+// ---------------------------------------------------------------------------
 // Fused down projection + routed combine (ggml: MUL_MAT_ID on h, ggml_mul by
 // the router weights, ggml_add over the slots in slot order), plus optional
 // shared-expert rows and residual:

@@ -117,6 +117,7 @@ EXTRA_SIGNATURES = {
     "sabah_synth_weights": ([c_vp, c_i, ctypes.c_longlong, c_i, ctypes.c_ulonglong, ctypes.c_float, c_vp], c_i),
     "sabah_rt_set_kernel_timing": ([c_i], c_i),
     "sabah_rt_set_layer_fusion": ([c_i], c_i),
+    "sabah_rt_set_mmid_rounds": ([c_i], c_i),
     "sabah_rt_set_layer_placement_test": ([c_i], c_i),
     "sabah_rt_set_selfcheck": ([c_i, ctypes.c_double, c_i], c_i),
     "sabah_rt_get_kernel_timing": ([c_i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_u64), c_i], c_i),

@@ -199,6 +199,62 @@ def test_mul_mat_id_padded_rows(hip_rt, orc, qt, k, rows, pad):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+# One token of IQ3_S runs the per-wave rounds kernel (k_mmid_rounds): its
+# outputs must be bit-identical to the whole-tile kernel's (k_mmid, forced with
+# sabah_rt_set_mmid_rounds(0)) and to the oracle.  Shapes: the shipped gate/up
+# form (k 2048: 32-row tiles, x one row) and down form (k 768: 85-row tiles, x
+# one row per slot); a last tile of 4 rows (100 = 3 x 32 + 4: five of its
+# eight waves own no unit); one unit per row (k 256, 256-row tiles, rows 300);
+# 16 units per row (k 4096, 16-row tiles); and a padded row stride, which keeps
+# the whole-tile kernel.
+@pytest.mark.parametrize("k,rows,x_rows_is_n_ids,pad", [(2048, 768, False, 0), (768, 2048, True, 0),
+                                                         (2048, 100, False, 0), (256, 300, True, 0),
+                                                         (4096, 40, False, 0), (2048, 64, False, 20)])
+def test_one_token_iq3s_rounds_kernel_equals_the_tile_kernel(hip_rt, orc, k, rows, x_rows_is_n_ids, pad):
+    rng = np.random.default_rng(k + rows + pad + 17 * x_rows_is_n_ids)
+    qt, E, K = IQ3_S, 12, 10
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    rb = raw.shape[-1]
+    padded = np.full((E, rows, rb + pad), 0xA5, dtype=np.uint8)
+    padded[:, :, :rb] = raw
+    ids = rng.choice(E, K, replace=False).astype(np.int32)[None]
+    ids[0, 7] = ids[0, 2]                                   # duplicate id
+    x_rows = K if x_rows_is_n_ids else 1
+    x = rng.standard_normal((1, x_rows, k)).astype(np.float32)
+    bank, xd, idd = T(padded), T(x), T(ids)
+    L = hip_rt.lib()
+    outs = []
+    try:
+        for mode in (1, 0):
+            hip_rt.check(L.sabah_rt_set_mmid_rounds(mode), "rounds mode")
+            out = torch.full((1, K, rows), float("nan"), dtype=torch.float32, device=DEV)
+            hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * (rb + pad), rb + pad, xd, idd, out, rows, k, E, qt), "v2")
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+    finally:
+        hip_rt.check(L.sabah_rt_set_mmid_rounds(1), "rounds mode")
+    assert_bits_equal(outs[0], outs[1], "rounds vs tile kernel, k=%d rows=%d" % (k, rows))
+    want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    assert np.array_equal(outs[0].view(np.uint32), want.view(np.uint32))
+    if x_rows == 1:
+        assert np.array_equal(outs[0][0, 7], outs[0][0, 2])
+
+
+def test_one_token_iq3s_rounds_kernel_poisons_a_bad_id(hip_rt, orc):
+    rng = np.random.default_rng(81)
+    qt, E, rows, k = IQ3_S, 4, 96, 2048
+    raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
+    x = T(rng.standard_normal((1, 1, k)).astype(np.float32))
+    ids = T(np.array([[3, -1, 0]], np.int32))
+    out = torch.zeros(1, 3, rows, dtype=torch.float32, device=DEV)
+    assert v2(hip_rt, T(raw).data_ptr(), rows * 880, 880, x, ids, out, rows, k, E, qt) == 0
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.all(np.isnan(o[0, 1])) and np.all(np.isfinite(o[0, [0, 2]]))
+    assert hip_rt.lib().sabah_rt_check_errors() == -1
+    assert hip_rt.lib().sabah_rt_check_errors() == 0
+
+
 def test_mul_mat_id_detects_wrong_expert_and_wrong_row(hip_rt, orc):
     rng = np.random.default_rng(77)
     qt, E, rows, k, K = IQ3_S, 8, 64, 768, 4
