@@ -87,6 +87,8 @@ def main() -> int:
     W = WORKLOADS[args.workload]
     if W.n_tokens > 1:
         return bench_batch(args, W)
+    if W.op == "mul_mat_id":
+        return bench_mmid_decode(args, W)
     dev = torch.device("cuda:0")
     rt.init(0)
     rt.check(rt.lib().sabah_rt_set_layer_fusion(args.layer_fusion), "layer fusion mode")
@@ -249,6 +251,184 @@ def main() -> int:
     return 0
 
 
+def bench_mmid_decode(args, W):
+    """Decode through the drop-in operator: per layer, the gate, up and down
+    sabah_rt_mul_mat_id_v2 calls of one token, as llama.cpp's hook makes them
+    (its graph's SwiGLU and weighted combine between and after the calls are
+    ggml ops, outside the path: down reads a fixed synthetic h).  The 48
+    layers' 144 calls replay as one HIP graph per step over static id
+    buffers; `value` is the step's distinct expert bytes / wall time, as for
+    the fused chain.  Layer 0's three calls are checked against the oracle,
+    bit for bit."""
+    import numpy as np
+    import torch
+
+    from sabah.runtime import rt
+    from sabah.runtime.bank import ExpertBank
+    from sabah.runtime.executor import MoEExecutor
+
+    dev = torch.device("cuda:0")
+    rt.init(0)
+    t0 = time.time()
+    bank = ExpertBank(W.n_layers, W.n_experts, W.d_model, W.d_ff,
+                      {"gate": W.qt_gate, "up": W.qt_up, "down": W.qt_down}, device="cuda:0")
+    bank.fill_synthetic(seed=args.seed)
+    torch.cuda.synchronize()
+    print("bank: %.1f GB generated in HBM in %.1f s" % (bank.total_bytes / 1e9, time.time() - t0),
+          file=sys.stderr, flush=True)
+    rng = np.random.default_rng(args.seed)
+    P, G, k = args.pool, W.n_layers, W.top_k
+    ids_np, _ = W.route(rng, n_tokens=P, n_layers=G)                # [G, P, k]
+    ids_np = np.ascontiguousarray(ids_np.transpose(1, 0, 2))[:, :, None, :]   # [P, G, 1, k]
+    x_np = rng.standard_normal((P, 1, 1, W.d_model)).astype(np.float32)
+    h_np = rng.standard_normal((1, k, W.d_ff)).astype(np.float32)
+    ids_all = torch.from_numpy(ids_np).to(dev)
+    xs = torch.from_numpy(x_np).to(dev)
+    ex = MoEExecutor(bank, max_used=k)
+    ids_s = torch.zeros(G, 1, k, dtype=torch.int32, device=dev)
+    x_s = torch.zeros(1, 1, W.d_model, dtype=torch.float32, device=dev)
+    h_s = torch.from_numpy(h_np).to(dev)
+    g_out = torch.empty(G, 1, k, W.d_ff, device=dev)
+    u_out = torch.empty_like(g_out)
+    d_out = torch.empty(G, 1, k, W.d_model, device=dev)
+
+    def calls():
+        for l in range(G):
+            ex.mul_mat_id(l, "gate", x_s, ids_s[l], out=g_out[l])
+            ex.mul_mat_id(l, "up", x_s, ids_s[l], out=u_out[l])
+            ex.mul_mat_id(l, "down", h_s, ids_s[l], out=d_out[l])
+
+    calls()                                                          # eager: checks every source once
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    torch.cuda.synchronize()
+
+    def step(i):
+        p = i % P
+        ids_s.copy_(ids_all[p])
+        x_s.copy_(xs[p])
+        graph.replay()
+
+    step_bytes = [W.step_expert_bytes(ids_np[p, :, 0][:, None, :]) for p in range(P)]
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(args.warmup, args.warmup + args.steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_total = ev0.elapsed_time(ev1)
+    ms_step = ms_total / args.steps
+    nbytes = sum(step_bytes[i % P] for i in range(args.warmup, args.warmup + args.steps))
+    gbs = nbytes / (ms_total * 1e6)
+    # the bare graph (inputs in place) replayed R times: per-call duration
+    R = max(4, args.steps // 2)
+    graph.replay()
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(R):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us_call = 1000.0 * ev0.elapsed_time(ev1) / (R * 3 * G)
+    # a call's algorithmic bytes: its k expert matrices (distinct at one
+    # token), the activation row(s) it reads and the rows it writes; per call,
+    # averaged over a layer's two gate/up-form calls and its down call
+    gate_call = k * W.matrix_bytes("gate") + 4 * W.d_model + 4 * k * W.d_ff
+    down_call = k * W.matrix_bytes("down") + 4 * k * W.d_ff + 4 * k * W.d_model
+    per_call = (2 * gate_call + down_call) / 3
+    # per-dispatch durations: the same calls run eagerly, each recording its own
+    # start/stop HIP event pair on the stream it runs on
+    L = rt.lib()
+    L.sabah_rt_set_kernel_timing(1)
+    rt.kernel_timing("mmid", reset=True)
+    for i in range(args.steps):
+        ids_s.copy_(ids_all[i % P])
+        calls()
+    torch.cuda.synchronize()
+    L.sabah_rt_set_kernel_timing(0)
+    kms, kn = rt.kernel_timing("mmid")
+
+    # parity: layer 0 of step 0's token against the oracle, all three calls
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    step(0)
+    torch.cuda.synchronize()
+    e_ids = ids_np[0, 0, 0]
+    used = np.unique(e_ids)
+    lid = np.searchsorted(used, e_ids).astype(np.int32)[None]
+    worst = 0.0
+    exact = True
+    for role, inp, out in (("gate", x_np[0], g_out[0]), ("up", x_np[0], u_out[0]), ("down", h_np, d_out[0])):
+        sub = np.stack([bank.read_expert(0, role, int(e)) for e in used])
+        rows = W.d_ff if role != "down" else W.d_model
+        kk = W.d_model if role != "down" else W.d_ff
+        want = O.mul_mat_id(sub, inp, lid, rows, kk, W.qt_down if role == "down" else W.qt_gate)
+        got = out.cpu().numpy()
+        worst = max(worst, float(np.abs(got.astype(np.float64) - want).max() / np.abs(want).max()))
+        exact &= bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+    parity = {"layer": 0, "calls": ["gate", "up", "down"], "max_rel": worst, "bit_identical": exact,
+              "tolerance": {"max_rel": 1e-3, "cos": 0.99999}}
+    cpu = None
+    if not args.no_cpu:
+        # the oracle's MUL_MAT_ID on this host's cores: whole tokens (the 144
+        # calls of the 48 layers) over the routed experts read back from HBM
+        threads = cpu_threads(args)
+        layers = []
+        for l in range(G):
+            e_ids = ids_np[0, l, 0]
+            used = np.unique(e_ids)
+            lid = np.searchsorted(used, e_ids).astype(np.int32)[None]
+            layers.append(({r: np.stack([bank.read_expert(l, r, int(e)) for e in used])
+                            for r in ("gate", "up", "down")}, lid))
+        xq, hq = x_np[0], h_np
+        t1 = time.perf_counter()
+        tokens = cbytes = 0
+        while True:
+            for sub, lid in layers:
+                for role in ("gate", "up", "down"):
+                    down = role == "down"
+                    O.mul_mat_id(sub[role], hq if down else xq, lid, W.d_model if down else W.d_ff,
+                                 W.d_ff if down else W.d_model, W.qt_down if down else W.qt_gate, n_threads=threads)
+                cbytes += len(lid[0]) * W.expert_bytes()
+            tokens += 1
+            if time.perf_counter() - t1 >= args.cpu_seconds:
+                break
+        dt = time.perf_counter() - t1
+        cpu = {"value": round(cbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "tok_s": round(tokens / dt, 3),
+               "sample": "%d decode token(s) x %d layers x 3 MUL_MAT_ID calls (%.0f MB of routed expert bytes "
+                         "read back from HBM), %.1f s" % (tokens, G, cbytes / tokens / 1e6, dt),
+               "host": host_info(threads)}
+    achieved = per_call / (us_call * 1e3)
+    line = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "compute": compute_note(W),
+        "data": "synthetic (N(0,0.02) weights quantised on device; %s routing; seeded)" % W.routing,
+        "config": {"workload": W.name, "n_layers": G, "n_experts": W.n_experts, "top_k": k, "d_model": W.d_model,
+                   "d_ff": W.d_ff, "n_tokens": 1, "quant": quant_note(W), "bank_bytes": bank.total_bytes,
+                   "expert_bytes_per_step": nbytes // args.steps, "calls_per_step": 3 * G,
+                   "mode": "drop-in sabah_rt_mul_mat_id_v2: gate, up and down calls per layer (h synthetic), "
+                           "the %d calls replayed as one HIP graph per step" % (3 * G)},
+        "tok_s": round(1000.0 / ms_step, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "us_per_layer": round(1000.0 * ms_step / G, 3),
+        "kernels": {"mmid": {"launches": kn, "avg_us": round(1000.0 * kms / max(kn, 1), 3)}},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(W.name, ["mmid"]),
+                     "kernel": "mmid", "bytes_per_launch": int(per_call), "avg_launch_us": round(us_call, 3),
+                     "timing": "replayed graph, %d replays of %d calls" % (R, 3 * G)},
+        "cpu_baseline": cpu, "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    copy_probe(args, dev)
+    return 0
+
+
 def copy_probe(args, dev):
     """One device-to-device copy of --copy-probe-mib MiB at the end of the run:
     a plain copy kernel of known size, to calibrate the FETCH_SIZE / WRITE_SIZE
@@ -303,7 +483,7 @@ class LayerCallsGraph:
 
 
 # kernel symbols of each timing kind, as the traffic summaries name them
-KERNEL_SYMBOL = {"gate_up": ("k_gate_up_rounds", "k_gate_up"), "down": ("k_down_combine",), "mmid": ("k_mmid",),
+KERNEL_SYMBOL = {"gate_up": ("k_gate_up_rounds", "k_gate_up"), "down": ("k_down_combine",), "mmid": ("k_mmid_rounds", "k_mmid"),
                  "layer": ("k_layer_decode",),
                  "grouped_gate_up": ("k_grouped_gate_up",), "grouped_down": ("k_grouped_down",)}
 INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
@@ -556,6 +736,7 @@ PROFILE_PREFIX = {"iq3s_48x512_top10": "decode_kernels_iq3s_48x512_top10",
                   "q4k_e128_top8": "decode_kernels_q4k_e128_top8",
                   "iq3s_prefill_t512": "prefill_layer_iq3s_t512_e512_top10",
                   "iq3s_mmid_t512": "mul_mat_id_iq3s_t512_e512_top10",
+                  "iq3s_mmid_48x512_top10": "mul_mat_id_iq3s_48x512_top10_decode",
                   "mixed_t32_q4k_q6k_shared": "mixed_layer_q4k_q6k_shared_t32"}
 
 

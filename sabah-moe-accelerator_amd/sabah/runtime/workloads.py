@@ -85,6 +85,10 @@ WORKLOADS = {
                               note="Q4_K decode, one MoE layer"),
     "iq3s_48x512_top10": Workload("iq3s_48x512_top10", 48, 512, 10, 2048, 768, 1, IQ3_S, IQ3_S, IQ3_S, "zipf",
                                   note="IQ3_S decode, 48 MoE layers, bank fully HBM-resident"),
+    "iq3s_mmid_48x512_top10": Workload("iq3s_mmid_48x512_top10", 48, 512, 10, 2048, 768, 1, IQ3_S, IQ3_S, IQ3_S,
+                                       "zipf", op="mul_mat_id",
+                                       note="the drop-in operator at decode: each of the 48 layers' gate, up and "
+                                            "down MUL_MAT_ID calls for one token, as llama.cpp's hook makes them"),
     "iq3s_prefill_t512": Workload("iq3s_prefill_t512", 1, 512, 10, 2048, 768, 512, IQ3_S, IQ3_S, IQ3_S, "zipf",
                                   note="group-major prefill, one layer"),
     "iq3s_mmid_t512": Workload("iq3s_mmid_t512", 1, 512, 10, 2048, 768, 512, IQ3_S, IQ3_S, IQ3_S, "zipf",
