@@ -394,7 +394,7 @@ template <int QT, int NT>
 __device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs, const uint8_t* stage,
                                    const int* leads, int k, const uint8_t* act0, int act_stride, int part_rows,
                                    float* part) {
-    constexpr bool SPLIT = QT == QT_IQ3_S && NT == 2 * kThreads;
+    constexpr bool SPLIT = (QT == QT_IQ3_S || QT == QT_Q4_K) && NT == 2 * kThreads;
     constexpr int PER = SPLIT ? 2 : 1;                  // lanes per unit
     const int n = S.T.n_mat * S.nv;
     const float rcp_nv = __builtin_amdgcn_rcpf((float)S.nv);
@@ -409,7 +409,7 @@ __device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs
         const int r = div_small(v, S.T.rcp_nus), us = v - r * S.T.NUS;
         const uint8_t* unit = stage + 16 * S.cpt * t + leads[t] + (int)((size_t)r * S.T.rb) + us * TileWalk<QT>::UB - S.b0;
         float* prow = part + (t * part_rows + r) * S.T.NCB;
-        if constexpr (SPLIT) {
+        if constexpr (SPLIT && QT == QT_IQ3_S) {
             const uint8_t* act = act0 + t * act_stride;
             const ActLayout AL(k, QT_Q8_K);
             uint32_t G[UnitFmt<QT>::NF], A[4][8], dbits;
@@ -419,6 +419,22 @@ __device__ inline void pass_decode(const TileRun<QT, NT>& S, const uint8_t* tabs
             bs += __shfl_xor(bs, 32);                    // the partner lane's half
             if (half == 0)
                 prow[us] = __fmul_rn(__fmul_rn(h2f(dbits), reinterpret_cast<const float*>(act + AL.off_d)[us]), (float)bs);
+        } else if constexpr (SPLIT) {                    // Q4_K: the halves' exact sums, then unit_dot's fp32 steps
+            const uint8_t* act = act0 + t * act_stride;
+            const ActLayout AL(k, QT_Q8_K);
+            Q4kHalf Q;
+            uint32_t A[4][8];
+            q4k_half_fields(unit, half, Q);
+            act_half(act + us * kActChunkStride, half, A);
+            int isum, msum;
+            q4k_half_sums(Q, half, A, reinterpret_cast<const int16_t*>(act + AL.off_bsum) + 16 * us, isum, msum);
+            isum += __shfl_xor(isum, 32);
+            msum += __shfl_xor(msum, 32);
+            if (half == 0) {
+                const float dx = reinterpret_cast<const float*>(act + AL.off_d)[us];
+                const float d = h2f(Q.F[0]), dmin = h2f(Q.F[0] >> 16);
+                prow[us] = __fsub_rn(__fmul_rn(__fmul_rn(d, dx), (float)isum), __fmul_rn(__fmul_rn(dmin, dx), (float)msum));
+            }
         } else {
             LdsWindow<QT> Wn;
             Wn.load(unit);
@@ -609,7 +625,7 @@ __device__ inline void store_h(float* p, float v, bool publish) {
 // row0 .. row0 + R of gate and up, h = silu(g) * u to hbase (laid out as
 // a.h), published with store_h when `publish`.  tabs, leads, stage: the
 // static LDS; smem: the plan's dynamic LDS.
-template <int QT>
+template <int QT, int NT = kThreads>
 __device__ inline void gate_up_tile(const GateUpArgs& a, int t, int s, int row0, uint8_t* tabs, int* leads,
                                     uint8_t* stage, uint8_t* smem, bool publish, float* hbase) {
     const int NCB = contribs_per_row(QT, a.d_model);
@@ -621,35 +637,36 @@ __device__ inline void gate_up_tile(const GateUpArgs& a, int t, int s, int row0,
     float* part = reinterpret_cast<float*>(smem + P.off_part);
     const ActBatch xb{a.x + (size_t)t * a.d_model, 0, 1, a.d_model, act_type(QT), act, 0};
     ActRegs<kRoundsX> xa;
-    act_prefetch<kRoundsX, kThreads>(xb, xa);
-    const TableRegs<QT, kThreads> gr = load_tables<QT, kThreads>((int)threadIdx.x);
+    act_prefetch<kRoundsX, NT>(xb, xa);
+    const TableRegs<QT, NT> gr = load_tables<QT, NT>((int)threadIdx.x);
     const uint8_t *wg, *wu;
     expert_pair(a.G, a.U, a.rt, t, s, a.n_slots, wg, wu);
     if (wg == nullptr || wu == nullptr) {
         flag_error(a.err);
-        for (int r = threadIdx.x; r < nrows; r += kThreads) store_h(h + r, __builtin_nanf(""), publish);
+        for (int r = threadIdx.x; r < nrows; r += NT) store_h(h + r, __builtin_nanf(""), publish);
         return;
     }
     wg += (size_t)row0 * rb;
     wu += (size_t)row0 * rb;
     auto tile_ptr = [&](int m) { return m ? wu : wg; };
-    TileRun<QT> S{TileWalk<QT>(2, nrows, rb, a.d_model)};
+    TileRun<QT, NT> S{TileWalk<QT, NT>(2, nrows, rb, a.d_model)};
     tiles_begin(S, tile_ptr);
-    store_tables<QT, kThreads>(tabs, gr, (int)threadIdx.x);
-    act_quantize<kRoundsX, kThreads>(xb, xa);
+    store_tables<QT, NT>(tabs, gr, (int)threadIdx.x);
+    act_quantize<kRoundsX, NT>(xb, xa);
     tiles_finish(S, tabs, stage, leads, a.d_model, act, 0, a.R, part);
-    for (int r = threadIdx.x; r < nrows; r += kThreads) {
+    for (int r = threadIdx.x; r < nrows; r += NT) {
         const float g = row_sum(part + r * NCB, NCB);
         const float up = row_sum(part + (a.R + r) * NCB, NCB);
         store_h(h + r, __fmul_rn(silu_f32(g), up), publish);
     }
 }
 
-template <int QT>
-__global__ __launch_bounds__(kThreads, tile_min_waves(QT)) void k_gate_up(GateUpArgs a) {
+// NT = 2 kThreads (Q4_K): two lanes per unit (pass_decode), twice the waves
+template <int QT, int NT = kThreads>
+__global__ __launch_bounds__(NT, tile_min_waves(QT)) void k_gate_up(GateUpArgs a) {
     SABAH_STATIC_LDS(QT)
     extern __shared__ __align__(16) uint8_t smem[];
-    gate_up_tile<QT>(a, blockIdx.z, blockIdx.y, blockIdx.x * a.R, tabs, leads, stage, smem, false, a.h);
+    gate_up_tile<QT, NT>(a, blockIdx.z, blockIdx.y, blockIdx.x * a.R, tabs, leads, stage, smem, false, a.h);
 }
 
 // ---------------------------------------------------------------------------

@@ -465,6 +465,61 @@ __device__ inline void q4k_item(const uint32_t (&F)[36], int j, uint32_t (&v)[8]
     for (int i = 0; i < 8; ++i) v[i] = (F[4 + 8 * (j >> 1) + i] >> sh) & 0x0F0F0F0Fu;
 }
 
+// Half h of a Q4_K unit staged in LDS (items 4h .. 4h + 3, two lanes per
+// unit): F[0..3] the unit's d, dmin and packed scales / mins, F[4..19] its qs
+// bytes 64h .. 64h + 63 (so item 4h + j takes F[4 + 8 (j / 2) ..]).  A
+// 16-byte aligned unit is read as five 16-byte words, otherwise as dwords
+// shifted into place.
+struct Q4kHalf {
+    uint32_t F[20];
+};
+__device__ inline void q4k_half_fields(const uint8_t* unit_lds, int h, Q4kHalf& Q) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    if ((reinterpret_cast<uintptr_t>(unit_lds) & 15) == 0) {
+        const v4u* g = reinterpret_cast<const v4u*>(unit_lds);
+#pragma unroll
+        for (int c = 0; c < 5; ++c) {
+            v4u v = g[c == 0 ? 0 : 4 * h + c];
+            asm("" : "+v"(v));
+            Q.F[4 * c] = v.x; Q.F[4 * c + 1] = v.y; Q.F[4 * c + 2] = v.z; Q.F[4 * c + 3] = v.w;
+        }
+        return;
+    }
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(unit_lds) & 3);
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(unit_lds - sh);
+    uint32_t W[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) W[i] = w[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Q.F[i] = __builtin_amdgcn_alignbyte(W[i + 1], W[i], sh);
+    const uint32_t* wq = w + 4 + 16 * h;
+    uint32_t V[17];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) V[i] = wq[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Q.F[4 + i] = __builtin_amdgcn_alignbyte(V[i + 1], V[i], sh);
+}
+// The exact integer sums of a half against the q8_K chunk's items (activation
+// bytes A of items 4h .. 4h + 3, bsums bs of the whole chunk):
+// isum = sum sc_j (q_j . x_j), msum = sum mn_j (bsum_2j + bsum_2j+1).
+__device__ inline void q4k_half_sums(const Q4kHalf& Q, int h, const uint32_t (&A)[4][8], const int16_t* bs, int& isum,
+                                     int& msum) {
+    isum = 0;
+    msum = 0;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * h + jj;
+        const int sh = 4 * (jj & 1);
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = sdot4((Q.F[4 + 8 * (jj >> 1) + i] >> sh) & 0x0F0F0F0Fu, A[jj][i], s);
+        int sc, mn;
+        q4k_scale_min(Q.F, j, sc, mn);
+        isum += __mul24(sc, s);
+        msum += __mul24(mn, (int)bs[2 * j] + (int)bs[2 * j + 1]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Q5_K: Q4_K's d, dmin and packed 6-bit scales / mins in F[0..3], qh[32] in
 // F[4..11], qs[128] in F[12..43]; element 32 j + l (sub-block j) is the nibble
