@@ -434,6 +434,13 @@ hipError_t launch_down(const DownArgs& a, int n_tokens, hipStream_t st) {
     constexpr int NT = QT == QT_IQ3_S ? 2 * kThreads : kThreads;
     const Plan P = make_plan(QT, a.d_ff, a.n_slots, a.n_slots * a.R * contribs_per_row(QT, a.d_ff));
     dim3 grid((unsigned)((a.d_model + a.R - 1) / a.R), (unsigned)n_tokens);
+    if constexpr (QT == QT_Q4_K) {
+        if (n_tokens == 1 && !a.hq) {                       // one token: two lanes per unit, as for gate/up
+            if (const hipError_t e = fit_lds(k_down_combine<QT, 2 * kThreads>, P.bytes, launch_lds(QT, P))) return e;
+            launch_kernel(KK_DOWN, k_down_combine<QT, 2 * kThreads>, grid, dim3(2 * kThreads), P.bytes, st, a);
+            return hipGetLastError();
+        }
+    }
     if (a.hq) {
         if (const hipError_t e = fit_lds(k_down_combine<QT, NT, true>, P.bytes, launch_lds(QT, P))) return e;
         launch_kernel(KK_DOWN, k_down_combine<QT, NT, true>, grid, dim3(NT), P.bytes, st, a);
