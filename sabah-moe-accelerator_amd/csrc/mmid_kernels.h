@@ -835,9 +835,11 @@ __global__ __launch_bounds__(NT) void k_gate_up_rounds(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// MUL_MAT_ID of one token's IQ3_S slots in per-wave rounds: k_gate_up_rounds'
-// scheme for the one matrix of a drop-in call (llama.cpp's gate, up and down
-// nodes at decode).  A workgroup of kMmidRoundThreads threads takes R = 256 /
+// MUL_MAT_ID of IQ3_S slots in per-wave rounds: k_gate_up_rounds' scheme for
+// the one matrix of a drop-in call (llama.cpp's gate, up and down nodes at
+// decode, or a few tokens' while their row tiles stay single-pass; more tokens
+// take k_mmid's grown tiles or the grouped kernels).  A workgroup of
+// kMmidRoundThreads threads takes R = 256 /
 // (units per row) packed rows of the slot's matrix, at most 256 units; each of
 // its eight waves owns 32 consecutive units (its contiguous bytes), issues
 // their loads as soon as the expert id is in, stages them in a private LDS

@@ -344,15 +344,16 @@ bool sync_ids_enabled() {
 template <int QT>
 hipError_t launch_mmid(const MmidArgs& a, hipStream_t st) {
     if constexpr (QT == QT_IQ3_S) {
-        // one token (a decode step's gate, up or down node): per-wave rounds
-        if (a.n_tokens == 1 && g_mmid_rounds.load() && mmid_rounds_ok(QT, a.k, a.row_stride, a.sg_w != nullptr)) {
+        // a decode step's gate, up or down node, or a few tokens' (the row tiles single-pass,
+        // not grown): per-wave rounds
+        if (a.R == rows_mmid_rounds(QT, a.k) && g_mmid_rounds.load() &&
+            mmid_rounds_ok(QT, a.k, a.row_stride, a.sg_w != nullptr)) {
             constexpr int NT = kMmidRoundThreads;
-            MmidArgs b = a;
-            b.R = rows_mmid_rounds(QT, a.k);
+            const MmidArgs& b = a;
             const Plan P = make_plan(QT, b.k, 1, b.R * contribs_per_row(QT, b.k));
             if (const hipError_t e = fit_lds(k_mmid_rounds<NT>, P.bytes, kMmidRoundStaticLds + P.bytes))
                 return e;
-            dim3 grid((unsigned)((b.rows + b.R - 1) / b.R), (unsigned)b.n_ids, 1u);
+            dim3 grid((unsigned)((b.rows + b.R - 1) / b.R), (unsigned)b.n_ids, (unsigned)b.n_tokens);
             launch_kernel(KK_MMID, k_mmid_rounds<NT>, grid, dim3(NT), P.bytes, st, b);
             return hipGetLastError();
         }

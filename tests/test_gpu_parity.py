@@ -207,27 +207,30 @@ def test_mul_mat_id_padded_rows(hip_rt, orc, qt, k, rows, pad):
 # eight waves own no unit); one unit per row (k 256, 256-row tiles, rows 300);
 # 16 units per row (k 4096, 16-row tiles); and a padded row stride, which keeps
 # the whole-tile kernel.
-@pytest.mark.parametrize("k,rows,x_rows_is_n_ids,pad", [(2048, 768, False, 0), (768, 2048, True, 0),
-                                                         (2048, 100, False, 0), (256, 300, True, 0),
-                                                         (4096, 40, False, 0), (2048, 64, False, 20)])
-def test_one_token_iq3s_rounds_kernel_equals_the_tile_kernel(hip_rt, orc, k, rows, x_rows_is_n_ids, pad):
-    rng = np.random.default_rng(k + rows + pad + 17 * x_rows_is_n_ids)
+@pytest.mark.parametrize("k,rows,x_rows_is_n_ids,pad,Tn", [(2048, 768, False, 0, 1), (768, 2048, True, 0, 1),
+                                                            (2048, 100, False, 0, 1), (256, 300, True, 0, 1),
+                                                            (4096, 40, False, 0, 1), (2048, 64, False, 20, 1),
+                                                            (2048, 768, False, 0, 4), (768, 2048, True, 0, 3)])
+def test_one_token_iq3s_rounds_kernel_equals_the_tile_kernel(hip_rt, orc, k, rows, x_rows_is_n_ids, pad, Tn):
+    """(The last two shapes: 4 and 3 tokens, whose row tiles stay single-pass, so they take
+    the rounds kernel too.)"""
+    rng = np.random.default_rng(k + rows + pad + 17 * x_rows_is_n_ids + 101 * Tn)
     qt, E, K = IQ3_S, 12, 10
     raw = orc.quantize_weights(qt, (rng.standard_normal((E, rows, k)) * 0.02).astype(np.float32))
     rb = raw.shape[-1]
     padded = np.full((E, rows, rb + pad), 0xA5, dtype=np.uint8)
     padded[:, :, :rb] = raw
-    ids = rng.choice(E, K, replace=False).astype(np.int32)[None]
+    ids = np.stack([rng.choice(E, K, replace=False) for _ in range(Tn)]).astype(np.int32)
     ids[0, 7] = ids[0, 2]                                   # duplicate id
     x_rows = K if x_rows_is_n_ids else 1
-    x = rng.standard_normal((1, x_rows, k)).astype(np.float32)
+    x = rng.standard_normal((Tn, x_rows, k)).astype(np.float32)
     bank, xd, idd = T(padded), T(x), T(ids)
     L = hip_rt.lib()
     outs = []
     try:
         for mode in (1, 0):
             hip_rt.check(L.sabah_rt_set_mmid_rounds(mode), "rounds mode")
-            out = torch.full((1, K, rows), float("nan"), dtype=torch.float32, device=DEV)
+            out = torch.full((Tn, K, rows), float("nan"), dtype=torch.float32, device=DEV)
             hip_rt.check(v2(hip_rt, bank.data_ptr(), rows * (rb + pad), rb + pad, xd, idd, out, rows, k, E, qt), "v2")
             torch.cuda.synchronize()
             outs.append(out.cpu().numpy())
