@@ -207,8 +207,8 @@ uint32_t* g_layer_sync[kMaxDevices] = {};
 // results are bit-identical; on the 48-layer decode the fused launch
 // measured 1,510 GB/s against 1,433 - 1,449 (same box, interleaved runs).
 std::atomic<int> g_layer_fusion{1};
-// 1 (default): one-token IQ3_S MUL_MAT_ID calls run k_mmid_rounds; 0: k_mmid.
-// The results are bit-identical.
+// 1 (default): IQ3_S MUL_MAT_ID calls whose row tiles stay single-pass (one
+// token, or a few) run k_mmid_rounds; 0: k_mmid.  The results are bit-identical.
 std::atomic<int> g_mmid_rounds{1};
 // set when a fused launch's wait ran out: the next fused launch first clears the flags
 std::atomic<bool> g_sync_reset_pending{false};
@@ -349,12 +349,11 @@ hipError_t launch_mmid(const MmidArgs& a, hipStream_t st) {
         if (a.R == rows_mmid_rounds(QT, a.k) && g_mmid_rounds.load() &&
             mmid_rounds_ok(QT, a.k, a.row_stride, a.sg_w != nullptr)) {
             constexpr int NT = kMmidRoundThreads;
-            const MmidArgs& b = a;
-            const Plan P = make_plan(QT, b.k, 1, b.R * contribs_per_row(QT, b.k));
+            const Plan P = make_plan(QT, a.k, 1, a.R * contribs_per_row(QT, a.k));
             if (const hipError_t e = fit_lds(k_mmid_rounds<NT>, P.bytes, kMmidRoundStaticLds + P.bytes))
                 return e;
-            dim3 grid((unsigned)((b.rows + b.R - 1) / b.R), (unsigned)b.n_ids, (unsigned)b.n_tokens);
-            launch_kernel(KK_MMID, k_mmid_rounds<NT>, grid, dim3(NT), P.bytes, st, b);
+            dim3 grid((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)a.n_ids, (unsigned)a.n_tokens);
+            launch_kernel(KK_MMID, k_mmid_rounds<NT>, grid, dim3(NT), P.bytes, st, a);
             return hipGetLastError();
         }
     }
@@ -636,9 +635,9 @@ SABAH_API int sabah_rt_set_layer_fusion(int mode) {
     return 0;
 }
 
-// One-token IQ3_S MUL_MAT_ID kernel: 1 (default) per-wave rounds
-// (k_mmid_rounds), 0 the whole-tile kernel (k_mmid).  The results do not
-// change; tests run both.
+// The IQ3_S MUL_MAT_ID kernel of single-pass launches (one token, or a few):
+// 1 (default) per-wave rounds (k_mmid_rounds), 0 the whole-tile kernel
+// (k_mmid).  The results do not change; tests run both.
 SABAH_API int sabah_rt_set_mmid_rounds(int mode) {
     if (mode < 0 || mode > 1) return fail("MUL_MAT_ID rounds mode %d outside {0 off, 1 on}", mode);
     g_mmid_rounds.store(mode);
