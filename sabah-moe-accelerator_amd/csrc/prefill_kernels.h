@@ -470,26 +470,33 @@ __device__ inline void mfma_blocks(const uint8_t* rowp, const uint8_t* tabs, int
 // tiles: each tile then costs only its MFMAs and the block sum.
 struct Iq3sBlockOps {
     long B[8];
-    uint32_t sc, d;
+    uint32_t ls[2];               // byte k of ls[p]: sub-block 2k + p's scale 2 sc + 1
+    uint32_t d;
 };
 __device__ inline void iq3s_block_ops(const uint8_t* unit, const uint8_t* tabs, int q, Iq3sBlockOps& O) {
     Iq3sQuarter F;
     iq3s_quarter_fields(unit, q, F);
 #pragma unroll
     for (int sub = 0; sub < 8; ++sub) O.B[sub] = iq3s_quarter_operand(F, tabs, sub, q);
-    O.sc = F.sc;
+    O.ls[0] = ((F.sc & 0x0F0F0F0Fu) << 1) | 0x01010101u;
+    O.ls[1] = (((F.sc >> 4) & 0x0F0F0F0Fu) << 1) | 0x01010101u;
     O.d = F.d;
 }
 // mfma_blocks' IQ3_S block (one block, the same integer sums and fp32 steps)
-// from operands decoded by iq3s_block_ops
-__device__ inline void mfma_block_iq3s_ops(const Iq3sBlockOps& O, const XRegs<1>& R, bool valid, int q, float (&c)[4]) {
+// from operands decoded by iq3s_block_ops.  Unmasked: lanes of a pair past
+// the tile hold the tile's last pair's activations (the row is clamped), so
+// their products are finite and reach only that pair's outputs, which the
+// epilogue skips.  (Masking there measured no faster; in k_grouped_down the
+// masked form is kept: unmasked it measured 205 against 170 us per 512-token
+// IQ3_S down, with the same instruction count less the selects.)
+__device__ inline void mfma_block_iq3s_ops(const Iq3sBlockOps& O, const XRegs<1>& R, int q, float (&c)[4]) {
     const v4i32 z = {0, 0, 0, 0};
-    const float dxv = valid ? R.dx[0] : 0.0f;
+    const float dxv = R.dx[0];
     int bs[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int sub = 0; sub < 8; ++sub) {
-        const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(valid ? R.X[0][sub] : 0, O.B[sub], z, 0, 0, 0);
-        const int ls = 2 * (int)((O.sc >> (4 * sub)) & 15u) + 1;
+        const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(R.X[0][sub], O.B[sub], z, 0, 0, 0);
+        const int ls = (int)((O.ls[sub & 1] >> (8 * (sub >> 1))) & 0xFFu);
 #pragma unroll
         for (int i = 0; i < 4; ++i) bs[i] += __mul24(ls, d[i]);
         if (sub == 3)
@@ -502,10 +509,14 @@ __device__ inline void mfma_block_iq3s_ops(const Iq3sBlockOps& O, const XRegs<1>
 }
 
 // Staging of a grouped workgroup's weights: n_reg regions (matrices) of
-// `bytes` contiguous bytes each, loaded as aligned 16-byte chunks by the NT
-// threads (NL loads each; loads past the last chunk repeat it) and stored in
-// LDS at reg * cap + chunk offset; the region's first byte lands at
-// lead[reg] (its address mod 16).  A repeat stores the same bytes to the same
+// `bytes` contiguous bytes each, loaded as aligned 16-byte chunks and stored
+// in LDS at reg * cap + chunk offset; the region's first byte lands at
+// lead[reg] (its address mod 16).  Region m is loaded by threads
+// m NT / n_reg .. (m + 1) NT / n_reg - 1, whole waves, so a wave's region and
+// its base, lead and chunk count are scalars (one region per thread needs no
+// per-lane choice of region).  Each thread makes NL loads, enough when
+// NL * NT >= n_reg * cap / 16 (every region's chunks fit in cap); loads past
+// a region's last chunk repeat it.  A repeat stores the same bytes to the same
 // place, so every store is unconditional (a store under a condition lets the
 // compiler sink its load past the table set-up, a whole memory latency late).
 // With row_bytes (a multiple of 16) and a region that starts 16-aligned, each
@@ -523,31 +534,26 @@ struct GroupStage {
 template <int NT, int NL, int NREG>
 __device__ inline void group_stage_issue(GroupStage<NL>& G, const uint8_t* const (&src)[NREG], int bytes, int cap,
                                          int* leads, int row_bytes = 0) {
+    static_assert(NT % (64 * NREG) == 0, "a region's threads are whole waves");
+    constexpr int TR = NT / NREG;                           // threads per region
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
-    int nch[NREG], rch[NREG];
-    float rrcp[NREG];
-    const uint8_t* base[NREG];
+    const int m = __builtin_amdgcn_readfirstlane((int)threadIdx.x / TR);
+    const uint8_t* s = src[0];
 #pragma unroll
-    for (int m = 0; m < NREG; ++m) {
-        const int lead = (int)(reinterpret_cast<uintptr_t>(src[m]) & 15);
-        base[m] = src[m] - lead;
-        nch[m] = (lead + bytes + 15) >> 4;
-        rch[m] = row_bytes && stage_row_stride(row_bytes, lead) != row_bytes ? row_bytes >> 4 : 0;   // chunks per padded row
-        rrcp[m] = __builtin_amdgcn_rcpf((float)max(rch[m], 1));
-        if (threadIdx.x == 0) leads[m] = lead;
-    }
+    for (int mm = 1; mm < NREG; ++mm)
+        if (m == mm) s = src[mm];
+    const int t = (int)threadIdx.x - m * TR;
+    const int lead = (int)(reinterpret_cast<uintptr_t>(s) & 15);
+    const uint8_t* const base = s - lead;
+    const int nch = (lead + bytes + 15) >> 4;
+    const int rch = row_bytes && stage_row_stride(row_bytes, lead) != row_bytes ? row_bytes >> 4 : 0;   // chunks per padded row
+    const float rrcp = __builtin_amdgcn_rcpf((float)max(rch, 1));
+    if (t == 0) leads[m] = lead;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-        int c = (int)threadIdx.x + NT * i, m = 0;
-#pragma unroll
-        for (int mm = 0; mm + 1 < NREG; ++mm)
-            if (m == mm && c >= nch[mm]) {
-                c -= nch[mm];
-                m = mm + 1;
-            }
-        const int cc = min(c, nch[m] - 1);
-        G.d[i] = *(g_u32x4*)(base[m] + 16 * cc);
-        G.off[i] = m * cap + 16 * cc + (rch[m] ? kRowPad * div_small(cc, rrcp[m]) : 0);
+        const int cc = min(t + TR * i, nch - 1);
+        G.d[i] = *(g_u32x4*)(base + 16 * cc);
+        G.off[i] = m * cap + 16 * cc + (rch ? kRowPad * div_small(cc, rrcp) : 0);
     }
 }
 template <int NL, bool PADDED = false>
@@ -675,11 +681,11 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
         const int pdst = MMID && threadIdx.x < 256 ? a.pair_of[g0 + pt + min((int)(threadIdx.x & 15u), cnt - 1)] : 0;
         if (b < nb) {
             float c[1][4];
-            if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O0, XR, valid, q, c[0]);
+            if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O0, XR, q, c[0]);
             else mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
             *reinterpret_cast<float4*>(&part[m][b][r][part_col(r, 4 * q)]) = make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
             if (both) {
-                if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O1, XR, valid, q, c[0]);
+                if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O1, XR, q, c[0]);
                 else mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
                 *reinterpret_cast<float4*>(&part[1][b][r][part_col(r, 4 * q)]) =
                     make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
