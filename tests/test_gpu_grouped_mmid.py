@@ -225,3 +225,31 @@ def test_grouping_mode_is_validated(hip_rt):
     assert lib.sabah_rt_set_mmid_grouping(3) == -1
     assert lib.sabah_rt_set_mmid_grouping(-1) == -1
     assert lib.sabah_rt_set_mmid_grouping(AUTO) == 0
+
+
+@pytest.mark.parametrize("off", [2, 6])
+@pytest.mark.parametrize("k,rows", [(2048, 64), (768, 128)])
+@pytest.mark.parametrize("qt", [IQ3_S, Q4_K, Q6_K])
+def test_grouped_mul_mat_id_with_a_bank_off_the_16_byte_grid(hip_rt, orc, grouping, qt, k, rows, off):
+    """A bank that starts `off` bytes past a 16-byte boundary: every staged
+    region then has a lead, which both the grouped staging (gate/up form: one
+    lead per matrix region) and the token-major staging carry.  The bank sits
+    inside a larger allocation, so the 16-byte chunks read around its ends stay
+    in bounds."""
+    E, Tn, K = 10, 24, 5
+    raw, ids, x = case(orc, 100 + k + qt + off, E, rows, k, Tn, K, 1, qt)
+    rb = raw.shape[-1]
+    buf = torch.zeros(raw.nbytes + 64, dtype=torch.uint8, device=DEV)
+    buf[16 + off:16 + off + raw.nbytes] = T(raw.reshape(-1))
+    bank = buf[16 + off:]
+    assert bank.data_ptr() % 16 == off
+    xd, idd = T(x), T(ids)
+    grouping(ALWAYS)
+    got = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=True, qt=qt)
+    grouping(NEVER)
+    tok = run(hip_rt, bank, rb, rows, k, E, xd, idd, grouped=False, qt=qt)
+    want = orc.mul_mat_id(raw, x, ids, rows, k, qt)
+    assert_parity(got, want, "grouped qt=%d k=%d rows=%d off=%d" % (qt, k, rows, off))
+    if qt == IQ3_S:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
