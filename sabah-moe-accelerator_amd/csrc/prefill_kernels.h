@@ -508,6 +508,40 @@ __device__ inline void mfma_block_iq3s_ops(const Iq3sBlockOps& O, const XRegs<1>
     for (int i = 0; i < 4; ++i) c[i] = __fmul_rn(__fmul_rn(dw, __shfl(dxv, 4 * q + i)), (float)bs[i]);
 }
 
+// The same for the wave's block of both matrices (gate and up) against one
+// pair tile: the two matrices' MFMAs for a sub-block issue back to back on the
+// shared activation operand, so each result has the other MFMA to cover its
+// latency before its multiply-adds; the pairs' d_x are shuffled once for both.
+// Each matrix's integer sums and fp32 steps are mfma_block_iq3s_ops'.
+__device__ inline void mfma_block_iq3s_ops2(const Iq3sBlockOps& O0, const Iq3sBlockOps& O1, const XRegs<1>& R, int q,
+                                            float (&c0)[4], float (&c1)[4]) {
+    const v4i32 z = {0, 0, 0, 0};
+    const float dxv = R.dx[0];
+    int bs0[4] = {0, 0, 0, 0}, bs1[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int sub = 0; sub < 8; ++sub) {
+        const v4i32 d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(R.X[0][sub], O0.B[sub], z, 0, 0, 0);
+        const v4i32 d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(R.X[0][sub], O1.B[sub], z, 0, 0, 0);
+        const int ls0 = (int)((O0.ls[sub & 1] >> (8 * (sub >> 1))) & 0xFFu);
+        const int ls1 = (int)((O1.ls[sub & 1] >> (8 * (sub >> 1))) & 0xFFu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            bs0[i] += __mul24(ls0, d0[i]);
+            bs1[i] += __mul24(ls1, d1[i]);
+        }
+        if (sub == 3)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(bs0[i]), "+v"(bs1[i]));
+    }
+    const float dw0 = h2f(O0.d), dw1 = h2f(O1.d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float dxi = __shfl(dxv, 4 * q + i);
+        c0[i] = __fmul_rn(__fmul_rn(dw0, dxi), (float)bs0[i]);
+        c1[i] = __fmul_rn(__fmul_rn(dw1, dxi), (float)bs1[i]);
+    }
+}
+
 // Staging of a grouped workgroup's weights: n_reg regions (matrices) of
 // `bytes` contiguous bytes each, loaded as aligned 16-byte chunks and stored
 // in LDS at reg * cap + chunk offset; the region's first byte lands at
@@ -681,14 +715,21 @@ __global__ __launch_bounds__(kGuThreads, 4) void k_grouped_gate_up(GroupedGateUp
         const int pdst = MMID && threadIdx.x < 256 ? a.pair_of[g0 + pt + min((int)(threadIdx.x & 15u), cnt - 1)] : 0;
         if (b < nb) {
             float c[1][4];
-            if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O0, XR, q, c[0]);
-            else mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
-            *reinterpret_cast<float4*>(&part[m][b][r][part_col(r, 4 * q)]) = make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
-            if (both) {
-                if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O1, XR, q, c[0]);
-                else mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
-                *reinterpret_cast<float4*>(&part[1][b][r][part_col(r, 4 * q)]) =
-                    make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
+            if (QT == QT_IQ3_S && both) {
+                float c1[4];
+                mfma_block_iq3s_ops2(O0, O1, XR, q, c[0], c1);
+                *reinterpret_cast<float4*>(&part[0][b][r][part_col(r, 4 * q)]) = make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
+                *reinterpret_cast<float4*>(&part[1][b][r][part_col(r, 4 * q)]) = make_float4(c1[0], c1[1], c1[2], c1[3]);
+            } else {
+                if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O0, XR, q, c[0]);
+                else mfma_blocks<QT, 1, true, false>(rowp, tabs, b, b + 1, XR, valid, q, c);
+                *reinterpret_cast<float4*>(&part[m][b][r][part_col(r, 4 * q)]) = make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
+                if (both) {
+                    if constexpr (QT == QT_IQ3_S) mfma_block_iq3s_ops(O1, XR, q, c[0]);
+                    else mfma_blocks<QT, 1, true, false>(rowp1, tabs, b, b + 1, XR, valid, q, c);
+                    *reinterpret_cast<float4*>(&part[1][b][r][part_col(r, 4 * q)]) =
+                        make_float4(c[0][0], c[0][1], c[0][2], c[0][3]);
+                }
             }
         }
         __syncthreads();
