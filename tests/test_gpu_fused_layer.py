@@ -279,3 +279,59 @@ def test_layer_fusion_mode_is_validated(hip_rt):
     assert lib.sabah_rt_set_layer_fusion(3) == -1
     assert lib.sabah_rt_set_layer_fusion(-1) == -1
     assert lib.sabah_rt_set_layer_fusion(1) == 0
+
+
+@pytest.mark.parametrize("off", [2, 6])
+def test_layers_with_banks_off_the_16_byte_grid(hip_rt, orc, fusion, off):
+    """Gate, up and down banks that start `off` bytes past a 16-byte boundary
+    (each inside a larger allocation, so the 16-byte chunks staged around
+    their ends stay in bounds): the fused one-token layer and the two-kernel
+    form stage regions with a lead and stay bit-identical to each other and
+    to the oracle; the group-major batch layer stays bit-identical to the
+    token-major batch layer on the same banks, and within tolerance of the
+    oracle (the bar of every batch layer)."""
+    from sabah.runtime import routing, rt
+    rng = np.random.default_rng(70 + off)
+    E, D, F, K = 16, 2048, 768, 8
+    shapes = {"gate": (F, D), "up": (F, D), "down": (D, F)}
+    raws = {r: orc.quantize_weights(IQ3_S, (rng.standard_normal((E,) + s) * 0.02).astype(np.float32))
+            for r, s in shapes.items()}
+    bufs, ptrs = {}, {}
+    for r, raw in raws.items():
+        buf = torch.zeros(raw.nbytes + 64, dtype=torch.uint8, device=DEV)
+        buf[16 + off:16 + off + raw.nbytes] = T(raw.reshape(-1))
+        bufs[r], ptrs[r] = buf, buf.data_ptr() + 16 + off
+        assert ptrs[r] % 16 == off
+    d = rt.MoeLayerDesc()
+    d.gate, d.up, d.down = ptrs["gate"], ptrs["up"], ptrs["down"]
+    d.qt_gate = d.qt_up = d.qt_down = IQ3_S
+    d.d_model, d.d_ff, d.n_experts = D, F, E
+    lib = hip_rt.lib()
+
+    def layer(x, ids, w, prefill=False):
+        out = torch.empty_like(x)
+        fn = lib.sabah_moe_prefill_layer if prefill else lib.sabah_moe_layer
+        hip_rt.check(fn(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(ids.data_ptr()),
+                        ctypes.c_void_p(w.data_ptr()), ids.shape[1], ids.shape[0], ctypes.c_void_p(out.data_ptr()),
+                        None, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "layer")
+        return out
+
+    def want(x, ids, w):
+        return orc.moe_layer(raws["gate"], raws["up"], raws["down"], (IQ3_S,) * 3, x, ids, w)
+
+    ids, w = routing.zipf_routing(rng, 1, E, K)
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    xd, idd, wd = T(x), T(ids), T(w)
+    fused, plain, n = run_both(hip_rt, fusion, lambda: layer(xd, idd, wd).cpu().numpy())
+    assert n == 1
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    ref = want(x, ids, w)
+    assert_parity(fused, ref, "fused layer, banks at +%d" % off)
+    assert np.array_equal(fused.view(np.uint32), ref.view(np.uint32))
+
+    ids, w = routing.zipf_routing(rng, 48, E, K)
+    x = rng.standard_normal((48, D)).astype(np.float32)
+    got = layer(T(x), T(ids), T(w), prefill=True).cpu().numpy()
+    tok = layer(T(x), T(ids), T(w)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
+    assert_parity(got, want(x, ids, w), "group-major layer, banks at +%d" % off)
